@@ -1,0 +1,309 @@
+#!/usr/bin/env python
+"""Flash-Born attention throughput on one MI355X.
+
+Default (what the driver runs): config C3, the headline -- causal bf16 Born
+attention forward, B=16 H=16 T=1024 D=64, Q, K, V ~ N(0, 1/64) (seeded,
+synthetic), scale 8.0, eps 1e-12.  A step is one forward launch over one
+input set; the timed steps rotate over several input sets (> the 256 MB
+Infinity Cache) so every step reads its inputs from HBM.
+
+Prints ONE JSON line (rank 0) with the metric of BASELINE.json: algorithmic
+TFLOP/s (4*D*visible_pairs*B*H per forward) and its fraction of the MI355X
+dense bf16 MFMA peak, plus ``roofline`` (the kernel's HIP-event-timed
+average launch against the HBM roof) and ``cpu_baseline`` (the reference's
+eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
+on this host).
+
+    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+CONFIGS = {
+    # name: (B, H, T, D, std, l2norm_qk, doc_mean, backward)
+    "c2": (32, 4, 1024, 64, 1.0, True, None, False),
+    "c3": (16, 16, 1024, 64, 0.125, False, None, False),
+    "c4": (4, 16, 8192, 64, 1.0, False, 512.0, False),
+    "c5fwd": (16, 16, 2048, 64, 1.0, False, None, False),
+    "c5": (16, 16, 2048, 64, 1.0, False, None, True),
+}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--sets", type=int, default=4, help="input sets rotated over the timed steps")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg)")
+    return ap.parse_args()
+
+
+def make_inputs(cfg, seed, device, dtype):
+    import numpy as np
+    import torch
+
+    from quantumdlblocks_amd import l2_normalize
+
+    B, H, T, D, std, l2, doc_mean, _ = cfg
+    g = torch.Generator("cpu").manual_seed(seed)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g) * std for _ in range(4))
+    if l2:
+        q, k = l2_normalize(q), l2_normalize(k)
+    doc = None
+    if doc_mean is not None:
+        rng = np.random.default_rng(seed)
+        ids = np.empty((B, T), dtype=np.int32)
+        for b in range(B):
+            t = n_doc = 0
+            while t < T:
+                n = int(rng.geometric(1.0 / doc_mean))
+                ids[b, t : t + n] = n_doc
+                t += n
+                n_doc += 1
+        doc = torch.from_numpy(ids).to(device)
+    return [x.to(device, dtype).contiguous() for x in (q, k, v, do)], doc
+
+
+def visible_pairs(cfg, doc):
+    """Visible (b, i, j) pairs summed over the batch, per head (causal)."""
+    B, H, T = cfg[0], cfg[1], cfg[2]
+    if doc is None:
+        return B * T * (T + 1) // 2
+    import numpy as np
+
+    total = 0
+    for row in doc.cpu().numpy():
+        _, counts = np.unique(row, return_counts=True)  # documents are contiguous runs
+        total += int((counts * (counts + 1) // 2).sum())
+    return total
+
+
+def cpu_baseline(cfg, budget_s, seed):
+    """Time the reference's eager CPU path (fp32, full T x T) on a bounded sample."""
+    import torch
+
+    from oracle.born_oracle import eager_fp32_torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    B, H, T, D, std = cfg[:5]
+    g = torch.Generator("cpu").manual_seed(seed)
+    per_run = max(budget_s / 8.0, 0.05)
+
+    def sample(n):
+        q, k, v = (torch.randn(1, n, T, D, generator=g) * std for _ in range(3))
+        return q, k, v
+
+    n = 1
+    q, k, v = sample(n)
+    t0 = time.perf_counter()
+    eager_fp32_torch(q, k, v, torch.tensor(8.0))
+    one = time.perf_counter() - t0
+    n = int(max(1, min(B * H, per_run / max(one, 1e-6))))
+    q, k, v = sample(n)
+    sc = torch.tensor(8.0)
+    for _ in range(3):
+        eager_fp32_torch(q, k, v, sc)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        eager_fp32_torch(q, k, v, sc)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = 4.0 * D * (T * (T + 1) // 2) * n
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{n} of the {B * H} (b,h) heads of the same config, fp32, eager "
+                   f"(flash_born.py:681-690 restated), median of 5 runs after 3 warm-ups, "
+                   f"{med * 1e3:.1f} ms per run"),
+        "cpu_model": cpu_model,
+        "seconds_per_run": med,
+        "speedup_of_gpu": None,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one GPU: this build's flash-Born path runs on a single MI355X "
+            "(the multi-GPU sharding plan is described in DESIGN.md, not built); rerun with --gpus 1",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from quantumdlblocks_amd import _native
+    from quantumdlblocks_amd.kernels.flash_born import _DTYPE_CODE
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    dtype = torch.bfloat16
+    cfg = CONFIGS[args.config]
+    B, H, T, D = cfg[:4]
+    backward = cfg[7]
+    steps, warmup = (20, 5) if args.profile else (args.steps, args.warmup)
+
+    sets = []
+    doc = None
+    for i in range(max(1, args.sets)):
+        (q, k, v, do), doc = make_inputs(cfg, args.seed + i, dev, dtype)
+        out = torch.empty_like(q)
+        z = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        grads = [torch.empty_like(q) for _ in range(3)] if backward else None
+        sets.append((q, k, v, do, out, z, grads))
+    scale = torch.tensor(8.0, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    code = _DTYPE_CODE[dtype]
+    doc_ptr = doc.data_ptr() if doc is not None else None
+    ws = None
+    dscale = torch.empty(1, dtype=torch.float32, device=dev)
+    if backward:
+        nbytes = int(lib.qdl_flash_born_bwd_workspace_size(code, B, H, T, D, 1))
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+
+    def fwd(s):
+        q, k, v, _, out, z, _ = s
+        rc = lib.qdl_flash_born_fwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    out.data_ptr(), z.data_ptr(), scale.data_ptr(), 1, doc_ptr,
+                                    1, 0, 1e-12, stream)
+        _native.check(rc, "qdl_flash_born_fwd")
+
+    def bwd(s):
+        q, k, v, do, out, z, (dq, dk, dv) = s
+        rc = lib.qdl_flash_born_bwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    out.data_ptr(), do.data_ptr(), z.data_ptr(), scale.data_ptr(), 1,
+                                    doc_ptr, 1, 0, 1e-12, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    dscale.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        _native.check(rc, "qdl_flash_born_bwd")
+
+    def step(i):
+        s = sets[i % len(sets)]
+        fwd(s)
+        if backward:
+            bwd(s)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    def timed(n_steps, rotate=True):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for i in range(n_steps):
+            step(i if rotate else 0)
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return wall / n_steps, ev0.elapsed_time(ev1) / 1e3 / n_steps
+
+    wall_step, ev_step = timed(steps, rotate=True)
+    hot_wall, hot_ev = timed(steps, rotate=False)
+    for s in sets:
+        assert torch.isfinite(s[4]).all(), "non-finite output"
+
+    pairs = visible_pairs(cfg, doc)
+    fwd_flops = 4.0 * D * pairs * H
+    flops = fwd_flops * (3.5 if backward else 1.0)
+    el = 2  # bf16 bytes
+    fwd_bytes = B * H * T * D * el * 4 + B * H * T * 4  # read Q, K, V; write O (+ Z fp32)
+    bwd_bytes = B * H * T * D * el * 8 + B * H * T * 4  # read Q,K,V,O,dO (+Z); write dQ,dK,dV
+    nbytes = fwd_bytes + (bwd_bytes if backward else 0)
+
+    value = flops / wall_step / 1e12
+    achieved_tflops = flops / ev_step / 1e12
+    achieved_gbs = nbytes / ev_step / 1e9
+    ai = flops / nbytes
+    hbm_bound = ai * PEAK_HBM_GBS / 1e3 < PEAK_BF16_TFLOPS
+    if hbm_bound:
+        roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved_gbs / PEAK_HBM_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4)}
+    roof["traffic"] = None
+
+    cpu = None
+    if not (args.no_cpu_baseline or args.profile):
+        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed)
+        cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
+
+    name = "fwd" if not backward else "fwd+bwd"
+    line = {
+        "metric": f"Born-attn {name} TFLOP/s + % of bf16 MFMA peak, B{B} H{H} T{T} hd{D}",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,%g) Q, K, V; %d rotated input sets)" % (cfg[4] ** 2, len(sets)),
+        "config": {
+            "workload": args.config + (" (headline)" if args.config == "c3" else ""),
+            "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
+            "doc_mask": doc is not None, "backward": backward, "scale": 8.0, "eps": 1e-12,
+        },
+        "pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "detail": {
+            "kernel_us_per_step_events": round(ev_step * 1e6, 3),
+            "hot_kernel_us_per_step_events": round(hot_ev * 1e6, 3),
+            "hot_tflops": round(flops / hot_wall / 1e12, 2),
+            "algorithmic_flops": flops,
+            "algorithmic_bytes": nbytes,
+            "arith_intensity": round(ai, 1),
+            "achieved_tflops_events": round(achieved_tflops, 2),
+            "mfma_frac_events": round(achieved_tflops / PEAK_BF16_TFLOPS, 4),
+            "visible_pairs_per_head": pairs,
+            "device": torch.cuda.get_device_name(dev),
+            "torch": torch.__version__,
+            "host": platform.node(),
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

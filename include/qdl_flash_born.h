@@ -1,0 +1,106 @@
+/*
+ * qdl_flash_born.h -- C ABI of the MI355X (gfx950) flash-Born attention library
+ * (libqdl_flash_born.so).
+ *
+ * Born attention, per (b, h):
+ *   a_ij = max(0, scale_h * q_i . k_j) * M_ij,  p_ij = a_ij^2,
+ *   Z_i  = sum_j p_ij + eps,                    O_i  = sum_j p_ij v_j / Z_i,
+ *   M_ij = [causal => j <= i] & [window > 0 => i - j < window] & [doc_i == doc_j].
+ *
+ * Conventions shared by every entry point:
+ *   - q, k, v, out, dout, dq, dk, dv: contiguous (B, H, T, D) arrays of the
+ *     element type `dtype`, base addresses 16-byte aligned.
+ *   - z, delta: contiguous (B, H, T) fp32.
+ *   - scale: `n_scale` fp32 values in device memory, n_scale == 1 (shared) or
+ *     n_scale == H (per head, indexed by h).
+ *   - doc_ids: contiguous (B, T) int32 in device memory, or NULL.
+ *   - D must be a multiple of 8 in [8, 256].  (The Python host zero-pads other
+ *     head dims up to the next multiple of 8; padding is exact.)
+ *   - Every call is asynchronous on `stream` (a hipStream_t; NULL is the null
+ *     stream), allocates nothing and keeps no state between calls.  The caller
+ *     owns all buffers, including the workspace.
+ *   - Return value: 0 on success; a negative QDL_BORN_E_* code for invalid
+ *     arguments (nothing was launched); a positive hipError_t value when a
+ *     launch failed.  qdl_flash_born_strerror() describes any code.
+ */
+#ifndef QDL_FLASH_BORN_H
+#define QDL_FLASH_BORN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the compute dtype of the reference's autograd Function). */
+#define QDL_BORN_DTYPE_F32 0
+#define QDL_BORN_DTYPE_F16 1
+#define QDL_BORN_DTYPE_BF16 2
+
+/* Error codes (negative: rejected before any launch). */
+#define QDL_BORN_OK 0
+#define QDL_BORN_E_DTYPE (-1)
+#define QDL_BORN_E_SHAPE (-2)
+#define QDL_BORN_E_HEADDIM (-3)
+#define QDL_BORN_E_ALIGN (-4)
+#define QDL_BORN_E_NULL (-5)
+#define QDL_BORN_E_SCALE (-6)
+#define QDL_BORN_E_WINDOW (-7)
+#define QDL_BORN_E_WORKSPACE (-8)
+
+typedef struct ihipStream_t *qdl_stream_t; /* == hipStream_t */
+
+/* Library version string, e.g. "qdl_flash_born 0.1.0 gfx950". */
+const char *qdl_flash_born_version(void);
+
+/* Human-readable text for a return code of any entry point. */
+const char *qdl_flash_born_strerror(int code);
+
+/* 1 if (dtype, head_dim) is served by the kernels without host padding. */
+int qdl_flash_born_supported(int dtype, int64_t head_dim);
+
+/*
+ * Forward pass.  Writes out (B, H, T, D) and z (B, H, T) = sum_j p_ij + eps.
+ *
+ * Replaces the launch of `_flash_born_fwd_kernel[grid](...)` in
+ * `_FlashBornAttentionFn.forward` (Vengo/QuantumDLBlocks
+ * src/qdlblocks/kernels/flash_born.py:475-513); arguments carry the same
+ * meaning as that launch's (pointers, B/H/T/D, PER_HEAD_SCALE via n_scale,
+ * IS_CAUSAL, WINDOW_SIZE, HAS_DOC_IDS via doc_ids != NULL, EPS).
+ */
+int qdl_flash_born_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                       const void *q, const void *k, const void *v, void *out,
+                       float *z, const float *scale, int64_t n_scale,
+                       const int32_t *doc_ids, int is_causal,
+                       int64_t window_size, double eps, qdl_stream_t stream);
+
+/* Bytes of device workspace qdl_flash_born_bwd needs for this problem. */
+int64_t qdl_flash_born_bwd_workspace_size(int dtype, int64_t B, int64_t H,
+                                          int64_t T, int64_t D,
+                                          int64_t n_scale);
+
+/*
+ * Backward pass.  Given the forward's out and z and the upstream gradient
+ * dout, writes dq, dk, dv (B, H, T, D) and dscale (n_scale fp32 values:
+ * per-head sums, or the total when n_scale == 1).  The dscale reduction is
+ * deterministic (fixed-order, no atomics).
+ *
+ * Replaces the two launches `_flash_born_bwd_kernel[grid_n](...)` and
+ * `_flash_born_bwd_dq_kernel[grid_m](...)` in `_FlashBornAttentionFn.backward`
+ * (flash_born.py:554-612) together with the zero-initialised dscale buffer
+ * they accumulate into (flash_born.py:536).
+ */
+int qdl_flash_born_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
+                       const void *q, const void *k, const void *v,
+                       const void *out, const void *dout, const float *z,
+                       const float *scale, int64_t n_scale,
+                       const int32_t *doc_ids, int is_causal,
+                       int64_t window_size, double eps, void *dq, void *dk,
+                       void *dv, float *dscale, void *workspace,
+                       int64_t workspace_bytes, qdl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QDL_FLASH_BORN_H */

@@ -1,0 +1,234 @@
+"""CPU oracle for flash-Born attention.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or the timed CPU baseline).  The product path in
+``quantumdlblocks_amd`` never imports it.
+
+It restates, from scratch, the semantics of the reference's Born attention
+(``src/qdlblocks/kernels/flash_born.py`` in Vengo/QuantumDLBlocks):
+
+    r_ij = q_i . k_j
+    a_ij = max(0, scale_h * r_ij) * M_ij          (flash_born.py:166-180, 684-686)
+    M_ij = [causal => j <= i] & [W > 0 => i - j < W] & [doc_i == doc_j]
+                                                  (flash_born.py:169-177, 635-652)
+    p_ij = a_ij ** 2
+    Z_i  = sum_j p_ij + eps                       (flash_born.py:182, 185, 192)
+    O_i  = sum_j p_ij v_j / Z_i                   (flash_born.py:183-186, 689-690)
+
+and the backward pass of ``_flash_born_bwd_kernel`` /
+``_flash_born_bwd_dq_kernel`` (flash_born.py:270-322, 387-427):
+
+    delta_i = dO_i . O_i
+    dP_ij   = (dO_i . v_j - delta_i) / Z_i
+    dS_ij   = 2 a_ij dP_ij
+    dq_i    = scale_h sum_j dS_ij k_j
+    dk_j    = scale_h sum_i dS_ij q_i
+    dv_j    = sum_i (p_ij / Z_i) dO_i
+    dscale  = sum_{b,i,j} dS_ij r_ij   (per head when the scale is per head)
+
+Everything is float64 numpy except ``eager_fp32_torch``, which restates the
+reference's eager CPU path (flash_born.py:681-690) op for op in fp32 torch and
+is what ``bench.py`` times as the CPU baseline.
+
+How each function is pinned (tests/test_oracle.py):
+  * ``compute_document_ids``: the literal golden tensor of the reference test
+    tests/test_hypothesis_016_speedrun_systems_and_arch.py:163-177.
+  * ``forward``: brute-force scalar loops in C (oracle/born_oracle.c, written
+    independently of this file) on small shapes; hand-computed closed forms
+    (T=1, T=2 with D=1); invariants (constant V, scale invariance, window=1,
+    window >= T, all-equal / all-distinct doc ids, permutation equivariance,
+    all-negative overlaps give O = 0, row weights sum to (Z-eps)/Z).
+  * ``backward``: torch.autograd of an independent float64 torch statement of
+    the forward, float64 finite differences (torch.autograd.gradcheck), the
+    C brute force, and the closed form dscale = (2/s) sum delta eps / Z.
+  * ``eager_fp32_torch``: against ``forward`` at fp32 tolerance.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "compute_document_ids",
+    "visible_mask",
+    "forward",
+    "backward",
+    "born_weights",
+    "eager_fp32_torch",
+    "visible_pairs",
+    "geometric_doc_ids",
+]
+
+
+def compute_document_ids(idx, eot_token_id: int = 50256) -> np.ndarray:
+    """Per-token document ids; an EOT token belongs to the document it ends.
+
+    Restates ``compute_document_ids`` (src/qdlblocks/layers/attention.py:308-315):
+    ``cumsum(idx == eot) - (idx == eot)`` as int32.
+    """
+    idx = np.asarray(idx)
+    is_eot = (idx == int(eot_token_id)).astype(np.int32)
+    return (np.cumsum(is_eot, axis=-1, dtype=np.int32) - is_eot).astype(np.int32)
+
+
+def visible_mask(T: int, is_causal: bool, window_size: int, doc_ids=None) -> np.ndarray:
+    """Boolean visibility mask, shape (1 or B, 1, T, T).
+
+    Restates ``_apply_window_and_doc_mask`` (flash_born.py:635-652): causal
+    ``i - j >= 0``; window ``i - j < W`` when W > 0 (applied with or without
+    causality); document equality when ``doc_ids`` (B, T) is given.
+    """
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    diff = i - j
+    m = (diff >= 0) if is_causal else np.ones((T, T), dtype=bool)
+    if window_size > 0:
+        m = m & (diff < int(window_size))
+    m = m[None, None]
+    if doc_ids is not None:
+        d = np.asarray(doc_ids)
+        m = m & (d[:, None, :, None] == d[:, None, None, :])
+    return m
+
+
+def _scale_bh(scale, H: int) -> np.ndarray:
+    """Scale broadcast to (1, H|1, 1, 1): scalar, or exactly H per-head values.
+
+    Mirrors flash_born.py:452-453 (``numel() > 1`` means per head, indexed by
+    h) and 681-683 (a 1-D scale is viewed as (1, H, 1, 1)).
+    """
+    s = np.asarray(scale, dtype=np.float64).reshape(-1)
+    if s.size == 1:
+        return s.reshape(1, 1, 1, 1)
+    if s.size != H:
+        raise ValueError(f"per-head scale needs exactly H={H} values, got {s.size}")
+    return s.reshape(1, H, 1, 1)
+
+
+def _f64(x) -> np.ndarray:
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().double().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+def born_weights(q, k, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+    """Normalised Born weights p_ij / Z_i, float64, shape (B, H, T, T)."""
+    q, k = _f64(q), _f64(k)
+    T = q.shape[-2]
+    r = q @ np.swapaxes(k, -1, -2)
+    a = np.maximum(_scale_bh(scale, q.shape[1]) * r, 0.0)
+    a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
+    p = a * a
+    return p / (p.sum(-1, keepdims=True) + eps)
+
+
+def forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+    """Born attention forward in float64.  Returns (O, Z), O (B,H,T,D), Z (B,H,T)."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    B, H, T, D = q.shape
+    r = q @ np.swapaxes(k, -1, -2)
+    a = np.maximum(_scale_bh(scale, H) * r, 0.0)
+    a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
+    p = a * a
+    Z = p.sum(-1) + eps
+    O = (p @ v) / Z[..., None]
+    return O, Z
+
+
+def backward(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+    """Closed-form gradients in float64.
+
+    Returns (dq, dk, dv, dscale) with dscale shaped like the flattened scale
+    (1 value, or H values for a per-head scale).
+    """
+    q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    B, H, T, D = q.shape
+    s_bh = _scale_bh(scale, H)
+    r = q @ np.swapaxes(k, -1, -2)
+    a = np.maximum(s_bh * r, 0.0)
+    a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
+    p = a * a
+    Z = p.sum(-1) + eps
+    O = (p @ v) / Z[..., None]
+    delta = (do * O).sum(-1)
+    dP = (do @ np.swapaxes(v, -1, -2) - delta[..., None]) / Z[..., None]
+    dS = 2.0 * a * dP
+    dq = s_bh * (dS @ k)
+    dk = s_bh * (np.swapaxes(dS, -1, -2) @ q)
+    dv = np.swapaxes(p / Z[..., None], -1, -2) @ do
+    per_head = np.asarray(scale).size > 1
+    dsr = (dS * r).sum(axis=(0, 2, 3))  # per head
+    dscale = dsr if per_head else np.array([dsr.sum()])
+    return dq, dk, dv, dscale
+
+
+def visible_pairs(B: int, T: int, is_causal: bool = True, window_size: int = 0, doc_ids=None) -> int:
+    """Number of visible (b, i, j) pairs summed over the batch, for one head.
+
+    Used for the algorithmic FLOP count: fwd = 4 * D * H * pairs.
+    """
+    if doc_ids is None:
+        if window_size <= 0:
+            per_row = T * (T + 1) // 2 if is_causal else T * T
+        else:
+            i = np.arange(T, dtype=np.int64)
+            if is_causal:
+                per_row = int(np.minimum(i + 1, window_size).sum())
+            else:  # keys j > i - W, i.e. j in [max(0, i-W+1), T)
+                per_row = int((T - np.maximum(0, i - window_size + 1)).sum())
+        return B * per_row
+    total = 0
+    d = np.asarray(doc_ids)
+    for b in range(d.shape[0]):
+        m = visible_mask(T, is_causal, window_size, d[b : b + 1])
+        total += int(m.sum())
+    return total
+
+
+def geometric_doc_ids(B: int, T: int, mean_len: float, seed: int) -> np.ndarray:
+    """Document ids for the long-context config: per row, document lengths are
+    drawn from a geometric distribution with the given mean (support >= 1) from
+    ``np.random.default_rng(seed)``, the last document truncated at T."""
+    rng = np.random.default_rng(seed)
+    out = np.empty((B, T), dtype=np.int32)
+    for b in range(B):
+        t = 0
+        doc = 0
+        while t < T:
+            n = int(rng.geometric(1.0 / mean_len))
+            out[b, t : t + n] = doc
+            t += n
+            doc += 1
+    return out
+
+
+def eager_fp32_torch(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+    """The reference's eager path (flash_born.py:681-690) restated op for op.
+
+    ``matmul(q, k^T) * scale -> relu -> square -> mask multiply ->
+    prob / (sum prob + eps) -> matmul(., v)``, computed in ``v.dtype`` on the
+    tensors' device.  Full T x T matmuls, no causal skipping.
+    """
+    import torch
+
+    if not isinstance(scale, torch.Tensor):
+        scale = torch.tensor(float(scale), dtype=torch.float32, device=q.device)
+    s_v = scale.to(v.dtype)
+    if s_v.ndim == 1:
+        s_v = s_v.view(1, -1, 1, 1)
+    scaled = torch.matmul(q.to(v.dtype), k.to(v.dtype).transpose(-1, -2)) * s_v
+    prob = torch.relu(scaled).square()
+    if is_causal or window_size > 0 or doc_ids is not None:
+        T = prob.shape[-1]
+        idx = torch.arange(T, device=prob.device)
+        diff = idx[:, None] - idx[None, :]
+        mask = (diff >= 0) if is_causal else torch.ones((T, T), device=prob.device, dtype=torch.bool)
+        if window_size > 0:
+            mask = mask & (diff < int(window_size))
+        mask = mask.view(1, 1, T, T)
+        if doc_ids is not None:
+            mask = mask & (doc_ids[:, None, :, None] == doc_ids[:, None, None, :])
+        prob = prob * mask.to(prob.dtype)
+    w = prob / (torch.sum(prob, dim=-1, keepdim=True) + eps)
+    return torch.matmul(w.to(v.dtype), v)

@@ -1,0 +1,153 @@
+// Shared device helpers for the gfx950 flash-Born kernels.
+//
+// Layout conventions (all tensors contiguous):
+//   q, k, v, o, do, dq, dk, dv : (B, H, T, D), element type E
+//   z, delta                   : (B, H, T) fp32
+//   doc_ids                    : (B, T) int32
+//
+// MFMA lane layouts used throughout (wave64, lane l, c = l % 32, g = l / 32):
+//   v_mfma_f32_32x32x16_{bf16,f16}
+//     A (32x16): lane holds A[c][8g .. 8g+7]       (8 x 16-bit = 4 dwords)
+//     B (16x32): lane holds B[8g .. 8g+7][c]
+//     C (32x32): lane holds C[row(r)][c], r = 0..15,
+//                row(r) = 8*(r/4) + 4*g + (r%4)
+//   v_mfma_f32_32x32x2_f32
+//     A (32x2):  lane holds A[c][g]; B (2x32): lane holds B[g][c]; C as above.
+// Only A/B consistency matters for a contraction, so the kernels permute the
+// contraction index freely; the C layout is what the score -> probability ->
+// next-operand handoff relies on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qdl {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// Row of a 32x32 MFMA accumulator register r for lane half g.
+__device__ __forceinline__ constexpr int acc_row(int r, int g) {
+    return 8 * (r >> 2) + 4 * g + (r & 3);
+}
+
+// Packed 16-bit ReLU: bf16 and fp16 are sign-magnitude, so a signed 16-bit
+// integer max against zero clears every negative value (including -0).
+__device__ __forceinline__ uint32_t relu_pk16(uint32_t u) {
+    i16x2 x = __builtin_bit_cast(i16x2, u);
+    i16x2 zero = {0, 0};
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(x, zero));
+}
+
+struct BF16 {
+    static constexpr int kDtype = 2;
+    __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    // Round-to-nearest-even fp32 pair -> packed 16-bit pair (v_cvt_pk_bf16_f32).
+    __device__ __forceinline__ static uint32_t pack(float x, float y) {
+        bf16x2 h = {(__bf16)x, (__bf16)y};
+        return __builtin_bit_cast(uint32_t, h);
+    }
+    // acc + u.lo + u.hi in fp32 (v_dot2c_f32_bf16 against (1, 1)).
+    __device__ __forceinline__ static float sum2(uint32_t u, float acc) {
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u), one, acc, false);
+    }
+    __device__ __forceinline__ static float lo(uint32_t u) { return __uint_as_float(u << 16); }
+    __device__ __forceinline__ static float hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+};
+
+struct F16 {
+    static constexpr int kDtype = 1;
+    __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    __device__ __forceinline__ static uint32_t pack(float x, float y) {
+        f16x2 h = {(_Float16)x, (_Float16)y};
+        return __builtin_bit_cast(uint32_t, h);
+    }
+    __device__ __forceinline__ static float sum2(uint32_t u, float acc) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u), one, acc, false);
+    }
+    __device__ __forceinline__ static float lo(uint32_t u) {
+        return (float)__builtin_bit_cast(f16x2, u)[0];
+    }
+    __device__ __forceinline__ static float hi(uint32_t u) {
+        return (float)__builtin_bit_cast(f16x2, u)[1];
+    }
+};
+
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    f32x16 z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    return z;
+}
+
+// Kernel argument block shared by the forward kernels.
+struct FwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* z;
+    const float* scale;
+    const int32_t* doc;  // (B, T) or nullptr
+    int per_head_scale;
+    int B, H, T, D;
+    int is_causal;
+    int window;
+    float eps;
+};
+
+// Kernel argument block shared by the backward kernels.
+struct BwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    const float* z;
+    const float* scale;
+    const int32_t* doc;
+    void* dq;
+    void* dk;
+    void* dv;
+    float* delta;          // (B, H, T) workspace
+    float* dscale_part;    // per-workgroup dscale partials (workspace)
+    float* dscale;         // n_scale outputs
+    int per_head_scale;
+    int B, H, T, D;
+    int is_causal;
+    int window;
+    float eps;
+};
+
+// Mask modes compiled into the kernels.
+enum MaskMode : int {
+    kDense = 0,    // non-causal, no window, no documents
+    kCausal = 1,   // causal only
+    kGeneral = 2,  // runtime causal flag + window + document ids
+};
+
+}  // namespace qdl

@@ -1,0 +1,550 @@
+// Flash-Born forward kernels for gfx950.
+//
+// Replaces the reference's `_flash_born_fwd_kernel`
+// (src/qdlblocks/kernels/flash_born.py:81-192).  One workgroup owns BM = NW*QW
+// query rows of one (b, h); each wave owns QW = 32*NQB of them.  K/V tiles of
+// BN keys are staged through LDS (double buffered, one barrier per tile) and
+// consumed by every wave of the workgroup.
+//
+// Per tile and wave (16-bit inputs):
+//   S^T = K * Q^T        v_mfma_f32_32x32x16, A = K from LDS, B = Q^T held in
+//                        registers for the whole kernel
+//   p'  = relu(r * |r|)  fp32 -> packed 16-bit, relu on the packed value; the
+//                        scale is folded out: relu(s r)^2 = s^2 relu(sign(s) r)^2,
+//                        sign(s) is applied to Q once, s^2 at the end
+//   z  += p'_lo + p'_hi  v_dot2c_f32 against (1, 1): z sums exactly the
+//                        rounded weights the PV product uses
+//   O^T += V^T * P^T     A = V^T from LDS (V is transposed while staging),
+//                        B = P^T straight from the S^T accumulator registers:
+//                        the 32x32 C layout gives each lane one query and 8
+//                        keys per 16-key chunk, which is the B layout up to a
+//                        permutation of keys that the V^T read applies too.
+// At the end each lane owns one query: z is completed with one cross-half
+// shuffle, O = O^T / (z + eps / s^2), Z = s^2 z + eps.
+#pragma once
+
+#include "born_common.h"
+
+namespace qdl {
+
+// ---------------------------------------------------------------------------
+// 16-bit (bf16 / fp16) forward.
+// ---------------------------------------------------------------------------
+template <class E, int DP, int NQB, int NW, int BN, int MODE, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void born_fwd16_kernel(FwdArgs p) {
+    static_assert(DP % 32 == 0 && DP <= 256, "padded head dim");
+    static_assert(BN % 32 == 0, "key tile");
+    constexpr int QW = 32 * NQB;
+    constexpr int BM = NW * QW;
+    constexpr int KS = DP / 16;
+    constexpr int DB = DP / 32;
+    constexpr int NB = BN / 32;
+    constexpr int NT = NW * 64;
+    constexpr int KSTR = DP + 8;   // K row stride in LDS (elements)
+    constexpr int VSTR = BN + 4;   // V^T row stride in LDS (elements)
+    constexpr int KCH = BN * DP / 8;          // 16-byte K chunks per tile
+    constexpr int KPT = (KCH + NT - 1) / NT;
+    constexpr int VCH = (BN / 2) * (DP / 8);  // (2 keys x 8 dims) V chunks per tile
+    constexpr int VPT = (VCH + NT - 1) / NT;
+    constexpr bool kDoc = (MODE == kGeneral);
+
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BN * KSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][DP * VSTR];
+    __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
+
+    const int T = p.T, D = p.D;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const bool causal = (MODE == kCausal) || (MODE == kGeneral && p.is_causal);
+    const int window = (MODE == kGeneral) ? p.window : 0;
+    const bool has_doc = kDoc && p.doc != nullptr;
+
+    // Heaviest query blocks first under causality; consecutive blocks share
+    // nothing, blocks BH apart share (b, h) and, with BH a multiple of 8, land
+    // on the same XCD.
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    const int mb = causal ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int b = bh / p.H, h = bh % p.H;
+    const int m0 = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, g = lane >> 5;
+    const int q0 = m0 + wave * QW;
+
+    const size_t base = (size_t)bh * T * D;
+    const uint16_t* __restrict__ Q = reinterpret_cast<const uint16_t*>(p.q) + base;
+    const uint16_t* __restrict__ K = reinterpret_cast<const uint16_t*>(p.k) + base;
+    const uint16_t* __restrict__ V = reinterpret_cast<const uint16_t*>(p.v) + base;
+    const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
+
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+
+    // Q^T operand, resident for the whole kernel.
+    u32x4 qr[NQB][KS];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const int row = q0 + qb * 32 + c;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + g * 8;
+            u32x4 x = {0u, 0u, 0u, 0u};
+            if (row < T && d < D) x = ldg16(Q + (size_t)row * D + d);
+            x ^= flip;
+            qr[qb][ks] = x;
+        }
+    }
+    int qdoc[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const int row = q0 + qb * 32 + c;
+        qdoc[qb] = (has_doc && row < T) ? docb[row] : -1;
+    }
+
+    // Key range of this workgroup (flash_born.py:152-154).
+    int kv_lo = 0;
+    int kv_hi = causal ? min(T, m0 + BM) : T;
+    if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
+    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+
+    u32x4 kreg[KPT];
+    u32x4 vreg[VPT][2];
+    int dreg = -2;
+
+    auto load_tile = [&](int key0) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int idx = tid + i * NT;
+            if (KCH % NT == 0 || idx < KCH) {
+                const int row = idx / (DP / 8);
+                const int col = (idx % (DP / 8)) * 8;
+                const int key = key0 + row;
+                u32x4 x = {0u, 0u, 0u, 0u};
+                if (key < T && col < D) x = ldg16(K + (size_t)key * D + col);
+                kreg[i] = x;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = tid + i * NT;
+            if (VCH % NT == 0 || idx < VCH) {
+                const int col = (idx % (DP / 8)) * 8;
+                const int key = key0 + 2 * (idx / (DP / 8));
+                u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
+                if (col < D) {
+                    if (key < T) x0 = ldg16(V + (size_t)key * D + col);
+                    if (key + 1 < T) x1 = ldg16(V + (size_t)(key + 1) * D + col);
+                }
+                vreg[i][0] = x0;
+                vreg[i][1] = x1;
+            }
+        }
+        if (kDoc && has_doc && tid < BN) {
+            const int key = key0 + tid;
+            dreg = key < T ? docb[key] : -2;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int idx = tid + i * NT;
+            if (KCH % NT == 0 || idx < KCH) {
+                const int row = idx / (DP / 8);
+                const int col = (idx % (DP / 8)) * 8;
+                *reinterpret_cast<u32x4*>(&k_lds[buf][row * KSTR + col]) = kreg[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = tid + i * NT;
+            if (VCH % NT == 0 || idx < VCH) {
+                const int col = (idx % (DP / 8)) * 8;
+                const int kp = idx / (DP / 8);
+                const u32x4 a = vreg[i][0], bb = vreg[i][1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t even = (a[j] & 0xffffu) | (bb[j] << 16);
+                    const uint32_t odd = (a[j] >> 16) | (bb[j] & 0xffff0000u);
+                    *reinterpret_cast<uint32_t*>(&v_lds[buf][(col + 2 * j) * VSTR + 2 * kp]) = even;
+                    *reinterpret_cast<uint32_t*>(&v_lds[buf][(col + 2 * j + 1) * VSTR + 2 * kp]) = odd;
+                }
+            }
+        }
+        if (kDoc && has_doc && tid < BN) doc_lds[buf][tid] = dreg;
+    };
+
+    f32x16 oacc[DB][NQB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
+    float zacc[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) zacc[qb] = 0.f;
+
+    if (ntiles > 0) {
+        load_tile(kv_lo);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int key0 = kv_lo + t * BN;
+        const int buf = t & 1;
+        const bool more = (t + 1) < ntiles;
+        if (more) load_tile(key0 + BN);
+
+        // Which of this wave's (query, key) pairs can be visible in the tile.
+        bool active = q0 < T;
+        bool need_mask = has_doc;
+        if (causal) {
+            active = active && (key0 <= q0 + QW - 1);
+            need_mask = need_mask || (key0 + BN - 1 > q0);
+        }
+        if (window > 0) {
+            active = active && (key0 + BN - 1 > q0 - window);
+            need_mask = need_mask || (key0 <= q0 + QW - 1 - window);
+        }
+
+        if (active) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                f32x16 s[NQB];
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(
+                        &k_lds[buf][(nb * 32 + c) * KSTR + ks * 16 + g * 8]);
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(a, qr[qb][ks], s[qb]);
+                }
+                if (need_mask) {
+                    const int kbase = key0 + nb * 32 + 4 * g;
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) {
+                        const int qi = q0 + qb * 32 + c;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = kbase + 8 * (r >> 2) + (r & 3);
+                            bool vis = true;
+                            if (causal) vis = vis && (key <= qi);
+                            if (window > 0) vis = vis && (qi - key < window);
+                            if (kDoc && has_doc)
+                                vis = vis && (doc_lds[buf][key - key0] == qdoc[qb]);
+                            if (!vis) s[qb][r] = 0.f;
+                        }
+                    }
+                }
+                uint32_t pk[NQB][8];
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                        uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
+                        u = relu_pk16(u);
+                        zacc[qb] = E::sum2(u, zacc[qb]);
+                        pk[qb][j] = u;
+                    }
+                }
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) {
+                        const uint16_t* vrow =
+                            &v_lds[buf][(db * 32 + c) * VSTR + nb * 32 + hh * 16 + g * 4];
+                        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+                        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+                        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+                        for (int qb = 0; qb < NQB; ++qb) {
+                            const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1],
+                                              pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
+                            oacc[db][qb] = E::mfma(a, bq, oacc[db][qb]);
+                        }
+                    }
+                }
+            }
+        }
+
+        if (more) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: one query per lane.
+    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    float* __restrict__ Zp = p.z + (size_t)bh * T;
+    const float s2 = sc * sc;
+    const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const float zt = zacc[qb] + __shfl_xor(zacc[qb], 32);
+        const float rcp = 1.0f / (zt + eps_s);
+        const int qi = q0 + qb * 32 + c;
+        if (qi < T) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int d = db * 32 + 8 * j + 4 * g;
+                    if (d < D) {
+                        const f32x16& o = oacc[db][qb];
+                        u32x2 w;
+                        w[0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
+                        w[1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
+                        *reinterpret_cast<u32x2*>(O + (size_t)qi * D + d) = w;
+                    }
+                }
+            }
+            if (g == 0) Zp[qi] = s2 * zt + p.eps;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 forward: v_mfma_f32_32x32x2_f32, no reduced-precision operands
+// (the reference runs its fp32 dots with allow_tf32=False).
+// ---------------------------------------------------------------------------
+template <int DP, int NW, int BN, int MODE, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void born_fwd32_kernel(FwdArgs p) {
+    static_assert(DP % 32 == 0 && DP <= 256, "padded head dim");
+    constexpr int QW = 32;
+    constexpr int BM = NW * QW;
+    constexpr int KQ = DP / 8;     // float4 pairs of contraction steps
+    constexpr int DB = DP / 32;
+    constexpr int NB = BN / 32;
+    constexpr int NT = NW * 64;
+    constexpr int KSTR = DP + 4;   // floats
+    constexpr int VSTR = DP + 4;
+    constexpr int CH = BN * DP / 4;    // 16-byte chunks per tile
+    constexpr int CPT = (CH + NT - 1) / NT;
+    constexpr bool kDoc = (MODE == kGeneral);
+
+    __shared__ __attribute__((aligned(16))) float k_lds[2][BN * KSTR];
+    __shared__ __attribute__((aligned(16))) float v_lds[2][BN * VSTR];
+    __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
+
+    const int T = p.T, D = p.D;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const bool causal = (MODE == kCausal) || (MODE == kGeneral && p.is_causal);
+    const int window = (MODE == kGeneral) ? p.window : 0;
+    const bool has_doc = kDoc && p.doc != nullptr;
+
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    const int mb = causal ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int b = bh / p.H, h = bh % p.H;
+    const int m0 = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, g = lane >> 5;
+    const int q0 = m0 + wave * QW;
+
+    const size_t base = (size_t)bh * T * D;
+    const float* __restrict__ Q = reinterpret_cast<const float*>(p.q) + base;
+    const float* __restrict__ K = reinterpret_cast<const float*>(p.k) + base;
+    const float* __restrict__ V = reinterpret_cast<const float*>(p.v) + base;
+    const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
+
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const float sgn = (sc < 0.f) ? -1.f : 1.f;
+
+    // Contraction step t of the QK product uses dim 8*(t/4) + 4*g + (t%4), so
+    // each lane reads 4 consecutive dims at once.
+    f32x4 qr[KQ];
+    {
+        const int row = q0 + c;
+#pragma unroll
+        for (int u = 0; u < KQ; ++u) {
+            const int d = 8 * u + 4 * g;
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if (row < T && d < D) x = *reinterpret_cast<const f32x4*>(Q + (size_t)row * D + d);
+            qr[u] = x * sgn;
+        }
+    }
+    const int qi = q0 + c;
+    const int qdoc = (has_doc && qi < T) ? docb[qi] : -1;
+
+    int kv_lo = 0;
+    int kv_hi = causal ? min(T, m0 + BM) : T;
+    if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
+    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+
+    f32x4 kreg[CPT], vreg[CPT];
+    int dreg = -2;
+    auto load_tile = [&](int key0) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int idx = tid + i * NT;
+            if (CH % NT == 0 || idx < CH) {
+                const int row = idx / (DP / 4);
+                const int col = (idx % (DP / 4)) * 4;
+                const int key = key0 + row;
+                f32x4 xk = {0.f, 0.f, 0.f, 0.f}, xv = {0.f, 0.f, 0.f, 0.f};
+                if (key < T && col < D) {
+                    xk = *reinterpret_cast<const f32x4*>(K + (size_t)key * D + col);
+                    xv = *reinterpret_cast<const f32x4*>(V + (size_t)key * D + col);
+                }
+                kreg[i] = xk;
+                vreg[i] = xv;
+            }
+        }
+        if (kDoc && has_doc && tid < BN) {
+            const int key = key0 + tid;
+            dreg = key < T ? docb[key] : -2;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int idx = tid + i * NT;
+            if (CH % NT == 0 || idx < CH) {
+                const int row = idx / (DP / 4);
+                const int col = (idx % (DP / 4)) * 4;
+                *reinterpret_cast<f32x4*>(&k_lds[buf][row * KSTR + col]) = kreg[i];
+                *reinterpret_cast<f32x4*>(&v_lds[buf][row * VSTR + col]) = vreg[i];
+            }
+        }
+        if (kDoc && has_doc && tid < BN) doc_lds[buf][tid] = dreg;
+    };
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float zacc = 0.f;
+
+    if (ntiles > 0) {
+        load_tile(kv_lo);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int key0 = kv_lo + t * BN;
+        const int buf = t & 1;
+        const bool more = (t + 1) < ntiles;
+        if (more) load_tile(key0 + BN);
+
+        bool active = q0 < T;
+        bool need_mask = has_doc;
+        if (causal) {
+            active = active && (key0 <= q0 + QW - 1);
+            need_mask = need_mask || (key0 + BN - 1 > q0);
+        }
+        if (window > 0) {
+            active = active && (key0 + BN - 1 > q0 - window);
+            need_mask = need_mask || (key0 <= q0 + QW - 1 - window);
+        }
+        if (active) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                f32x16 s = zero16();
+#pragma unroll
+                for (int u = 0; u < KQ; ++u) {
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(
+                        &k_lds[buf][(nb * 32 + c) * KSTR + 8 * u + 4 * g]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s = mfma_f32(a[e], qr[u][e], s);
+                }
+                if (need_mask) {
+                    const int kbase = key0 + nb * 32 + 4 * g;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kbase + 8 * (r >> 2) + (r & 3);
+                        bool vis = true;
+                        if (causal) vis = vis && (key <= qi);
+                        if (window > 0) vis = vis && (qi - key < window);
+                        if (kDoc && has_doc) vis = vis && (doc_lds[buf][key - key0] == qdoc);
+                        if (!vis) s[r] = 0.f;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float x = fmaxf(s[r], 0.f);
+                    const float pr = x * x;
+                    zacc += pr;
+                    s[r] = pr;
+                }
+                // O^T += V^T P^T: step r contracts key acc_row(r, g) of this block.
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int krow = nb * 32 + acc_row(r, g);
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+                        oacc[db] = mfma_f32(v_lds[buf][krow * VSTR + db * 32 + c], s[r], oacc[db]);
+                }
+            }
+        }
+        if (more) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    float* __restrict__ O = reinterpret_cast<float*>(p.o) + base;
+    float* __restrict__ Zp = p.z + (size_t)bh * T;
+    const float s2 = sc * sc;
+    const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+    const float zt = zacc + __shfl_xor(zacc, 32);
+    const float rcp = 1.0f / (zt + eps_s);
+    if (qi < T) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = db * 32 + 8 * j + 4 * g;
+                if (d < D) {
+                    f32x4 w = {oacc[db][4 * j] * rcp, oacc[db][4 * j + 1] * rcp,
+                               oacc[db][4 * j + 2] * rcp, oacc[db][4 * j + 3] * rcp};
+                    *reinterpret_cast<f32x4*>(O + (size_t)qi * D + d) = w;
+                }
+            }
+        }
+        if (g == 0) Zp[qi] = s2 * zt + p.eps;
+    }
+}
+
+// Tile configuration per padded head dim (16-bit inputs).
+template <int DP>
+struct Fwd16Cfg {
+    static constexpr int NQB = DP <= 64 ? 2 : 1;
+    static constexpr int NW = 4;
+    static constexpr int BN = DP <= 128 ? 64 : 32;
+    static constexpr int WPE = DP <= 128 ? 2 : 1;
+    static constexpr int BM = NW * 32 * NQB;
+};
+
+template <int DP>
+struct Fwd32Cfg {
+    static constexpr int NW = 4;
+    static constexpr int BN = 32;
+    static constexpr int WPE = DP <= 128 ? 2 : 1;
+    static constexpr int BM = NW * 32;
+};
+
+template <class E, int DP, int MODE>
+hipError_t launch_fwd16(const FwdArgs& a, hipStream_t st) {
+    using C = Fwd16Cfg<DP>;
+    const int nmb = (a.T + C::BM - 1) / C::BM;
+    const dim3 grid((unsigned)nmb * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_kernel<E, DP, C::NQB, C::NW, C::BN, MODE, C::WPE>), grid,
+                       dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int DP, int MODE>
+hipError_t launch_fwd32(const FwdArgs& a, hipStream_t st) {
+    using C = Fwd32Cfg<DP>;
+    const int nmb = (a.T + C::BM - 1) / C::BM;
+    const dim3 grid((unsigned)nmb * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd32_kernel<DP, C::NW, C::BN, MODE, C::WPE>), grid, dim3(C::NW * 64),
+                       0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace qdl

@@ -1,0 +1,31 @@
+"""Host-side helpers on the flash-Born path's inputs.
+
+``compute_document_ids`` builds the ``doc_ids`` argument from token ids
+(reference src/qdlblocks/layers/attention.py:308-315); ``l2_normalize`` is the
+per-head-vector normalisation the Born layer applies to Q and K before the
+kernel (reference src/qdlblocks/functional.py:59-84).
+"""
+
+from __future__ import annotations
+
+import torch
+
+__all__ = ["compute_document_ids", "l2_normalize"]
+
+
+def compute_document_ids(idx: torch.Tensor, eot_token_id: int = 50256) -> torch.Tensor:
+    """Document id per token, (B, T) int32.
+
+    Ids count the end-of-text tokens strictly before each position, so an
+    end-of-text token closes (belongs to) the document it terminates.
+    """
+    eot = (idx == int(eot_token_id)).to(torch.int32)
+    before = torch.cumsum(eot, dim=-1, dtype=torch.int32) - eot
+    return before.to(torch.int32)
+
+
+def l2_normalize(x: torch.Tensor, dim: int = -1, eps: float = 1e-12) -> torch.Tensor:
+    """x / sqrt(sum x^2 + eps) along ``dim``, computed in fp32, returned in x.dtype."""
+    xf = x.float()
+    inv = torch.rsqrt(xf.square().sum(dim=dim, keepdim=True) + eps)
+    return (xf * inv).to(x.dtype)

@@ -1,0 +1,22 @@
+"""GPU kernels of quantumdlblocks_amd (mirrors ``qdlblocks.kernels`` for the
+flash-Born path; reference src/qdlblocks/kernels/__init__.py:3-10)."""
+
+from .flash_born import (
+    HAS_HIP_KERNELS,
+    HAS_TRITON,
+    IS_HIP,
+    flash_born_attention,
+    get_flash_born_launch_meta,
+    get_mi355x_launch_meta,
+    get_rdna4_autotune_configs,
+)
+
+__all__ = [
+    "HAS_HIP_KERNELS",
+    "HAS_TRITON",
+    "IS_HIP",
+    "flash_born_attention",
+    "get_flash_born_launch_meta",
+    "get_mi355x_launch_meta",
+    "get_rdna4_autotune_configs",
+]

@@ -1,0 +1,223 @@
+"""GPU parity of the flash-Born forward (HIP kernels via the C ABI) against the
+float64 CPU oracle on the same (dtype-rounded) inputs.
+
+Tolerances (normwise relative error max|out-ref|/max|ref|): 1e-5 for fp32,
+2e-2 for bf16 / fp16, as stated for this path; max-abs error is printed.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import born_oracle as orc
+from util import TOL, f64, max_abs, rel_err, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, scale, **kw):
+    from quantumdlblocks_amd import flash_born_attention
+
+    out = flash_born_attention(q, k, v, scale, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, window_size=0,
+               doc=None, std=1.0, seed=0, heads=None, tol=None):
+    q, k, v = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, dtype=dtype))
+    doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
+    scale_arg = scale
+    if isinstance(scale, np.ndarray):
+        scale_arg = torch.as_tensor(scale, dtype=torch.float32, device=dev)
+    out = _run(q, k, v, scale_arg, is_causal=is_causal, eps=eps, window_size=window_size, doc_ids=doc_t)
+    assert out.shape == (B, H, T, D) and out.dtype == dtype
+    if heads is None:
+        ref, _ = orc.forward(f64(q), f64(k), f64(v), np.asarray(scale, dtype=np.float64), is_causal, eps,
+                             window_size, doc)
+        got = f64(out)
+    else:  # check a subset of (b, h) rows of a large problem
+        got_l, ref_l = [], []
+        sc = np.asarray(scale, dtype=np.float64).reshape(-1)
+        for b, h in heads:
+            s_h = sc[h] if sc.size > 1 else sc[0]
+            r, _ = orc.forward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
+                               f64(v[b : b + 1, h : h + 1]), s_h, is_causal, eps, window_size,
+                               None if doc is None else doc[b : b + 1])
+            ref_l.append(r)
+            got_l.append(f64(out[b : b + 1, h : h + 1]))
+        ref, got = np.concatenate(ref_l), np.concatenate(got_l)
+    err = rel_err(got, ref)
+    print(f"fwd B{B} H{H} T{T} D{D} {dtype} causal={is_causal} W={window_size} doc={doc is not None} "
+          f"rel={err:.3e} maxabs={max_abs(got, ref):.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= (tol or TOL[dtype]), err
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_c1_shape(cuda_device, dtype, is_causal):
+    """Config C1's shape (B1 H4 T256 D64) on the GPU, every dtype."""
+    _check_fwd(1, 4, 256, 64, dtype, cuda_device, is_causal=is_causal)
+
+
+@pytest.mark.parametrize("T", [1, 2, 7, 31, 64, 65, 100, 257])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fwd_ragged_lengths(cuda_device, T, dtype):
+    _check_fwd(2, 3, T, 64, dtype, cuda_device, seed=T)
+
+
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 80, 96, 112, 128, 160, 192, 256, 20, 3])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fwd_head_dims(cuda_device, D, dtype):
+    """Every head dim up to 256; D not a multiple of 8 is zero-padded by the host."""
+    _check_fwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("window", [1, 5, 64, 100, 1000])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_sliding_window(cuda_device, dtype, window, is_causal):
+    _check_fwd(2, 2, 200, 64, dtype, cuda_device, is_causal=is_causal, window_size=window, seed=window)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_document_mask(cuda_device, dtype, is_causal):
+    doc = orc.geometric_doc_ids(3, 300, 40.0, seed=1)
+    _check_fwd(3, 2, 300, 64, dtype, cuda_device, is_causal=is_causal, doc=doc)
+
+
+def test_fwd_document_and_window(cuda_device):
+    doc = orc.geometric_doc_ids(2, 333, 60.0, seed=2)
+    _check_fwd(2, 4, 333, 64, torch.bfloat16, cuda_device, window_size=37, doc=doc)
+    _check_fwd(2, 4, 333, 64, torch.float32, cuda_device, window_size=37, doc=doc)
+
+
+def test_fwd_reference_doc_literal(cuda_device):
+    """The reference's own window + document case (test_hypothesis_016:179-206):
+    B2 H4 T8 D16, window 4, scale 10, doc ids from the literal EOT example."""
+    from quantumdlblocks_amd import compute_document_ids, l2_normalize
+
+    idx = torch.tensor([[10, 20, 50256, 30, 40, 50256, 50, 60], [11, 50256, 22, 33, 44, 55, 66, 77]])
+    doc = compute_document_ids(idx)
+    torch.manual_seed(2)
+    q = l2_normalize(torch.randn(2, 4, 8, 16), dim=-1)
+    k = l2_normalize(0.85 * q + 0.15 * torch.randn(2, 4, 8, 16), dim=-1)
+    v = l2_normalize(torch.randn(2, 4, 8, 16), dim=-1)
+    out = _run(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), 10.0, window_size=4,
+               doc_ids=doc.to(cuda_device))
+    ref, _ = orc.forward(f64(q), f64(k), f64(v), 10.0, True, 1e-12, 4, doc.numpy())
+    assert rel_err(f64(out), ref) <= 1e-5
+    assert max_abs(f64(out), ref) <= 1e-3  # the reference's own GPU-vs-CPU bound
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fwd_per_head_and_signed_scales(cuda_device, dtype):
+    H = 4
+    for scale in (np.array([2.5, 3.2, 0.5, 7.0]), np.array([-1.5, 2.0, -8.0, 1.0]), np.array([0.0, 1.0, 0.0, 3.0])):
+        _check_fwd(2, H, 130, 64, dtype, cuda_device, scale=scale.astype(np.float32))
+    for s in (-8.0, 0.0, 1e-3, 100.0):
+        _check_fwd(2, H, 70, 64, dtype, cuda_device, scale=s)
+
+
+def test_fwd_scale_shapes(cuda_device):
+    """scale as float, 0-d, (1,), (H,), (1,H,1,1) tensors (flash_born.py:452-453, 681-683)."""
+    B, H, T, D = 2, 3, 50, 32
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=5))
+    sc = torch.tensor([1.5, 4.0, 9.0], device=cuda_device)
+    outs = [
+        _run(q, k, v, sc),
+        _run(q, k, v, sc.view(1, H, 1, 1)),
+    ]
+    ref, _ = orc.forward(f64(q), f64(k), f64(v), sc.cpu().numpy(), True, 1e-12)
+    for o in outs:
+        assert rel_err(f64(o), ref) <= 1e-5
+    for s in (3.0, torch.tensor(3.0, device=cuda_device), torch.tensor([3.0], device=cuda_device)):
+        o = _run(q, k, v, s)
+        ref, _ = orc.forward(f64(q), f64(k), f64(v), 3.0, True, 1e-12)
+        assert rel_err(f64(o), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("eps", [0.0, 1e-12, 1e-6, 1.0])
+def test_fwd_eps(cuda_device, eps):
+    _check_fwd(1, 2, 64, 64, torch.float32, cuda_device, eps=eps, std=0.2)
+    _check_fwd(1, 2, 64, 64, torch.bfloat16, cuda_device, eps=eps, std=0.2)
+
+
+def test_fwd_all_negative_overlaps_give_zero(cuda_device):
+    """Keys anti-aligned with every query: every weight is relu(<0)^2 = 0, so O = 0."""
+    B, H, T, D = 1, 2, 96, 64
+    (base,) = seeded_inputs((1, 1, 1, D), seed=9, n=1)
+    q = base.expand(B, H, T, D).abs().contiguous()
+    k = -q.clone()
+    (v,) = seeded_inputs((B, H, T, D), seed=10, n=1)
+    for dtype in (torch.bfloat16, torch.float32):
+        out = _run(q.to(cuda_device, dtype), k.to(cuda_device, dtype), v.to(cuda_device, dtype), 8.0)
+        assert torch.count_nonzero(out).item() == 0
+
+
+def test_fwd_empty_and_non_contiguous(cuda_device):
+    for shape in ((0, 2, 16, 64), (1, 0, 16, 64), (1, 2, 0, 64)):
+        q = torch.zeros(shape, device=cuda_device, dtype=torch.bfloat16)
+        assert _run(q, q, q, 8.0).shape == shape
+    # (B, T, H, D) storage viewed as (B, H, T, D): the host makes it contiguous.
+    x = torch.randn(2, 40, 3, 64, device=cuda_device).transpose(1, 2)
+    out = _run(x, x, x, 8.0)
+    ref, _ = orc.forward(f64(x), f64(x), f64(x), 8.0)
+    assert rel_err(f64(out), ref) <= 1e-5
+    # a storage offset that breaks 16-byte alignment
+    y = torch.randn(1 * 2 * 33 * 64 + 3, device=cuda_device)[3:].view(1, 2, 33, 64)
+    out = _run(y, y, y, 8.0)
+    ref, _ = orc.forward(f64(y), f64(y), f64(y), 8.0)
+    assert rel_err(f64(out), ref) <= 1e-5
+
+
+def test_fwd_autocast(cuda_device):
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((1, 2, 64, 64), seed=3))
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = _run(q, k, v, 8.0)
+    assert out.dtype == torch.bfloat16
+    ref, _ = orc.forward(f64(q.bfloat16()), f64(k.bfloat16()), f64(v.bfloat16()), 8.0)
+    assert rel_err(f64(out), ref) <= 2e-2
+
+
+# ---- BASELINE.json configs at full size (subsets of heads vs the oracle) ----
+
+def test_fwd_config_c2(cuda_device):
+    """C2: bf16 B32 H4 T1024 D64, Q and K L2-normalised per head vector."""
+    from quantumdlblocks_amd import l2_normalize
+
+    B, H, T, D = 32, 4, 1024, 64
+    q, k, v = seeded_inputs((B, H, T, D), seed=0)
+    q, k = l2_normalize(q), l2_normalize(k)
+    q, k, v = (x.to(cuda_device, torch.bfloat16) for x in (q, k, v))
+    out = _run(q, k, v, 8.0)
+    heads = [(0, 0), (7, 1), (31, 3), (16, 2)]
+    got = np.concatenate([f64(out[b : b + 1, h : h + 1]) for b, h in heads])
+    ref = np.concatenate([orc.forward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
+                                      f64(v[b : b + 1, h : h + 1]), 8.0)[0] for b, h in heads])
+    assert rel_err(got, ref) <= 2e-2
+    assert torch.isfinite(out).all()
+
+
+def test_fwd_config_c3(cuda_device):
+    """C3 (headline): bf16 B16 H16 T1024 D64, Q, K, V ~ N(0, 1/64)."""
+    _check_fwd(16, 16, 1024, 64, torch.bfloat16, cuda_device, std=0.125,
+               heads=[(0, 0), (15, 15), (3, 9), (8, 4), (11, 0)])
+
+
+def test_fwd_config_c4(cuda_device):
+    """C4: bf16 B4 H16 T8192 D64, causal within geometric(mean 512) documents."""
+    doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
+    _check_fwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=[(0, 0), (3, 15), (1, 7)])
+
+
+def test_fwd_config_c5_forward(cuda_device):
+    """C5's forward: bf16 B16 H16 T2048 D64, N(0,1)."""
+    _check_fwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=[(0, 0), (15, 15), (9, 3)])
