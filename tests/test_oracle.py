@@ -1,0 +1,396 @@
+"""Pins the CPU oracle (oracle/born_oracle.py) before anything is checked against it.
+
+Each check is independent of the formula it tests: a literal golden tensor
+from the reference's own tests, a brute-force C restatement, hand-computed
+closed forms, invariants of the mathematics, torch.autograd / finite
+differences for the backward, and planted mistakes that the pins must catch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import born_oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLIB = os.path.join(ROOT, "oracle", "_build", "libborn_oracle.so")
+
+
+# --------------------------------------------------------------------------
+# brute-force C restatement (oracle/born_oracle.c)
+# --------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def clib():
+    if not os.path.exists(CLIB):
+        import subprocess
+
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    return ctypes.CDLL(CLIB)
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+
+
+def _c_doc(doc):
+    return None if doc is None else np.ascontiguousarray(doc, dtype=np.int32)
+
+
+def c_forward(lib, q, k, v, scale, causal, eps, window, doc):
+    q, k, v = (np.ascontiguousarray(x, np.float64) for x in (q, k, v))
+    B, H, T, D = q.shape
+    out = np.zeros_like(q)
+    z = np.zeros((B, H, T))
+    sc = np.ascontiguousarray(np.asarray(scale, np.float64).reshape(-1))
+    d = _c_doc(doc)
+    lib.born_oracle_fwd(_I(B), _I(H), _I(T), _I(D), q.ctypes.data_as(_P), k.ctypes.data_as(_P),
+                        v.ctypes.data_as(_P), sc.ctypes.data_as(_P), _I(sc.size),
+                        None if d is None else d.ctypes.data_as(_P), ctypes.c_int(int(causal)),
+                        _I(window), ctypes.c_double(eps), out.ctypes.data_as(_P), z.ctypes.data_as(_P))
+    return out, z
+
+
+def c_backward(lib, q, k, v, scale, do, causal, eps, window, doc):
+    q, k, v, do = (np.ascontiguousarray(x, np.float64) for x in (q, k, v, do))
+    B, H, T, D = q.shape
+    dq, dk, dv = (np.zeros_like(q) for _ in range(3))
+    sc = np.ascontiguousarray(np.asarray(scale, np.float64).reshape(-1))
+    ds = np.zeros(sc.size)
+    d = _c_doc(doc)
+    lib.born_oracle_bwd(_I(B), _I(H), _I(T), _I(D), q.ctypes.data_as(_P), k.ctypes.data_as(_P),
+                        v.ctypes.data_as(_P), sc.ctypes.data_as(_P), _I(sc.size),
+                        None if d is None else d.ctypes.data_as(_P), ctypes.c_int(int(causal)),
+                        _I(window), ctypes.c_double(eps), do.ctypes.data_as(_P), dq.ctypes.data_as(_P),
+                        dk.ctypes.data_as(_P), dv.ctypes.data_as(_P), ds.ctypes.data_as(_P))
+    return dq, dk, dv, ds
+
+
+def _rand(shape, seed, n=3):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal(shape) for _ in range(n)]
+
+
+CASES = [
+    # (B, H, T, D, scale, causal, window, doc_mean, eps)
+    (2, 3, 17, 8, 1.5, True, 0, None, 1e-12),
+    (1, 2, 33, 16, [2.5, -3.0], True, 0, None, 1e-6),
+    (2, 2, 29, 4, 0.7, False, 0, None, 1e-12),
+    (2, 1, 40, 8, 1.0, True, 5, None, 1e-12),
+    (1, 2, 40, 8, [1.0, 0.0], False, 7, None, 1e-3),
+    (3, 2, 41, 8, 2.0, True, 0, 6.0, 1e-12),
+    (2, 2, 37, 8, 1.0, False, 0, 4.0, 1e-12),
+    (2, 2, 50, 8, 1.3, True, 9, 8.0, 1e-9),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_forward_matches_brute_force(clib, case):
+    B, H, T, D, scale, causal, window, doc_mean, eps = case
+    q, k, v = _rand((B, H, T, D), seed=T)
+    doc = None if doc_mean is None else orc.geometric_doc_ids(B, T, doc_mean, seed=B)
+    o_c, z_c = c_forward(clib, q, k, v, scale, causal, eps, window, doc)
+    o_n, z_n = orc.forward(q, k, v, np.asarray(scale), causal, eps, window, doc)
+    np.testing.assert_allclose(o_n, o_c, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(z_n, z_c, rtol=1e-12, atol=1e-15)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_backward_matches_brute_force(clib, case):
+    B, H, T, D, scale, causal, window, doc_mean, eps = case
+    q, k, v, do = _rand((B, H, T, D), seed=T + 1, n=4)
+    doc = None if doc_mean is None else orc.geometric_doc_ids(B, T, doc_mean, seed=B)
+    got = orc.backward(q, k, v, np.asarray(scale), do, causal, eps, window, doc)
+    want = c_backward(clib, q, k, v, scale, do, causal, eps, window, doc)
+    for g, w in zip(got, want):
+        np.testing.assert_allclose(g, w, rtol=1e-9, atol=1e-9 * max(1.0, np.abs(w).max()))
+
+
+# --------------------------------------------------------------------------
+# literal golden of the reference's own test
+# --------------------------------------------------------------------------
+
+def test_compute_document_ids_literal_golden():
+    """tests/test_hypothesis_016_speedrun_systems_and_arch.py:163-177 of the reference."""
+    idx = np.array([[10, 20, 50256, 30, 40, 50256, 50, 60], [11, 50256, 22, 33, 44, 55, 66, 77]])
+    expected = np.array([[0, 0, 0, 1, 1, 1, 2, 2], [0, 0, 1, 1, 1, 1, 1, 1]], dtype=np.int32)
+    got = orc.compute_document_ids(idx, eot_token_id=50256)
+    assert got.dtype == np.int32
+    np.testing.assert_array_equal(got, expected)
+
+
+# --------------------------------------------------------------------------
+# hand-computed closed forms
+# --------------------------------------------------------------------------
+
+def test_single_token():
+    """T=1: O_0 = v_0 * p/(p+eps) with p = relu(s q.k)^2, so v_0 if q.k > 0 else 0."""
+    q = np.array([[[[1.0, 2.0]]]])
+    k = np.array([[[[0.5, 0.25]]]])  # q.k = 1
+    v = np.array([[[[3.0, -4.0]]]])
+    o, z = orc.forward(q, k, v, 2.0, eps=0.0)
+    np.testing.assert_allclose(o, v)
+    np.testing.assert_allclose(z, [[[4.0]]])
+    o, z = orc.forward(q, -k, v, 2.0, eps=0.0)  # overlap -2 -> relu 0
+    assert np.all(np.nan_to_num(o) == 0)
+
+
+def test_two_tokens_by_hand():
+    """D=1, T=2, causal, scale 1: r = q_i k_j.
+    q = (1, 2), k = (3, -1), v = (10, 20), eps = 1:
+    row 0: r00 = 3 -> p = 9; Z = 10; O = 90/10 = 9
+    row 1: r10 = 6 -> 36, r11 = -2 -> 0; Z = 37; O = 360/37."""
+    q = np.array([1.0, 2.0]).reshape(1, 1, 2, 1)
+    k = np.array([3.0, -1.0]).reshape(1, 1, 2, 1)
+    v = np.array([10.0, 20.0]).reshape(1, 1, 2, 1)
+    o, z = orc.forward(q, k, v, 1.0, True, 1.0)
+    np.testing.assert_allclose(o.ravel(), [9.0, 360.0 / 37.0])
+    np.testing.assert_allclose(z.ravel(), [10.0, 37.0])
+    # non-causal: row 0 also sees key 1: r01 = -1 -> 0; unchanged.  Row 1 unchanged.
+    o2, _ = orc.forward(q, k, v, 1.0, False, 1.0)
+    np.testing.assert_allclose(o2.ravel(), [9.0, 360.0 / 37.0])
+    # negative scale flips which overlaps survive: row 1 keeps r11=-2 -> (2)^2 = 4
+    o3, z3 = orc.forward(q, k, v, -1.0, True, 1.0)
+    np.testing.assert_allclose(o3.ravel(), [0.0, 80.0 / 5.0])
+    np.testing.assert_allclose(z3.ravel(), [1.0, 5.0])
+
+
+def test_two_tokens_backward_by_hand():
+    """Same D=1 case, dO = 1 everywhere, eps = 1, scale s = 1, causal.
+    Row 1: p = (36, 0), Z = 37, O = 360/37, delta = O.
+    dP_10 = (v_0 - O)/Z = (10 - 360/37)/37;  dS_10 = 2*6*dP_10
+    dq_1 = s * dS_10 * k_0 = 3 dS_10; dk_0 gets s*dS_10*q_1 = 2 dS_10 from row 1
+    dv_0 gets p/Z = 36/37 from row 1 and 9/10 from row 0.
+    Row 0: dP_00 = (10 - 9)/10 = 0.1; dS_00 = 2*3*0.1 = 0.6; dq_0 = 0.6*3; dk_0 += 0.6*1."""
+    q = np.array([1.0, 2.0]).reshape(1, 1, 2, 1)
+    k = np.array([3.0, -1.0]).reshape(1, 1, 2, 1)
+    v = np.array([10.0, 20.0]).reshape(1, 1, 2, 1)
+    do = np.ones((1, 1, 2, 1))
+    dq, dk, dv, ds = orc.backward(q, k, v, 1.0, do, True, 1.0)
+    dS10 = 12.0 * (10.0 - 360.0 / 37.0) / 37.0
+    np.testing.assert_allclose(dq.ravel(), [1.8, 3.0 * dS10])
+    np.testing.assert_allclose(dk.ravel(), [0.6 + 2.0 * dS10, 0.0])
+    np.testing.assert_allclose(dv.ravel(), [0.9 + 36.0 / 37.0, 0.0])
+    # dscale = sum dS * r = 0.6*3 + dS10*6
+    np.testing.assert_allclose(ds, [1.8 + 6.0 * dS10])
+
+
+# --------------------------------------------------------------------------
+# invariants
+# --------------------------------------------------------------------------
+
+def test_constant_values_give_scaled_constant():
+    B, H, T, D = 2, 2, 30, 8
+    q, k = _rand((B, H, T, D), seed=1, n=2)
+    c = np.linspace(-1, 1, D)
+    v = np.broadcast_to(c, (B, H, T, D)).copy()
+    o, z = orc.forward(q, k, v, 1.7, True, 1e-3)
+    np.testing.assert_allclose(o, c * ((z - 1e-3) / z)[..., None], rtol=1e-12, atol=1e-14)
+
+
+def test_scale_invariance_and_weights():
+    B, H, T, D = 1, 3, 25, 8
+    q, k, v = _rand((B, H, T, D), seed=2)
+    o1, _ = orc.forward(q, k, v, 1.0, True, 0.0)
+    o2, _ = orc.forward(q, k, v, 37.0, True, 0.0)
+    np.testing.assert_allclose(o1, o2, rtol=1e-10, atol=1e-12)
+    w = orc.born_weights(q, k, 2.0, True, 1e-9)
+    _, z = orc.forward(q, k, v, 2.0, True, 1e-9)
+    np.testing.assert_allclose(w.sum(-1), (z - 1e-9) / z, rtol=1e-12)
+    assert np.all(np.triu(w[0, 0], 1) == 0.0)  # causal upper triangle exactly zero
+    assert np.all(w >= 0)
+
+
+def test_window_special_cases():
+    B, H, T, D = 2, 2, 21, 6
+    q, k, v = _rand((B, H, T, D), seed=3)
+    # window 1: only the diagonal survives
+    o, z = orc.forward(q, k, v, 1.0, True, 0.0, window_size=1)
+    r = (q * k).sum(-1)
+    keep = (r > 0)[..., None]
+    np.testing.assert_allclose(np.nan_to_num(o), np.where(keep, v, 0.0), rtol=1e-12, atol=1e-12)
+    # window >= T is plain causal
+    a, _ = orc.forward(q, k, v, 1.0, True, 1e-12, window_size=T)
+    b, _ = orc.forward(q, k, v, 1.0, True, 1e-12)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_document_special_cases():
+    B, H, T, D = 2, 2, 19, 5
+    q, k, v = _rand((B, H, T, D), seed=4)
+    same = np.zeros((B, T), dtype=np.int32)
+    a, _ = orc.forward(q, k, v, 1.0, True, 1e-12, doc_ids=same)
+    b, _ = orc.forward(q, k, v, 1.0, True, 1e-12)
+    np.testing.assert_array_equal(a, b)
+    distinct = np.tile(np.arange(T, dtype=np.int32), (B, 1))
+    a, _ = orc.forward(q, k, v, 1.0, False, 1e-12, doc_ids=distinct)
+    b, _ = orc.forward(q, k, v, 1.0, True, 1e-12, window_size=1)
+    np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-15)
+
+
+def test_permutation_equivariance():
+    B, H, T, D = 3, 4, 16, 8
+    q, k, v = _rand((B, H, T, D), seed=5)
+    sc = np.array([1.0, 2.0, 3.0, 4.0])
+    o, _ = orc.forward(q, k, v, sc, True, 1e-12)
+    pb, ph = np.array([2, 0, 1]), np.array([3, 1, 0, 2])
+    o2, _ = orc.forward(q[pb][:, ph], k[pb][:, ph], v[pb][:, ph], sc[ph], True, 1e-12)
+    np.testing.assert_allclose(o2, o[pb][:, ph], rtol=1e-13)
+
+
+def test_all_negative_overlaps_give_zero():
+    B, H, T, D = 1, 1, 12, 4
+    q = np.abs(_rand((B, H, T, D), seed=6, n=1)[0]) + 0.1
+    k = -np.abs(_rand((B, H, T, D), seed=7, n=1)[0]) - 0.1
+    v = _rand((B, H, T, D), seed=8, n=1)[0]
+    o, z = orc.forward(q, k, v, 3.0, False, 1e-12)
+    assert np.all(o == 0.0) and np.all(z == 1e-12)
+    dq, dk, dv, ds = orc.backward(q, k, v, 3.0, v, False, 1e-12)
+    assert np.all(dq == 0) and np.all(dk == 0) and np.all(dv == 0) and np.all(ds == 0)
+
+
+def test_visible_pairs_counts():
+    T = 37
+    for causal in (True, False):
+        for W in (0, 1, 5, 100):
+            m = orc.visible_mask(T, causal, W)
+            assert orc.visible_pairs(2, T, causal, W) == 2 * int(m.sum())
+    doc = orc.geometric_doc_ids(3, T, 6.0, seed=0)
+    assert orc.visible_pairs(3, T, True, 0, doc) == int(orc.visible_mask(T, True, 0, doc).sum())
+
+
+def test_geometric_doc_ids_properties():
+    d = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
+    assert d.shape == (4, 8192) and d.dtype == np.int32
+    assert np.all(np.diff(d, axis=1) >= 0) and np.all(d[:, 0] == 0)
+    lengths = np.concatenate([np.unique(r, return_counts=True)[1][:-1] for r in d])
+    assert 300 < lengths.mean() < 800  # geometric with mean 512
+
+
+# --------------------------------------------------------------------------
+# backward: autograd of an independent torch statement, finite differences,
+# and the closed form of dscale
+# --------------------------------------------------------------------------
+
+def _torch_forward(q, k, v, scale, causal, eps, window, doc):
+    """Independent float64 torch statement of the forward (differentiable)."""
+    T = q.shape[-2]
+    s = scale.view(1, -1, 1, 1) if scale.dim() == 1 else scale
+    r = torch.einsum("bhid,bhjd->bhij", q, k)
+    a = torch.clamp(s * r, min=0.0)
+    i = torch.arange(T).view(T, 1)
+    j = torch.arange(T).view(1, T)
+    keep = torch.ones(T, T, dtype=torch.bool)
+    if causal:
+        keep &= j <= i
+    if window > 0:
+        keep &= (i - j) < window
+    keep = keep.view(1, 1, T, T)
+    if doc is not None:
+        dd = torch.as_tensor(doc)
+        keep = keep & (dd.view(dd.shape[0], 1, T, 1) == dd.view(dd.shape[0], 1, 1, T))
+    p = torch.where(keep, a * a, torch.zeros_like(a))
+    return torch.einsum("bhij,bhjd->bhid", p, v) / (p.sum(-1, keepdim=True) + eps)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_backward_matches_autograd(case):
+    B, H, T, D, scale, causal, window, doc_mean, eps = case
+    q, k, v, do = _rand((B, H, T, D), seed=T + 2, n=4)
+    doc = None if doc_mean is None else orc.geometric_doc_ids(B, T, doc_mean, seed=B)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    ts = torch.tensor(np.asarray(scale, dtype=np.float64), requires_grad=True)
+    out = _torch_forward(tq, tk, tv, ts, causal, eps, window, doc)
+    (out * torch.tensor(do)).sum().backward()
+    dq, dk, dv, ds = orc.backward(q, k, v, np.asarray(scale), do, causal, eps, window, doc)
+    np.testing.assert_allclose(dq, tq.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(dk, tk.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(dv, tv.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(ds.reshape(ts.grad.shape), ts.grad.numpy(), rtol=1e-6, atol=1e-9)
+
+
+def test_forward_statement_gradcheck():
+    """Finite differences pin the differentiable torch statement used above."""
+    q, k, v = (torch.tensor(x, requires_grad=True) for x in _rand((1, 2, 6, 3), seed=11))
+    s = torch.tensor([1.3, 2.1], dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(
+        lambda a, b, c, d: _torch_forward(a, b, c, d, True, 1e-3, 0, None), (q, k, v, s), eps=1e-6, atol=1e-6
+    )
+
+
+def test_dscale_closed_form():
+    """dscale_h = (2/s_h) sum_{b,i} delta_i eps / Z_i (scale invariance)."""
+    B, H, T, D = 2, 2, 24, 8
+    q, k, v, do = _rand((B, H, T, D), seed=12, n=4)
+    sc = np.array([1.5, -2.5])
+    for eps in (1e-3, 1.0):
+        o, z = orc.forward(q, k, v, sc, True, eps)
+        delta = (do * o).sum(-1)
+        want = (2.0 / sc) * (delta * eps / z).sum(axis=(0, 2))
+        _, _, _, ds = orc.backward(q, k, v, sc, do, True, eps)
+        np.testing.assert_allclose(ds, want, rtol=1e-9)
+
+
+def test_eager_fp32_restatement_matches():
+    B, H, T, D = 2, 3, 40, 16
+    q, k, v = (torch.tensor(x, dtype=torch.float32) for x in _rand((B, H, T, D), seed=13))
+    doc = orc.geometric_doc_ids(B, T, 7.0, seed=1)
+    for kw in ({}, {"is_causal": False}, {"window_size": 6}, {"doc_ids": torch.as_tensor(doc)}):
+        out = orc.eager_fp32_torch(q, k, v, torch.tensor([1.0, 2.0, 3.0]), **kw)
+        kw2 = dict(kw)
+        if "doc_ids" in kw2:
+            kw2["doc_ids"] = doc
+        ref, _ = orc.forward(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                             np.array([1.0, 2.0, 3.0]), **kw2)
+        assert np.abs(out.numpy() - ref).max() / np.abs(ref).max() < 1e-5
+
+
+# --------------------------------------------------------------------------
+# planted mistakes: each must be caught by the pins above
+# --------------------------------------------------------------------------
+
+def _mutant_forward(kind):
+    def f(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+        q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+        B, H, T, D = q.shape
+        s = np.asarray(scale, np.float64).reshape(-1)
+        s = s.reshape(1, -1, 1, 1) if s.size > 1 else s.reshape(1, 1, 1, 1)
+        r = q @ np.swapaxes(k, -1, -2)
+        if kind == "transposed":
+            r = np.swapaxes(r, -1, -2)
+        a = s * r if kind == "no_relu" else np.maximum(s * r, 0.0)
+        m = orc.visible_mask(T, is_causal, window_size, doc_ids)
+        if kind == "mask_flipped":
+            m = orc.visible_mask(T, False, 0, None) & ~m if is_causal else m
+        if kind == "window_off_by_one" and window_size > 0:
+            i = np.arange(T)[:, None]
+            j = np.arange(T)[None, :]
+            m = m | ((i - j) == window_size)[None, None] & ((j <= i) if is_causal else True)
+        a = a * m
+        p = a * a if kind != "no_square" else a
+        Z = p.sum(-1) + (0.0 if kind == "drop_eps" else eps)
+        return (p @ v) / Z[..., None], Z
+
+    return f
+
+
+@pytest.mark.parametrize("kind", ["transposed", "no_relu", "mask_flipped", "window_off_by_one", "no_square", "drop_eps"])
+def test_planted_mistakes_are_caught(clib, kind):
+    f = _mutant_forward(kind)
+    caught = False
+    for case in CASES:
+        B, H, T, D, scale, causal, window, doc_mean, eps = case
+        q, k, v = _rand((B, H, T, D), seed=T)
+        doc = None if doc_mean is None else orc.geometric_doc_ids(B, T, doc_mean, seed=B)
+        with np.errstate(all="ignore"):
+            o_m, z_m = f(q, k, v, np.asarray(scale), causal, eps, window, doc)
+        o_c, z_c = c_forward(clib, q, k, v, scale, causal, eps, window, doc)
+        if not (np.allclose(o_m, o_c, rtol=1e-12, atol=1e-12) and np.allclose(z_m, z_c, rtol=1e-12, atol=1e-15)):
+            caught = True
+            break
+    assert caught, f"planted mistake {kind!r} was not caught by the brute-force pin"
