@@ -1,0 +1,179 @@
+"""GPU parity of the flash-Born backward (dq, dk, dv, dscale) against the
+float64 oracle's closed-form gradients on the same (dtype-rounded) inputs.
+
+Tolerances (normwise relative error): 2e-2 for bf16 / fp16, 1e-5 for fp32.
+dscale is compared against the scale of its terms, (2/|s|) eps sum|delta/Z|,
+because its value is itself a small difference.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import born_oracle as orc
+from util import TOL, f64, max_abs, rel_err, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _grads(q, k, v, do, scale, **kw):
+    from quantumdlblocks_amd import flash_born_attention
+
+    q = q.detach().clone().requires_grad_(True)
+    k = k.detach().clone().requires_grad_(True)
+    v = v.detach().clone().requires_grad_(True)
+    sc = scale.detach().clone().requires_grad_(True) if isinstance(scale, torch.Tensor) else scale
+    out = flash_born_attention(q, k, v, sc, **kw)
+    out.backward(do)
+    torch.cuda.synchronize()
+    ds = sc.grad if isinstance(sc, torch.Tensor) else None
+    return out, q.grad, k.grad, v.grad, ds
+
+
+def _check_bwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, window_size=0, doc=None,
+               std=1.0, seed=0, heads=None, tol=None, check_dscale=False):
+    q, k, v, do = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, n=4, dtype=dtype))
+    doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
+    sc_np = np.asarray(scale, dtype=np.float32)
+    sc_t = torch.as_tensor(sc_np, device=dev)
+    out, dq, dk, dv, ds = _grads(q, k, v, do, sc_t, is_causal=is_causal, eps=eps, window_size=window_size,
+                                 doc_ids=doc_t)
+    for g, x in ((dq, q), (dk, k), (dv, v)):
+        assert g.dtype == x.dtype and g.shape == x.shape
+    assert ds.shape == sc_t.shape and ds.dtype == sc_t.dtype
+    sel = heads or [(b, h) for b in range(B) for h in range(H)]
+    tol = tol or TOL[dtype]
+    errs = {}
+    for name, got_t, idx in (("dq", dq, 0), ("dk", dk, 1), ("dv", dv, 2)):
+        got_l, ref_l = [], []
+        for b, h in sel:
+            s_h = sc_np.reshape(-1)[h] if sc_np.size > 1 else sc_np.reshape(-1)[0]
+            r = orc.backward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
+                             f64(v[b : b + 1, h : h + 1]), s_h, f64(do[b : b + 1, h : h + 1]), is_causal, eps,
+                             window_size, None if doc is None else doc[b : b + 1])[idx]
+            ref_l.append(r)
+            got_l.append(f64(got_t[b : b + 1, h : h + 1]))
+        ref, got = np.concatenate(ref_l), np.concatenate(got_l)
+        assert np.isfinite(got).all(), name
+        errs[name] = (rel_err(got, ref), max_abs(got, ref))
+    print(f"bwd B{B} H{H} T{T} D{D} {dtype} causal={is_causal} W={window_size} doc={doc is not None} "
+          + " ".join(f"{n}:rel={e[0]:.2e}/abs={e[1]:.2e}" for n, e in errs.items()), flush=True)
+    for name, (e, _) in errs.items():
+        assert e <= tol, (name, e)
+    if check_dscale:
+        O, Z = orc.forward(f64(q), f64(k), f64(v), sc_np.astype(np.float64), is_causal, eps, window_size, doc)
+        delta_n = (f64(do) * O).sum(-1) / Z
+        s = sc_np.astype(np.float64).reshape(-1)
+        if s.size > 1:
+            want = 2.0 / s * eps * delta_n.sum(axis=(0, 2))
+            mag = 2.0 / np.abs(s) * eps * np.abs(delta_n).sum(axis=(0, 2))
+        else:
+            want = np.array([2.0 / s[0] * eps * delta_n.sum()])
+            mag = np.array([2.0 / abs(s[0]) * eps * np.abs(delta_n).sum()])
+        got = f64(ds).reshape(-1)
+        print(f"  dscale got={got} want={want} mag={mag}", flush=True)
+        assert np.all(np.abs(got - want) <= tol * mag + 1e-30)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_c1_shape(cuda_device, dtype, is_causal):
+    _check_bwd(1, 4, 256, 64, dtype, cuda_device, is_causal=is_causal)
+
+
+@pytest.mark.parametrize("T", [1, 5, 33, 64, 100, 257])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bwd_ragged_lengths(cuda_device, T, dtype):
+    _check_bwd(2, 3, T, 64, dtype, cuda_device, seed=T)
+
+
+@pytest.mark.parametrize("D", [8, 16, 32, 48, 80, 96, 128, 160, 192, 256, 20])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bwd_head_dims(cuda_device, D, dtype):
+    _check_bwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window", [1, 7, 64, 150])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_sliding_window(cuda_device, dtype, window, is_causal):
+    _check_bwd(2, 2, 200, 64, dtype, cuda_device, is_causal=is_causal, window_size=window, seed=window)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_document_mask(cuda_device, dtype, is_causal):
+    doc = orc.geometric_doc_ids(3, 300, 40.0, seed=1)
+    _check_bwd(3, 2, 300, 64, dtype, cuda_device, is_causal=is_causal, doc=doc)
+    _check_bwd(2, 2, 257, 64, dtype, cuda_device, is_causal=is_causal, doc=doc[:2, :257], window_size=30)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bwd_scales_and_dscale(cuda_device, dtype):
+    for scale in (np.array([2.5, 3.2, -0.5, 7.0]), np.array([1.0, 0.0, -8.0, 2.0])):
+        _check_bwd(2, 4, 130, 64, dtype, cuda_device, scale=scale, eps=1e-3, std=0.3, check_dscale=True)
+    for s in (8.0, -3.0):
+        _check_bwd(2, 4, 70, 64, dtype, cuda_device, scale=s, eps=1.0, std=0.3, check_dscale=True)
+
+
+def test_bwd_reference_jax_parity_case(cuda_device):
+    """The reference's torch-vs-JAX gradient case (test_jax_haliax.py:74-134):
+    B2 H2 T16 D8, causal, eps 1e-6, scale sqrt(8) and per-head [2.5, 3.2]; grads atol 1e-4."""
+    rng = np.random.default_rng(123)
+    q, k, v, do = (rng.standard_normal((2, 2, 16, 8)).astype(np.float32) for _ in range(4))
+    for scale in (math.sqrt(8), np.array([2.5, 3.2], dtype=np.float32)):
+        sc_t = torch.as_tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+        t = [torch.as_tensor(x, device=cuda_device) for x in (q, k, v, do)]
+        out, dq, dk, dv, ds = _grads(*t, sc_t, is_causal=True, eps=1e-6)
+        o_ref, _ = orc.forward(q, k, v, np.asarray(scale, np.float64), True, 1e-6)
+        ref = orc.backward(q, k, v, np.asarray(scale, np.float64), do, True, 1e-6)
+        assert max_abs(f64(out), o_ref) <= 1e-5
+        for got, want in zip((dq, dk, dv), ref[:3]):
+            assert max_abs(f64(got), want) <= 1e-4
+        assert max_abs(f64(ds).reshape(-1), ref[3]) <= 1e-4
+
+
+def test_bwd_mixed_input_dtypes(cuda_device):
+    """Compute dtype is v.dtype; grads come back in each input's own dtype."""
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((1, 2, 64, 32), seed=4, n=4))
+    out, dq, dk, dv, ds = _grads(q, k.bfloat16(), v.bfloat16(), do.bfloat16(), torch.tensor(4.0, device=cuda_device))
+    assert out.dtype == torch.bfloat16
+    assert dq.dtype == torch.float32 and dk.dtype == torch.bfloat16 and dv.dtype == torch.bfloat16
+    ref = orc.backward(f64(q.bfloat16()), f64(k.bfloat16()), f64(v.bfloat16()), 4.0, f64(do.bfloat16()))
+    assert rel_err(f64(dq), ref[0]) <= 2e-2
+
+
+def test_bwd_deterministic(cuda_device):
+    q, k, v, do = (x.to(cuda_device, torch.bfloat16) for x in seeded_inputs((2, 4, 300, 64), seed=8, n=4))
+    sc = torch.tensor([1.0, 2.0, 3.0, 4.0], device=cuda_device)
+    a = _grads(q, k, v, do, sc, eps=1e-3)
+    b = _grads(q, k, v, do, sc, eps=1e-3)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_bwd_empty(cuda_device):
+    from quantumdlblocks_amd import flash_born_attention
+
+    for shape in ((0, 2, 16, 64), (1, 2, 0, 64)):
+        q = torch.zeros(shape, device=cuda_device, dtype=torch.bfloat16, requires_grad=True)
+        sc = torch.tensor(2.0, device=cuda_device, requires_grad=True)
+        out = flash_born_attention(q, q, q, sc)
+        out.sum().backward()
+        torch.cuda.synchronize()
+        assert q.grad.shape == shape and sc.grad.item() == 0.0
+
+
+def test_bwd_config_c5(cuda_device):
+    """C5: bf16 B16 H16 T2048 D64 forward + backward, N(0,1); heads checked vs the oracle."""
+    _check_bwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=[(0, 0), (15, 15), (7, 9)])
+
+
+def test_bwd_config_c4_documents(cuda_device):
+    doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
+    _check_bwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=[(0, 0), (3, 15)])
