@@ -41,7 +41,11 @@ How each function is pinned (tests/test_oracle.py):
     all-negative overlaps give O = 0, row weights sum to (Z-eps)/Z).
   * ``backward``: torch.autograd of an independent float64 torch statement of
     the forward, float64 finite differences (torch.autograd.gradcheck), the
-    C brute force, and the closed form dscale = (2/s) sum delta eps / Z.
+    C brute force, and the closed form dscale = (2/s) sum delta eps / Z; the
+    ``out=`` path (delta from a given forward output) by perturbing ``out``
+    and checking dP moves by -dO . d(out) / Z.
+  * ``backward_magnitudes``: bounds |backward| elementwise, and equals |dv|
+    when dO > 0 (every dv term is then non-negative).
   * ``eager_fp32_torch``: against ``forward`` at fp32 tolerance.
 """
 
@@ -55,6 +59,7 @@ __all__ = [
     "forward",
     "backward",
     "born_weights",
+    "backward_magnitudes",
     "eager_fp32_torch",
     "visible_pairs",
     "geometric_doc_ids",
@@ -136,11 +141,13 @@ def forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=No
     return O, Z
 
 
-def backward(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+def backward(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_ids=None, out=None):
     """Closed-form gradients in float64.
 
     Returns (dq, dk, dv, dscale) with dscale shaped like the flattened scale
-    (1 value, or H values for a per-head scale).
+    (1 value, or H values for a per-head scale).  ``out``: the forward output
+    the backward is handed; as in the reference (flash_born.py:277, 302,
+    387), delta_i = dO_i . out_i is formed from it.  Defaults to the exact O.
     """
     q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
     B, H, T, D = q.shape
@@ -150,7 +157,7 @@ def backward(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_i
     a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
     p = a * a
     Z = p.sum(-1) + eps
-    O = (p @ v) / Z[..., None]
+    O = (p @ v) / Z[..., None] if out is None else _f64(out)
     delta = (do * O).sum(-1)
     dP = (do @ np.swapaxes(v, -1, -2) - delta[..., None]) / Z[..., None]
     dS = 2.0 * a * dP
@@ -161,6 +168,29 @@ def backward(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_i
     dsr = (dS * r).sum(axis=(0, 2, 3))  # per head
     dscale = dsr if per_head else np.array([dsr.sum()])
     return dq, dk, dv, dscale
+
+
+def backward_magnitudes(q, k, v, scale, do, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
+    """Size of the terms each gradient sums, float64, same shapes as
+    (dq, dk, dv): the closed form of ``backward`` with every product taken in
+    absolute value.  Gradients that cancel to ~0 (a row that sees one key, or
+    a window of 1) are compared against a small fraction of this scale."""
+    q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    B, H, T, D = q.shape
+    s_bh = _scale_bh(scale, H)
+    r = q @ np.swapaxes(k, -1, -2)
+    a = np.maximum(s_bh * r, 0.0)
+    a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
+    p = a * a
+    Z = p.sum(-1) + eps
+    O = (p @ v) / Z[..., None]
+    delta = np.abs(do * O).sum(-1)
+    dP = (np.abs(do) @ np.abs(np.swapaxes(v, -1, -2)) + delta[..., None]) / Z[..., None]
+    dS = 2.0 * a * dP
+    dq = np.abs(s_bh) * (dS @ np.abs(k))
+    dk = np.abs(s_bh) * (np.swapaxes(dS, -1, -2) @ np.abs(q))
+    dv = np.swapaxes(p / Z[..., None], -1, -2) @ np.abs(do)
+    return dq, dk, dv
 
 
 def visible_pairs(B: int, T: int, is_causal: bool = True, window_size: int = 0, doc_ids=None) -> int:

@@ -4,21 +4,25 @@
 // `_flash_born_bwd_dq_kernel` (src/qdlblocks/kernels/flash_born.py:195-430).
 //
 // With Z_i = sum_j p_ij + eps, delta_i = dO_i . O_i and s the (per-head) scale:
-//   dP_ij = (dO_i . v_j - delta_i) / Z_i = dO'_i . v_j - delta'_i,
-//           dO' = dO / Z, delta' = delta / Z
+//   dP_ij = (dO_i . v_j - delta_i) / Z_i
 //   dS_ij = 2 a_ij dP_ij,   a_ij = |s| relu(r'_ij),  r' = sign(s) q . k
 //   dq_i  = s sum_j dS_ij k_j = 2 s|s| sum_j relu(r'_ij) dP_ij k_j
 //   dk_j  = s sum_i dS_ij q_i = 2 s|s| sum_i relu(r'_ij) dP_ij q_i
-//   dv_j  = sum_i p_ij / Z_i dO_i = s^2 sum_i relu(r'_ij)^2 dO'_i
-//   dscale = sum dS_ij r_ij = (2/s) sum_ij p_ij dP_ij = (2/s) eps sum_i delta'_i
+//   dv_j  = sum_i p_ij / Z_i dO_i = s^2 sum_i relu(r'_ij)^2 / Z_i dO_i
+//   dscale = sum dS_ij r_ij = (2/s) sum_ij p_ij dP_ij = (2/s) eps sum_i delta_i / Z_i
+// delta is taken from the stored forward output O, as the reference does
+// (flash_born.py:277, 302).  dO . v_j - delta_i cancels strongly in rows with
+// few visible keys, and 2 a dP / Z amplifies it by 1/a there, so it is always
+// formed in fp32 from the unscaled bf16/fp16 dO (the dP accumulator starts at
+// -delta_i) before 1/Z_i is applied.
 // The last identity (sum_j p_ij dP_ij = delta_i eps / Z_i) makes dscale a
 // per-row closed form, reduced in a fixed order: deterministic, and free of
 // the cancellation of an O(T^2) sum whose true value is O(eps).
 //
-// Launch sequence: delta pre-pass (delta' per row) -> dK/dV kernel (keys
-// stationary in registers, query tiles of Q and dO' staged in LDS in row and
-// transposed layouts) -> dQ kernel (queries stationary, K staged in both
-// layouts, V row-major) -> dscale reduction.
+// Launch sequence: delta pre-pass (delta and delta / Z per row) -> dK/dV
+// kernel (keys stationary in registers, query tiles of Q and dO staged in LDS
+// in row and transposed layouts) -> dQ kernel (queries stationary, K staged in
+// both layouts, V row-major) -> dscale reduction.
 #pragma once
 
 #include "born_common.h"
@@ -27,7 +31,7 @@
 namespace qdl {
 
 // ---------------------------------------------------------------------------
-// Pre-pass: delta'_i = (dO_i . O_i) / Z_i, one group of G lanes per row.
+// Pre-pass: delta_i = dO_i . O_i and delta_i / Z_i, one group of G lanes per row.
 // ---------------------------------------------------------------------------
 template <class E, bool F32>
 __global__ __launch_bounds__(256) void born_bwd_delta_kernel(BwdArgs p, int G) {
@@ -59,7 +63,10 @@ __global__ __launch_bounds__(256) void born_bwd_delta_kernel(BwdArgs p, int G) {
         }
     }
     for (int off = G >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (row < nrows && sub == 0) p.delta[row] = acc / p.z[row];
+    if (row < nrows && sub == 0) {
+        p.delta[row] = acc;
+        p.delta_z[row] = acc / p.z[row];
+    }
 }
 
 // Visibility of (query i, key j) under the kernel's mask mode.
@@ -126,7 +133,7 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     const uint16_t* __restrict__ V = reinterpret_cast<const uint16_t*>(p.v) + base;
     const uint16_t* __restrict__ dO = reinterpret_cast<const uint16_t*>(p.dout) + base;
     const float* __restrict__ Zr = p.z + (size_t)bh * T;
-    const float* __restrict__ Dl = p.delta + (size_t)bh * T;
+    const float* __restrict__ Dl = p.delta_z + (size_t)bh * T;
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
@@ -298,11 +305,11 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 // ---------------------------------------------------------------------------
 // dK / dV, 16-bit.  Keys stationary: each wave owns 32 keys, their K (sign
 // flipped) and V rows held in registers as MFMA B operands.  Query tiles of
-// BQ rows stream through LDS: Q and dO' = dO / Z, each in row-major and
-// transposed copies, plus -delta' per query.  Per tile and wave:
-//   S  = Q K'^T            (C layout: one key per lane, 16 queries per block)
-//   dP = dO' V^T - delta'  (accumulator initialised with -delta')
-//   dV^T += dO'^T relu(S)^2,  dK^T += Q^T (relu(S) dP)
+// BQ rows stream through LDS: Q and dO, each in row-major and transposed
+// copies, plus -delta and 1/Z per query.  Per tile and wave:
+//   S   = Q K'^T          (C layout: one key per lane, 16 queries per block)
+//   dPz = dO V^T - delta  (accumulator initialised with -delta)
+//   t = relu(S) / Z_i;  dV^T += dO^T (t relu(S)),  dK^T += Q^T (t dPz)
 // ---------------------------------------------------------------------------
 template <class E, int DP, int NW, int BQ, int MODE, int WPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
@@ -322,6 +329,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) uint16_t d_lds[2][BQ * RS];
     __shared__ __attribute__((aligned(16))) uint16_t dt_lds[2][DP * TS];
     __shared__ __attribute__((aligned(16))) float nd_lds[2][BQ];
+    __shared__ __attribute__((aligned(16))) float zi_lds[2][BQ];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BQ : 1];
 
     const int T = p.T, D = p.D;
@@ -376,14 +384,15 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     const int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
 
     Stage qst, dst;
-    float ndreg = 0.f;
+    float ndreg = 0.f, zireg = 0.f;
     int dreg = -1;
     auto load_tile = [&](int i0) {
         qst.template load<E>(Q, i0, T, D, tid);
-        dst.template load<E>(dO, i0, T, D, tid, Zr);
+        dst.template load<E>(dO, i0, T, D, tid);
         if (tid < BQ) {
             const int i = i0 + tid;
             ndreg = i < T ? -Dl[i] : 0.f;
+            zireg = i < T ? 1.0f / Zr[i] : 0.f;
             if (kDoc && has_doc) dreg = i < T ? docb[i] : -1;
         }
     };
@@ -394,6 +403,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         dst.template store_trans<TS>(dt_lds[buf], tid);
         if (tid < BQ) {
             nd_lds[buf][tid] = ndreg;
+            zi_lds[buf][tid] = zireg;
             if (kDoc && has_doc) doc_lds[buf][tid] = dreg;
         }
     };
@@ -431,12 +441,16 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
 #pragma unroll
             for (int qs = 0; qs < NQ; ++qs) {
                 f32x16 s = zero16();
-                f32x16 dp;
+                f32x16 dp, zi;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 n4 = *reinterpret_cast<const f32x4*>(&nd_lds[buf][qs * 32 + 8 * j + 4 * g]);
+                    const f32x4 z4 = *reinterpret_cast<const f32x4*>(&zi_lds[buf][qs * 32 + 8 * j + 4 * g]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) dp[4 * j + e] = n4[e];
+                    for (int e = 0; e < 4; ++e) {
+                        dp[4 * j + e] = n4[e];
+                        zi[4 * j + e] = z4[e];
+                    }
                 }
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
@@ -460,8 +474,9 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const float a0 = fmaxf(s[2 * j], 0.f), a1 = fmaxf(s[2 * j + 1], 0.f);
-                    w2[j] = E::pack(a0 * a0, a1 * a1);
-                    u2[j] = E::pack(a0 * dp[2 * j], a1 * dp[2 * j + 1]);
+                    const float t0 = a0 * zi[2 * j], t1 = a1 * zi[2 * j + 1];
+                    w2[j] = E::pack(t0 * a0, t1 * a1);
+                    u2[j] = E::pack(t0 * dp[2 * j], t1 * dp[2 * j + 1]);
                 }
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
@@ -574,7 +589,7 @@ void born_bwd_dq32_kernel(BwdArgs p) {
     }
     const bool qok = qi < T;
     const float zinv = qok ? 1.0f / p.z[(size_t)bh * T + qi] : 0.f;
-    const float nd = qok ? -p.delta[(size_t)bh * T + qi] : 0.f;
+    const float nd = qok ? -p.delta_z[(size_t)bh * T + qi] : 0.f;
     const int qdoc = (has_doc && qok) ? docb[qi] : -1;
 
     int kv_lo = 0;
@@ -677,7 +692,8 @@ void born_bwd_dq32_kernel(BwdArgs p) {
 // ---------------------------------------------------------------------------
 // dK / dV, fp32.  Keys stationary; K' and V rows of the wave's 32 keys are
 // B operands, in registers (KV_LDS = false) or, for wide heads, read from a
-// per-workgroup LDS copy (KV_LDS = true, one wave per workgroup).
+// per-workgroup LDS copy (KV_LDS = true, one wave per workgroup).  Same
+// arithmetic as the 16-bit kernel; fp32 operands need no transposed copies.
 // ---------------------------------------------------------------------------
 template <int DP, int NW, int BQ, int MODE, int WPE, bool KV_LDS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
@@ -697,6 +713,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) float d_lds[NBUF][BQ * RS];
     __shared__ __attribute__((aligned(16))) float kv_lds[KV_LDS ? 2 : 1][KV_LDS ? 32 * RS : 4];
     __shared__ __attribute__((aligned(16))) float nd_lds[NBUF][BQ];
+    __shared__ __attribute__((aligned(16))) float zi_lds[NBUF][BQ];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? NBUF : 1][kDoc ? BQ : 1];
 
     const int T = p.T, D = p.D;
@@ -763,7 +780,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     const int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
 
     Stage qst, dst;
-    float ndreg = 0.f;
+    float ndreg = 0.f, zireg = 0.f;
     int dreg = -1;
     auto load_tile = [&](int i0) {
         qst.load(Q, i0, T, D, tid);
@@ -771,25 +788,16 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         if (tid < BQ) {
             const int i = i0 + tid;
             ndreg = i < T ? -Dl[i] : 0.f;
+            zireg = i < T ? 1.0f / Zr[i] : 0.f;
             if (kDoc && has_doc) dreg = i < T ? docb[i] : -1;
         }
     };
-    // dO is divided by Z per row when written to LDS.
-    auto store_tile = [&](int buf, int i0) {
+    auto store_tile = [&](int buf) {
         qst.template store_rows<RS>(q_lds[buf], tid);
-#pragma unroll
-        for (int i = 0; i < Stage::PT; ++i) {
-            const int idx = tid + i * NT;
-            if (Stage::CH % NT == 0 || idx < Stage::CH) {
-                const int col = (idx % Stage::CPR) * 4;
-                const int row = idx / Stage::CPR;
-                const int gi = i0 + row;
-                const float zi = gi < T ? 1.0f / Zr[gi] : 0.f;
-                *reinterpret_cast<f32x4*>(&d_lds[buf][row * RS + col]) = dst.x[i] * zi;
-            }
-        }
+        dst.template store_rows<RS>(d_lds[buf], tid);
         if (tid < BQ) {
             nd_lds[buf][tid] = ndreg;
+            zi_lds[buf][tid] = zireg;
             if (kDoc && has_doc) doc_lds[buf][tid] = dreg;
         }
     };
@@ -803,7 +811,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
 
     if (ntiles > 0) {
         load_tile(q_lo);
-        store_tile(0, q_lo);
+        store_tile(0);
     }
     __syncthreads();
 
@@ -826,12 +834,16 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         if (active) {
 #pragma unroll
             for (int qs = 0; qs < NQ; ++qs) {
-                f32x16 s = zero16(), dp;
+                f32x16 s = zero16(), dp, zi;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 n4 = *reinterpret_cast<const f32x4*>(&nd_lds[buf][qs * 32 + 8 * j + 4 * g]);
+                    const f32x4 z4 = *reinterpret_cast<const f32x4*>(&zi_lds[buf][qs * 32 + 8 * j + 4 * g]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) dp[4 * j + e] = n4[e];
+                    for (int e = 0; e < 4; ++e) {
+                        dp[4 * j + e] = n4[e];
+                        zi[4 * j + e] = z4[e];
+                    }
                 }
 #pragma unroll
                 for (int u = 0; u < KQ; ++u) {
@@ -861,8 +873,9 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
                         const int qd = (kDoc && has_doc) ? doc_lds[buf][qi - i0] : 0;
                         if (!visible<MODE>(qi, key, causal, window, has_doc, qd, kdoc)) a = 0.f;
                     }
-                    w[r] = a * a;
-                    uu[r] = a * dp[r];
+                    const float t = a * zi[r];
+                    w[r] = t * a;
+                    uu[r] = t * dp[r];
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -876,13 +889,13 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
             }
         }
         if (NBUF == 2) {
-            if (more) store_tile(buf ^ 1, i0 + BQ);
+            if (more) store_tile(buf ^ 1);
             __syncthreads();
         } else {
             __syncthreads();
             if (more) {
                 load_tile(i0 + BQ);
-                store_tile(0, i0 + BQ);
+                store_tile(0);
             }
             __syncthreads();
         }

@@ -5,8 +5,8 @@
 
 namespace qdl {
 
-// dscale[out] = (2 / s) * eps * sum delta' over the rows of that output, in a
-// fixed order (double accumulation, fixed tree).
+// dscale[out] = (2 / s) * eps * sum delta / Z over the rows of that output,
+// in a fixed order (double accumulation, fixed tree).
 __global__ __launch_bounds__(256) void born_bwd_dscale_kernel(BwdArgs p) {
     __shared__ double red[256];
     const int out = blockIdx.x;
@@ -16,11 +16,11 @@ __global__ __launch_bounds__(256) void born_bwd_dscale_kernel(BwdArgs p) {
         const int64_t n = (int64_t)p.B * p.T;
         for (int64_t j = tid; j < n; j += 256) {
             const int64_t b = j / p.T, i = j % p.T;
-            acc += (double)p.delta[(b * p.H + out) * p.T + i];
+            acc += (double)p.delta_z[(b * p.H + out) * p.T + i];
         }
     } else {
         const int64_t n = (int64_t)p.B * p.H * p.T;
-        for (int64_t j = tid; j < n; j += 256) acc += (double)p.delta[j];
+        for (int64_t j = tid; j < n; j += 256) acc += (double)p.delta_z[j];
     }
     red[tid] = acc;
     __syncthreads();

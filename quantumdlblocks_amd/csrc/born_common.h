@@ -133,8 +133,8 @@ struct BwdArgs {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;          // (B, H, T) workspace
-    float* dscale_part;    // per-workgroup dscale partials (workspace)
+    float* delta;          // (B, H, T) workspace: dO . O per row
+    float* delta_z;        // (B, H, T) workspace: dO . O / Z per row
     float* dscale;         // n_scale outputs
     int per_head_scale;
     int B, H, T, D;

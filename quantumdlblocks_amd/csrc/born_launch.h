@@ -46,7 +46,7 @@ hipError_t bwd_launch_f32(const BwdArgs& a, hipStream_t s);
     }
 
 namespace qdl {
-// Backward workspace: delta (B*H*T fp32) followed by per-row dscale terms
+// Backward workspace: delta = dO . O (B*H*T fp32) followed by delta / Z
 // (B*H*T fp32), each region 256-byte aligned.
 inline int64_t bwd_region_bytes(int64_t B, int64_t H, int64_t T) {
     return ((B * H * T * 4) + 255) / 256 * 256;
@@ -56,10 +56,10 @@ inline int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t T) {
     return r > 0 ? 2 * r : 256;
 }
 inline void bwd_workspace_carve(void* ws, int64_t B, int64_t H, int64_t T, float** delta,
-                                float** dscale_part) {
+                                float** delta_z) {
     char* p = static_cast<char*>(ws);
     *delta = reinterpret_cast<float*>(p);
-    *dscale_part = reinterpret_cast<float*>(p + bwd_region_bytes(B, H, T));
+    *delta_z = reinterpret_cast<float*>(p + bwd_region_bytes(B, H, T));
 }
 }  // namespace qdl
 

@@ -336,6 +336,48 @@ def test_dscale_closed_form():
         np.testing.assert_allclose(ds, want, rtol=1e-9)
 
 
+def test_backward_out_argument():
+    """delta from a supplied forward output (the reference's stored O):
+    identical to the default for the exact O; dv does not depend on it; the
+    gradients are affine in it; a change in row i moves only row-i terms."""
+    B, H, T, D = 1, 2, 20, 6
+    q, k, v, do = _rand((B, H, T, D), seed=21, n=4)
+    O, _ = orc.forward(q, k, v, 1.7, True, 1e-6)
+    base = orc.backward(q, k, v, 1.7, do, True, 1e-6)
+    same = orc.backward(q, k, v, 1.7, do, True, 1e-6, out=O)
+    for x, y in zip(base, same):
+        np.testing.assert_array_equal(x, y)
+    rng = np.random.default_rng(0)
+    dO_ = rng.standard_normal(O.shape) * 1e-3
+    g1 = orc.backward(q, k, v, 1.7, do, True, 1e-6, out=O + dO_)
+    g2 = orc.backward(q, k, v, 1.7, do, True, 1e-6, out=O + 2 * dO_)
+    np.testing.assert_array_equal(g1[2], base[2])
+    for x0, x1, x2 in zip(base, g1, g2):
+        np.testing.assert_allclose(x2 - x0, 2 * (x1 - x0), rtol=1e-6, atol=1e-12)
+    row = np.zeros_like(O)
+    row[0, 1, 7] = 1e-3
+    g3 = orc.backward(q, k, v, 1.7, do, True, 1e-6, out=O + row)
+    changed = np.abs(g3[0] - base[0]).sum(-1) > 0  # dq rows
+    assert changed[0, 1, 7] and changed.sum() == 1
+    # dk of key j moves only where query 7 sees it (causal: j <= 7)
+    moved = np.abs(g3[1] - base[1]).sum(-1)[0, 1] > 0
+    assert not moved[8:].any()
+
+
+def test_backward_magnitudes_bound_and_dv():
+    B, H, T, D = 2, 2, 24, 8
+    q, k, v, do = _rand((B, H, T, D), seed=22, n=4)
+    for kw in ({}, {"is_causal": False}, {"window_size": 5}):
+        g = orc.backward(q, k, v, 2.0, do, eps=1e-6, **kw)
+        m = orc.backward_magnitudes(q, k, v, 2.0, do, eps=1e-6, **kw)
+        for gi, mi in zip(g[:3], m):
+            assert np.all(np.abs(gi) <= mi * (1 + 1e-12) + 1e-300)
+    dpos = np.abs(do)
+    g = orc.backward(q, k, v, 2.0, dpos, eps=1e-6)
+    m = orc.backward_magnitudes(q, k, v, 2.0, dpos, eps=1e-6)
+    np.testing.assert_allclose(m[2], np.abs(g[2]), rtol=1e-12)
+
+
 def test_eager_fp32_restatement_matches():
     B, H, T, D = 2, 3, 40, 16
     q, k, v = (torch.tensor(x, dtype=torch.float32) for x in _rand((B, H, T, D), seed=13))
