@@ -68,6 +68,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    wanted = {s.stem + ".o" for s in sources}
+    for stale in BUILD.glob("*.o"):  # objects of sources that no longer exist
+        if stale.name not in wanted:
+            stale.unlink()
     jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), sources))

@@ -5,22 +5,27 @@
 
 namespace qdl {
 
-// dscale[out] = (2 / s) * eps * sum delta / Z over the rows of that output,
-// in a fixed order (double accumulation, fixed tree).
-__global__ __launch_bounds__(256) void born_bwd_dscale_kernel(BwdArgs p) {
+// dscale[out] = (2 / s) * eps * sum delta / Z over the rows of that output.
+// Two fixed-order stages (no atomics, so the result is bitwise reproducible):
+// stage 1 sums DSCALE_CHUNKS contiguous chunks of each output's rows into
+// double partials, stage 2 adds the partials in order.
+__global__ __launch_bounds__(256) void born_bwd_dscale_partial_kernel(BwdArgs p, double* part) {
     __shared__ double red[256];
-    const int out = blockIdx.x;
+    const int out = blockIdx.y;
+    const int chunk = blockIdx.x;
     const int tid = threadIdx.x;
+    const int64_t n = p.per_head_scale ? (int64_t)p.B * p.T : (int64_t)p.B * p.H * p.T;
+    const int64_t len = (n + DSCALE_CHUNKS - 1) / DSCALE_CHUNKS;
+    const int64_t lo = chunk * len;
+    const int64_t hi = lo + len < n ? lo + len : n;
     double acc = 0.0;
-    if (p.per_head_scale) {
-        const int64_t n = (int64_t)p.B * p.T;
-        for (int64_t j = tid; j < n; j += 256) {
+    for (int64_t j = lo + tid; j < hi; j += 256) {
+        int64_t idx = j;
+        if (p.per_head_scale) {
             const int64_t b = j / p.T, i = j % p.T;
-            acc += (double)p.delta_z[(b * p.H + out) * p.T + i];
+            idx = (b * p.H + out) * p.T + i;
         }
-    } else {
-        const int64_t n = (int64_t)p.B * p.H * p.T;
-        for (int64_t j = tid; j < n; j += 256) acc += (double)p.delta_z[j];
+        acc += (double)p.delta_z[idx];
     }
     red[tid] = acc;
     __syncthreads();
@@ -28,10 +33,16 @@ __global__ __launch_bounds__(256) void born_bwd_dscale_kernel(BwdArgs p) {
         if (tid < w) red[tid] += red[tid + w];
         __syncthreads();
     }
-    if (tid == 0) {
-        const float s = p.scale[out];
-        p.dscale[out] = (s == 0.f) ? 0.f : (float)(2.0 / (double)s * (double)p.eps * red[0]);
-    }
+    if (tid == 0) part[out * DSCALE_CHUNKS + chunk] = red[0];
+}
+
+__global__ __launch_bounds__(64) void born_bwd_dscale_final_kernel(BwdArgs p, const double* part) {
+    const int out = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    double acc = 0.0;
+    for (int c = 0; c < DSCALE_CHUNKS; ++c) acc += part[out * DSCALE_CHUNKS + c];
+    const float s = p.scale[out];
+    p.dscale[out] = (s == 0.f) ? 0.f : (float)(2.0 / (double)s * (double)p.eps * acc);
 }
 
 __global__ void born_zero_fill_kernel(float* __restrict__ x, int64_t n) {
@@ -42,7 +53,12 @@ __global__ void born_zero_fill_kernel(float* __restrict__ x, int64_t n) {
 
 hipError_t launch_bwd_common_post(const BwdArgs& a, hipStream_t st) {
     const int nout = a.per_head_scale ? a.H : 1;
-    hipLaunchKernelGGL(born_bwd_dscale_kernel, dim3(nout), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(born_bwd_dscale_partial_kernel, dim3(DSCALE_CHUNKS, nout), dim3(256), 0, st, a,
+                       a.dscale_part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(born_bwd_dscale_final_kernel, dim3(nout), dim3(64), 0, st, a,
+                       (const double*)a.dscale_part);
     return hipGetLastError();
 }
 

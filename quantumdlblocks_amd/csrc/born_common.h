@@ -53,10 +53,11 @@ struct BF16 {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
-    // Round-to-nearest-even fp32 pair -> packed 16-bit pair (v_cvt_pk_bf16_f32).
+    // Round-to-nearest-even fp32 pair -> packed 16-bit pair; the vector
+    // conversion maps to one v_cvt_pk_bf16_f32 (element-wise casts do not).
     __device__ __forceinline__ static uint32_t pack(float x, float y) {
-        bf16x2 h = {(__bf16)x, (__bf16)y};
-        return __builtin_bit_cast(uint32_t, h);
+        const f32x2 f = {x, y};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
     }
     // acc + u.lo + u.hi in fp32 (v_dot2c_f32_bf16 against (1, 1)).
     __device__ __forceinline__ static float sum2(uint32_t u, float acc) {
@@ -74,8 +75,8 @@ struct F16 {
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
     }
     __device__ __forceinline__ static uint32_t pack(float x, float y) {
-        f16x2 h = {(_Float16)x, (_Float16)y};
-        return __builtin_bit_cast(uint32_t, h);
+        const f32x2 f = {x, y};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
     }
     __device__ __forceinline__ static float sum2(uint32_t u, float acc) {
         const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -91,6 +92,17 @@ struct F16 {
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives
+// element (i % 4) of the 4 x 16-bit chunks addressed by lanes i/4, 4 + i/4,
+// 8 + i/4 and 12 + i/4.  With those four lanes pointing at 4 consecutive rows
+// of a row-major tile, lane i gets 4 consecutive rows of one column.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(u32x2, v);
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
@@ -135,6 +147,7 @@ struct BwdArgs {
     void* dv;
     float* delta;          // (B, H, T) workspace: dO . O per row
     float* delta_z;        // (B, H, T) workspace: dO . O / Z per row
+    double* dscale_part;   // (n_scale, DSCALE_CHUNKS) workspace: dscale partial sums
     float* dscale;         // n_scale outputs
     int per_head_scale;
     int B, H, T, D;
@@ -142,6 +155,9 @@ struct BwdArgs {
     int window;
     float eps;
 };
+
+// Fixed number of partial sums per dscale output (deterministic reduction).
+constexpr int DSCALE_CHUNKS = 128;
 
 // Mask modes compiled into the kernels.
 enum MaskMode : int {

@@ -14,11 +14,15 @@
 //                        sign(s) is applied to Q once, s^2 at the end
 //   z  += p'_lo + p'_hi  v_dot2c_f32 against (1, 1): z sums exactly the
 //                        rounded weights the PV product uses
-//   O^T += V^T * P^T     A = V^T from LDS (V is transposed while staging),
-//                        B = P^T straight from the S^T accumulator registers:
-//                        the 32x32 C layout gives each lane one query and 8
-//                        keys per 16-key chunk, which is the B layout up to a
+//   O^T += V^T * P^T     A = V^T read from the row-major V tile with
+//                        ds_read_b64_tr_b16 (transpose on read), B = P^T
+//                        straight from the S^T accumulator registers: the
+//                        32x32 C layout gives each lane one query and 8 keys
+//                        per 16-key chunk, which is the B layout up to a
 //                        permutation of keys that the V^T read applies too.
+// LDS rows are padded for the 32-bank LDS: K rows by 16 bytes (conflict-free
+// 16-byte reads of 8 consecutive rows), V rows to 32 mod 128 bytes (the four
+// rows a 16-lane transpose read touches fall in distinct banks).
 // At the end each lane owns one query: z is completed with one cross-half
 // shuffle, O = O^T / (z + eps / s^2), Z = s^2 z + eps.
 #pragma once
@@ -42,15 +46,13 @@ void born_fwd16_kernel(FwdArgs p) {
     constexpr int NB = BN / 32;
     constexpr int NT = NW * 64;
     constexpr int KSTR = DP + 8;   // K row stride in LDS (elements)
-    constexpr int VSTR = BN + 4;   // V^T row stride in LDS (elements)
-    constexpr int KCH = BN * DP / 8;          // 16-byte K chunks per tile
+    constexpr int VSTR = DP + 16;  // V row stride in LDS (elements)
+    constexpr int KCH = BN * DP / 8;          // 16-byte chunks per K or V tile
     constexpr int KPT = (KCH + NT - 1) / NT;
-    constexpr int VCH = (BN / 2) * (DP / 8);  // (2 keys x 8 dims) V chunks per tile
-    constexpr int VPT = (VCH + NT - 1) / NT;
     constexpr bool kDoc = (MODE == kGeneral);
 
     __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BN * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][DP * VSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][BN * VSTR];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
 
     const int T = p.T, D = p.D;
@@ -85,6 +87,7 @@ void born_fwd16_kernel(FwdArgs p) {
 
     // Q^T operand, resident for the whole kernel.
     u32x4 qr[NQB][KS];
+    const bool q_full = (q0 + QW <= T) && (D == DP);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const int row = q0 + qb * 32 + c;
@@ -92,7 +95,7 @@ void born_fwd16_kernel(FwdArgs p) {
         for (int ks = 0; ks < KS; ++ks) {
             const int d = ks * 16 + g * 8;
             u32x4 x = {0u, 0u, 0u, 0u};
-            if (row < T && d < D) x = ldg16(Q + (size_t)row * D + d);
+            if (q_full || (row < T && d < D)) x = ldg16(Q + (size_t)row * D + d);
             x ^= flip;
             qr[qb][ks] = x;
         }
@@ -110,11 +113,15 @@ void born_fwd16_kernel(FwdArgs p) {
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
     const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
 
-    u32x4 kreg[KPT];
-    u32x4 vreg[VPT][2];
-    int dreg = -2;
-
-    auto load_tile = [&](int key0) {
+    // Staged tile in registers: 16-byte K and V row chunks, the tile's doc ids.
+    struct Regs {
+        u32x4 k[KPT];
+        u32x4 v[KPT];
+        int d;
+    };
+    // Interior tiles (all keys < T, D == DP) load without bounds checks.
+    auto load_tile = [&](Regs& r, int key0) {
+        const bool full = (key0 + BN <= T) && (D == DP);
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int idx = tid + i * NT;
@@ -122,58 +129,32 @@ void born_fwd16_kernel(FwdArgs p) {
                 const int row = idx / (DP / 8);
                 const int col = (idx % (DP / 8)) * 8;
                 const int key = key0 + row;
-                u32x4 x = {0u, 0u, 0u, 0u};
-                if (key < T && col < D) x = ldg16(K + (size_t)key * D + col);
-                kreg[i] = x;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = tid + i * NT;
-            if (VCH % NT == 0 || idx < VCH) {
-                const int col = (idx % (DP / 8)) * 8;
-                const int key = key0 + 2 * (idx / (DP / 8));
-                u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
-                if (col < D) {
-                    if (key < T) x0 = ldg16(V + (size_t)key * D + col);
-                    if (key + 1 < T) x1 = ldg16(V + (size_t)(key + 1) * D + col);
+                u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+                if (full || (key < T && col < D)) {
+                    x = ldg16(K + (size_t)key * D + col);
+                    y = ldg16(V + (size_t)key * D + col);
                 }
-                vreg[i][0] = x0;
-                vreg[i][1] = x1;
+                r.k[i] = x;
+                r.v[i] = y;
             }
         }
         if (kDoc && has_doc && tid < BN) {
             const int key = key0 + tid;
-            dreg = key < T ? docb[key] : -2;
+            r.d = key < T ? docb[key] : -2;
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](const Regs& r, int buf) {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int idx = tid + i * NT;
             if (KCH % NT == 0 || idx < KCH) {
                 const int row = idx / (DP / 8);
                 const int col = (idx % (DP / 8)) * 8;
-                *reinterpret_cast<u32x4*>(&k_lds[buf][row * KSTR + col]) = kreg[i];
+                *reinterpret_cast<u32x4*>(&k_lds[buf][row * KSTR + col]) = r.k[i];
+                *reinterpret_cast<u32x4*>(&v_lds[buf][row * VSTR + col]) = r.v[i];
             }
         }
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = tid + i * NT;
-            if (VCH % NT == 0 || idx < VCH) {
-                const int col = (idx % (DP / 8)) * 8;
-                const int kp = idx / (DP / 8);
-                const u32x4 a = vreg[i][0], bb = vreg[i][1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t even = (a[j] & 0xffffu) | (bb[j] << 16);
-                    const uint32_t odd = (a[j] >> 16) | (bb[j] & 0xffff0000u);
-                    *reinterpret_cast<uint32_t*>(&v_lds[buf][(col + 2 * j) * VSTR + 2 * kp]) = even;
-                    *reinterpret_cast<uint32_t*>(&v_lds[buf][(col + 2 * j + 1) * VSTR + 2 * kp]) = odd;
-                }
-            }
-        }
-        if (kDoc && has_doc && tid < BN) doc_lds[buf][tid] = dreg;
+        if (kDoc && has_doc && tid < BN) doc_lds[buf][tid] = r.d;
     };
 
     f32x16 oacc[DB][NQB];
@@ -181,22 +162,11 @@ void born_fwd16_kernel(FwdArgs p) {
     for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
-    float zacc[NQB];
+    float zacc[NQB][2];
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) zacc[qb] = 0.f;
+    for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
 
-    if (ntiles > 0) {
-        load_tile(kv_lo);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int key0 = kv_lo + t * BN;
-        const int buf = t & 1;
-        const bool more = (t + 1) < ntiles;
-        if (more) load_tile(key0 + BN);
-
+    auto compute = [&](int buf, int key0) {
         // Which of this wave's (query, key) pairs can be visible in the tile.
         bool active = q0 < T;
         bool need_mask = has_doc;
@@ -208,70 +178,93 @@ void born_fwd16_kernel(FwdArgs p) {
             active = active && (key0 + BN - 1 > q0 - window);
             need_mask = need_mask || (key0 <= q0 + QW - 1 - window);
         }
-
-        if (active) {
+        if (!active) return;
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                f32x16 s[NQB];
+        for (int nb = 0; nb < NB; ++nb) {
+            f32x16 s[NQB];
 #pragma unroll
-                for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
+            for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(
-                        &k_lds[buf][(nb * 32 + c) * KSTR + ks * 16 + g * 8]);
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(
+                    &k_lds[buf][(nb * 32 + c) * KSTR + ks * 16 + g * 8]);
 #pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(a, qr[qb][ks], s[qb]);
-                }
-                if (need_mask) {
-                    const int kbase = key0 + nb * 32 + 4 * g;
-#pragma unroll
-                    for (int qb = 0; qb < NQB; ++qb) {
-                        const int qi = q0 + qb * 32 + c;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = kbase + 8 * (r >> 2) + (r & 3);
-                            bool vis = true;
-                            if (causal) vis = vis && (key <= qi);
-                            if (window > 0) vis = vis && (qi - key < window);
-                            if (kDoc && has_doc)
-                                vis = vis && (doc_lds[buf][key - key0] == qdoc[qb]);
-                            if (!vis) s[qb][r] = 0.f;
-                        }
-                    }
-                }
-                uint32_t pk[NQB][8];
+                for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(a, qr[qb][ks], s[qb]);
+            }
+            if (need_mask) {
+                const int kbase = key0 + nb * 32 + 4 * g;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
+                    // key = kbase + off(r); visible iff off(r) <= qi - kbase
+                    // (causal) and off(r) > qi - kbase - window.
+                    const int lim = q0 + qb * 32 + c - kbase;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
-                        uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
-                        u = relu_pk16(u);
-                        zacc[qb] = E::sum2(u, zacc[qb]);
-                        pk[qb][j] = u;
+                    for (int r = 0; r < 16; ++r) {
+                        const int off = 8 * (r >> 2) + (r & 3);
+                        bool vis = true;
+                        if (causal) vis = vis && (off <= lim);
+                        if (window > 0) vis = vis && (off > lim - window);
+                        if (kDoc && has_doc)
+                            vis = vis && (doc_lds[buf][kbase - key0 + off] == qdoc[qb]);
+                        if (!vis) s[qb][r] = 0.f;
                     }
                 }
+            }
+            uint32_t pk[NQB][8];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
+            for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
-                    for (int db = 0; db < DB; ++db) {
-                        const uint16_t* vrow =
-                            &v_lds[buf][(db * 32 + c) * VSTR + nb * 32 + hh * 16 + g * 4];
-                        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-                        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-                        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+                for (int j = 0; j < 8; ++j) {
+                    const float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                    uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
+                    u = relu_pk16(u);
+                    zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
+                    pk[qb][j] = u;
+                }
+            }
+            // V^T operand of the 16-key chunk (nb, hh): lane group G = lane / 16
+            // reads rows key + 4 (G / 2) + i / 4 (and +8), columns
+            // 16 (G % 2) + 4 (i % 4) of each 32-wide d block.
+            const int vr = nb * 32 + 4 * (lane >> 5) + ((lane & 15) >> 2);
+            const int vc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-                        for (int qb = 0; qb < NQB; ++qb) {
-                            const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1],
-                                              pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
-                            oacc[db][qb] = E::mfma(a, bq, oacc[db][qb]);
-                        }
+            for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const uint16_t* vp = &v_lds[buf][(vr + hh * 16) * VSTR + db * 32 + vc];
+                    const u32x2 lo = lds_read_tr16(vp);
+                    const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
+                    const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+                    for (int qb = 0; qb < NQB; ++qb) {
+                        const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2],
+                                          pk[qb][4 * hh + 3]};
+                        oacc[db][qb] = E::mfma(a, bq, oacc[db][qb]);
                     }
                 }
             }
         }
+    };
 
-        if (more) store_tile(buf ^ 1);
+    // Software pipeline, prefetch distance 2: while tile t is consumed from
+    // LDS buffer t%2, register set (t+1)%2 holds tile t+1 and tile t+2 is in
+    // flight into the other set; each load has two tiles of compute to land.
+    Regs ra, rb;
+    if (ntiles > 0) {
+        load_tile(ra, kv_lo);
+        store_tile(ra, 0);
+    }
+    if (ntiles > 1) load_tile(rb, kv_lo + BN);
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {
+        if (t + 2 < ntiles) load_tile(ra, kv_lo + (t + 2) * BN);
+        compute(0, kv_lo + t * BN);
+        if (t + 1 < ntiles) store_tile(rb, 1);
+        __syncthreads();
+        if (t + 1 >= ntiles) break;
+        if (t + 3 < ntiles) load_tile(rb, kv_lo + (t + 3) * BN);
+        compute(1, kv_lo + (t + 1) * BN);
+        if (t + 2 < ntiles) store_tile(ra, 0);
         __syncthreads();
     }
 
@@ -282,7 +275,8 @@ void born_fwd16_kernel(FwdArgs p) {
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-        const float zt = zacc[qb] + __shfl_xor(zacc[qb], 32);
+        const float zl = zacc[qb][0] + zacc[qb][1];
+        const float zt = zl + __shfl_xor(zl, 32);
         const float rcp = 1.0f / (zt + eps_s);
         const int qi = q0 + qb * 32 + c;
         if (qi < T) {
@@ -455,13 +449,14 @@ void born_fwd32_kernel(FwdArgs p) {
                 }
                 if (need_mask) {
                     const int kbase = key0 + nb * 32 + 4 * g;
+                    const int lim = qi - kbase;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int key = kbase + 8 * (r >> 2) + (r & 3);
+                        const int off = 8 * (r >> 2) + (r & 3);
                         bool vis = true;
-                        if (causal) vis = vis && (key <= qi);
-                        if (window > 0) vis = vis && (qi - key < window);
-                        if (kDoc && has_doc) vis = vis && (doc_lds[buf][key - key0] == qdoc);
+                        if (causal) vis = vis && (off <= lim);
+                        if (window > 0) vis = vis && (off > lim - window);
+                        if (kDoc && has_doc) vis = vis && (doc_lds[buf][kbase - key0 + off] == qdoc);
                         if (!vis) s[r] = 0.f;
                     }
                 }
@@ -509,13 +504,26 @@ void born_fwd32_kernel(FwdArgs p) {
     }
 }
 
-// Tile configuration per padded head dim (16-bit inputs).
+// Tile configuration per padded head dim (16-bit inputs).  The D <= 64
+// configuration can be overridden at build time (QDL_FWD64_*) for tuning.
+#ifndef QDL_FWD64_NQB
+#define QDL_FWD64_NQB 2
+#endif
+#ifndef QDL_FWD64_NW
+#define QDL_FWD64_NW 4
+#endif
+#ifndef QDL_FWD64_BN
+#define QDL_FWD64_BN 64
+#endif
+#ifndef QDL_FWD64_WPE
+#define QDL_FWD64_WPE 2
+#endif
 template <int DP>
 struct Fwd16Cfg {
-    static constexpr int NQB = DP <= 64 ? 2 : 1;
-    static constexpr int NW = 4;
-    static constexpr int BN = DP <= 128 ? 64 : 32;
-    static constexpr int WPE = DP <= 128 ? 2 : 1;
+    static constexpr int NQB = DP <= 64 ? QDL_FWD64_NQB : 1;
+    static constexpr int NW = DP <= 64 ? QDL_FWD64_NW : 4;
+    static constexpr int BN = DP <= 64 ? QDL_FWD64_BN : (DP <= 128 ? 64 : 32);
+    static constexpr int WPE = DP <= 64 ? QDL_FWD64_WPE : (DP <= 128 ? 2 : 1);
     static constexpr int BM = NW * 32 * NQB;
 };
 

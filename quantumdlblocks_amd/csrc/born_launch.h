@@ -46,20 +46,27 @@ hipError_t bwd_launch_f32(const BwdArgs& a, hipStream_t s);
     }
 
 namespace qdl {
-// Backward workspace: delta = dO . O (B*H*T fp32) followed by delta / Z
-// (B*H*T fp32), each region 256-byte aligned.
+// Backward workspace (each region 256-byte aligned):
+//   delta   = dO . O          (B*H*T fp32)
+//   delta_z = dO . O / Z      (B*H*T fp32)
+//   dscale partial sums       (H * DSCALE_CHUNKS fp64)
 inline int64_t bwd_region_bytes(int64_t B, int64_t H, int64_t T) {
     return ((B * H * T * 4) + 255) / 256 * 256;
 }
+inline int64_t bwd_partial_bytes(int64_t H) {
+    const int64_t n = (H > 1 ? H : 1) * DSCALE_CHUNKS * 8;
+    return (n + 255) / 256 * 256;
+}
 inline int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t T) {
-    const int64_t r = bwd_region_bytes(B, H, T);
-    return r > 0 ? 2 * r : 256;
+    return 2 * bwd_region_bytes(B, H, T) + bwd_partial_bytes(H);
 }
 inline void bwd_workspace_carve(void* ws, int64_t B, int64_t H, int64_t T, float** delta,
-                                float** delta_z) {
+                                float** delta_z, double** part) {
     char* p = static_cast<char*>(ws);
+    const int64_t r = bwd_region_bytes(B, H, T);
     *delta = reinterpret_cast<float*>(p);
-    *delta_z = reinterpret_cast<float*>(p + bwd_region_bytes(B, H, T));
+    *delta_z = reinterpret_cast<float*>(p + r);
+    *part = reinterpret_cast<double*>(p + 2 * r);
 }
 }  // namespace qdl
 
