@@ -1,5 +1,6 @@
 // Forward kernel instantiations for bf16 inputs.
 #include "born_fwd.h"
+#include "born_fwd_fast.h"
 #include "born_launch.h"
 
 namespace qdl {
@@ -7,6 +8,10 @@ namespace qdl {
 hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
     const int dp = padded_head_dim(a.D);
     const int mode = mask_mode(a.is_causal, a.window, a.doc);
+    // Hot path: D == 64 exactly, dense or causal, per-head slice addressable
+    // with 32-bit buffer offsets.
+    if (a.D == 64 && mode != kGeneral && (int64_t)a.T * a.D * 2 < ((int64_t)1 << 31))
+        return mode == kCausal ? launch_fwd16_fast<BF16, 64, kCausal>(a, s) : launch_fwd16_fast<BF16, 64, kDense>(a, s);
 #define QDL_MODE_BODY(M) return launch_fwd16<BF16, DPV, M>(a, s);
 #define QDL_DP_BODY(D_) { constexpr int DPV = D_; QDL_SWITCH_MODE(mode, QDL_MODE_BODY) }
     QDL_SWITCH_DP(dp, QDL_DP_BODY)
