@@ -2,28 +2,36 @@
 // or causal without window/document masks: the C2/C3/C5 hot path.
 //
 // Same arithmetic as born_fwd16_kernel (born_fwd.h); what changes is how the
-// tiles move and how the wave's instruction stream is laid out:
-//   * K and V tiles go global -> LDS with buffer_load_dwordx4 ... lds (no
+// tiles move, how work is spread over workgroups and waves, and how the
+// wave's instruction stream is laid out:
+//   * Q, K and V tiles go global -> LDS with buffer_load_dwordx4 ... lds (no
 //     staging registers, no staging VALU).  Each wave instruction writes 1 KiB
 //     of LDS contiguously (lane l at base + 16 l), so tiles are dense in LDS
 //     and 16-byte chunks are XOR-swizzled within each row instead of padded:
-//       K: chunk' = chunk ^ (row & 7)       -> 8-row ds_read_b128 conflict-free
-//       V: chunk' = chunk ^ 2 (row & 3)     -> 4-row ds_read_b64_tr_b16 conflict-free
+//       Q, K: chunk' = chunk ^ (row & 7)    -> 8-row ds_read_b128 conflict-free
+//       V:    chunk' = chunk ^ 2 (row & 3)  -> 4-row ds_read_b64_tr_b16 conflict-free
 //     (32 banks x 4 bytes).  Each lane picks the global chunk that belongs in
-//     its fixed LDS slot.  Keys >= T lie beyond the buffer's num_records and
+//     its fixed LDS slot.  Rows >= T lie beyond the buffer's num_records and
 //     arrive as zeros.
-//   * Four LDS stages: loads run three tiles ahead and are waited for one
-//     tile ahead, so tile t+1 is resident while tile t is computed.  One
-//     barrier per tile.
+//   * A workgroup handles two 256-row query blocks of one (batch, head): mb
+//     and nmb-1-mb.  Under causality their key ranges add up to the same
+//     length for every pair, so all workgroups carry equal work, and the
+//     second block's Q and first K/V tiles are loaded while the first block
+//     finishes: there is one load burst per workgroup instead of one per
+//     query block.  On the second block the wave -> rows map is mirrored, so
+//     each wave's visible-key count, summed over both blocks, is the same.
+//   * K/V tiles of both blocks form one sequence through a ring of three LDS
+//     stages: tile u+2 is issued when tile u starts and tile u+1 is waited
+//     for one tile ahead.  One barrier per tile.
 //   * Per tile the wave runs QK(keys 0-31), then QK(keys 32-63) interleaved
 //     with the first half's elementwise pass, then PV(first half) interleaved
 //     with the second half's elementwise pass, then PV(second half); the
 //     interleave is pinned with sched_group_barrier so MFMA and VALU co-issue.
 //     Every phase's LDS operands are read one phase earlier (the next tile's
 //     first K operands during the last PV), so no MFMA waits on an LDS read.
-//   * Each wave owns 32*NQB consecutive query rows; under causality a wave
-//     skips the tiles past its last row and masks exactly one diagonal tile
-//     (the same code path with the causal mask applied).
+//   * Each wave owns 64 consecutive query rows of a block; under causality a
+//     wave skips the tiles past its last row and masks exactly one diagonal
+//     tile (the same code path, instantiated with the causal mask).
 #pragma once
 
 #include <type_traits>
@@ -76,9 +84,13 @@ struct FastFwdCfg {
     static constexpr int NW = 4;
     static constexpr int NQB = 2;
     static constexpr int BN = 64;
-    static constexpr int NST = 4;
+    static constexpr int NST = 3;
     static constexpr int BM = NW * 32 * NQB;
 };
+
+// Query blocks per (batch, head) and workgroups per (batch, head).
+__host__ __device__ inline int fast_fwd_nmb(int T, int BM) { return (T + BM - 1) / BM; }
+__host__ __device__ inline int fast_fwd_npair(int T, int BM) { return (fast_fwd_nmb(T, BM) + 1) / 2; }
 
 template <class E, int DP, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -92,64 +104,56 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int QB = BM * RB;            // bytes per Q block
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
-    static_assert(TB % (1024 * NW) == 0, "tile split");
+    constexpr int LQW = QB / (1024 * NW);  // 1-KiB loads per wave per Q block
+    static_assert(TB % (1024 * NW) == 0 && QB % (1024 * NW) == 0, "tile split");
+    static_assert(NST == 3, "vmcnt bookkeeping below assumes a three-stage ring");
     constexpr bool kCaus = (MODE == kCausal);
 
-    // Ring of NST stages.  The DMA loads are issued as inline asm, so the
-    // compiler never waits on them; their completion is tracked by the
-    // pipeline's own vmcnt waits and barriers.
+    // The DMA loads are issued as inline asm, so the compiler never waits on
+    // them; their completion is tracked by the pipeline's own vmcnt waits and
+    // barriers.  80 KiB in all: two workgroups per CU.
     __shared__ __attribute__((aligned(1024))) uint8_t k_lds[NST * TB];
     __shared__ __attribute__((aligned(1024))) uint8_t v_lds[NST * TB];
+    __shared__ __attribute__((aligned(1024))) uint8_t q_lds[QB];
 
     const int T = p.T;
     const int BH = p.B * p.H;
-    const int nmb = (T + BM - 1) / BM;
+    const int nmb = fast_fwd_nmb(T, BM);
     const int bid = blockIdx.x;
     const int bh = bid % BH;
-    const int mb = kCaus ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int pr = bid / BH;
     const int h = bh % p.H;
-    const int m0 = mb * BM;
+    // Item 0: query block nmb-1-pr (the longer key range under causality);
+    // item 1: query block pr, when that is a different block.
+    const int mb_a = nmb - 1 - pr, mb_b = pr;
+    const int nitems = (mb_a != mb_b) ? 2 : 1;
+    auto item_tiles = [&](int mb) -> int {
+        const int kv_hi = kCaus ? min(T, (mb + 1) * BM) : T;
+        return (kv_hi + BN - 1) / BN;
+    };
+    const int nt_a = item_tiles(mb_a);
+    const int ntot = nt_a + (nitems == 2 ? item_tiles(mb_b) : 0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const int c = lane & 31, g = lane >> 5;
 
-    // Query rows of block qb of this wave.
-    int qrow0[NQB];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) qrow0[qb] = m0 + 32 * (NQB * wave + qb);
-    const int q_lo = qrow0[0];
-
     const size_t base = (size_t)bh * T * DP;
-    const uint16_t* __restrict__ Q = reinterpret_cast<const uint16_t*>(p.q) + base;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
 
-    u32x4 qr[NQB][KS];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        const int row = qrow0[qb] + c;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            u32x4 x = {0u, 0u, 0u, 0u};
-            if (row < T) x = ldg16(Q + (size_t)row * DP + ks * 16 + g * 8);
-            qr[qb][ks] = x ^ flip;
-        }
-    }
-
-    const int kv_hi = kCaus ? min(T, m0 + BM) : T;
-    const int ntiles = (kv_hi + BN - 1) / BN;
-
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
 
-    // Tile `t` -> stage `st`: wave-instruction i writes LDS slots
-    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
-    auto issue = [&](int t, int st) __attribute__((always_inline)) {
-        const int key0 = t * BN;
+    // Tile u of the block's sequence -> stage st: wave-instruction i writes
+    // LDS slots (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    auto issue = [&](int u, int st) __attribute__((always_inline)) {
+        const int key0 = (u < nt_a ? u : u - nt_a) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -161,15 +165,20 @@ void born_fwd16_fast_kernel(FwdArgs p) {
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
         }
     };
+    auto issue_q = [&](int mb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < LQW; ++i) {
+            const int slot = (wave * LQW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            dma_load16(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
+                       (mb * BM + row) * RB + ((pc ^ (row & 7)) << 4));
+        }
+    };
 
+    int qrow0[NQB];  // first query row of block qb of this wave (current item)
+    u32x4 qr[NQB][KS];
     f32x16 oacc[DB][NQB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
     float zacc[NQB][2];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
 
     // Per-lane LDS byte offsets that do not depend on the tile.
     // K (A operand of S^T = K Q^T): row nb*32 + c, chunk 2 ks + g.
@@ -292,74 +301,117 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Tile t lives in stage t % NST.  Loads run three tiles ahead; tile t+1
-    // is waited for at the top of iteration t, so it is resident while tile
-    // t is computed and its first K operands can be read in tile t's last phase.
-    for (int t = 0; t < 3 && t < ntiles; ++t) issue(t, t);
-    if (ntiles > 2)
-        wait_vmcnt<2 * LPW>();
+    // Rows 64 wr .. 64 wr + 63 of the Q block in LDS -> B operands of S^T.
+    // The sign of the scale is folded into Q; the asm pins the result in
+    // registers so it is not recomputed inside the tile loop.
+    auto load_q = [&](int wr) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int row = 32 * (NQB * wr + qb) + c;
+                const int pc = (2 * ks + g) ^ (row & 7);
+                qr[qb][ks] = *reinterpret_cast<const u32x4*>(q_lds + row * RB + pc * 16) ^ flip;
+                asm volatile("" : "+v"(qr[qb][ks]));
+            }
+    };
+
+    // Top of iteration u: tile u+1 resident for everyone and tile u-1
+    // consumed; tile u+2 is then issued into the stage tile u-1 held.  The
+    // second item's Q block is issued at the top of iteration 1 (every wave
+    // has read the first item's Q by then) ahead of tile 3, so the full drain
+    // at the top of iteration 2 covers it.
+    const bool early_q = (nitems == 2) && (nt_a >= 3);
+    int st = 0;         // stage of tile u
+    int sti = NST - 1;  // stage of tile u + NST - 1
+    auto advance = [&](int u) __attribute__((always_inline)) {
+        if (u > 0) {
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+        if (u == 1 && early_q) issue_q(mb_b);
+        if (u + NST - 1 < ntot) issue(u + NST - 1, sti);
+        sti = (sti + 1 == NST) ? 0 : sti + 1;
+    };
+    auto next_stage = [](int s) { return (s + 1 == NST) ? 0 : s + 1; };
+
+    issue_q(mb_a);
+    const int npro = min(NST - 1, ntot);
+    for (int u = 0; u < npro; ++u) issue(u, u);
+    if (npro > 1)
+        wait_vmcnt<2 * LPW>();  // Q and tile 0 landed; tile 1 may be in flight
     else
         wait_vmcnt<0>();
     __syncthreads();
-    read_k(kop, k_lds, 0);
-    int st = 0;  // stage of tile t
-    // Top of iteration t: tile t+1 resident for everyone, tile t-1 consumed;
-    // then tile t+3 is issued into the stage tile t-1 held.
-    auto advance = [&](int t) __attribute__((always_inline)) {
-        if (t > 0) {
-            if (t + 2 < ntiles)
-                wait_vmcnt<2 * LPW>();  // this wave's loads of tile t+1 landed
-            else
-                wait_vmcnt<0>();
-            __syncthreads();
-        }
-        if (t + 3 < ntiles) issue(t + 3, (st + 3) & (NST - 1));
-    };
-    // Unmasked tiles first, then (causal) the wave's diagonal tile and the
-    // tiles past its rows, which it only keeps in step with the barriers.
-    const int t_diag = kCaus ? min(q_lo / BN, ntiles) : ntiles;
-    int t = 0;
-    for (; t < t_diag; ++t) {
-        advance(t);
-        const int st1 = (st + 1) & (NST - 1);
-        tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::false_type{}, t * BN);
-        st = st1;
-    }
-    if constexpr (kCaus) {
-        static_assert(BN == 64 && NQB == 2, "one diagonal tile per wave");
-        for (; t < ntiles; ++t) {
-            advance(t);
-            const int st1 = (st + 1) & (NST - 1);
-            if (t == t_diag) tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::true_type{}, t * BN);
-            st = st1;
-        }
-    }
 
-    // Epilogue: one query per lane.
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
     float* __restrict__ Zp = p.z + (size_t)bh * T;
     const float s2 = sc * sc;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+
+    int u = 0;
+    for (int it = 0; it < nitems; ++it) {
+        const int mb = it ? mb_b : mb_a;
+        const int wr = it ? (NW - 1 - wave) : wave;
+        const int nt = it ? ntot - nt_a : nt_a;
+        if (it > 0 && !early_q) {  // short first item: fetch the second Q block now
+            issue_q(mb_b);
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        const float zl = zacc[qb][0] + zacc[qb][1];
-        const float zt = zl + __shfl_xor(zl, 32);
-        const float rcp = 1.0f / (zt + eps_s);
-        const int qi = qrow0[qb] + c;
-        if (qi < T) {
+        for (int qb = 0; qb < NQB; ++qb) qrow0[qb] = mb * BM + 32 * (NQB * wr + qb);
+        load_q(wr);
+        read_k(kop, k_lds + st * TB, 0);
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int d = db * 32 + 8 * j + 4 * g;
-                    const f32x16& o = oacc[db][qb];
-                    u32x2 w;
-                    w[0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
-                    w[1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
-                    *reinterpret_cast<u32x2*>(O + (size_t)qi * DP + d) = w;
-                }
+            for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
+
+        // Unmasked tiles first, then (causal) the wave's diagonal tile and
+        // the tiles past its rows, which it only keeps in step with the barriers.
+        const int t_diag = kCaus ? min(qrow0[0] / BN, nt) : nt;
+        int t = 0;
+        for (; t < t_diag; ++t, ++u) {
+            advance(u);
+            const int st1 = next_stage(st);
+            tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::false_type{}, t * BN);
+            st = st1;
+        }
+        if constexpr (kCaus) {
+            static_assert(BN == 64 && NQB == 2, "one diagonal tile per wave");
+            for (; t < nt; ++t, ++u) {
+                advance(u);
+                const int st1 = next_stage(st);
+                if (t == t_diag) tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::true_type{}, t * BN);
+                st = st1;
             }
-            if (g == 0) Zp[qi] = s2 * zt + p.eps;
+        }
+
+        // Epilogue: one query per lane.
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float zl = zacc[qb][0] + zacc[qb][1];
+            const float zt = zl + __shfl_xor(zl, 32);
+            const float rcp = 1.0f / (zt + eps_s);
+            const int qi = qrow0[qb] + c;
+            if (qi < T) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int d = db * 32 + 8 * j + 4 * g;
+                        const f32x16& o = oacc[db][qb];
+                        u32x2 w;
+                        w[0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
+                        w[1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
+                        *reinterpret_cast<u32x2*>(O + (size_t)qi * DP + d) = w;
+                    }
+                }
+                if (g == 0) Zp[qi] = s2 * zt + p.eps;
+            }
         }
     }
 }
@@ -367,8 +419,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 template <class E, int DP, int MODE>
 hipError_t launch_fwd16_fast(const FwdArgs& a, hipStream_t st) {
     using C = FastFwdCfg<DP>;
-    const int nmb = (a.T + C::BM - 1) / C::BM;
-    const dim3 grid((unsigned)nmb * (unsigned)(a.B * a.H));
+    const dim3 grid((unsigned)fast_fwd_npair(a.T, C::BM) * (unsigned)(a.B * a.H));
     hipLaunchKernelGGL((born_fwd16_fast_kernel<E, DP, MODE>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }

@@ -78,6 +78,16 @@ def test_fwd_ragged_lengths(cuda_device, T, dtype):
     _check_fwd(2, 3, T, 64, dtype, cuda_device, seed=T)
 
 
+@pytest.mark.parametrize("T", [300, 513, 600, 777, 1100])
+@pytest.mark.parametrize("is_causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale", [8.0, -3.0])
+def test_fwd_d64_block_pairs(cuda_device, T, is_causal, dtype, scale):
+    """D = 64 without masks pairs 256-row query blocks mb and nmb-1-mb in one
+    workgroup: even and odd block counts, ragged last blocks, both scale signs."""
+    _check_fwd(1, 2, T, 64, dtype, cuda_device, scale=scale, is_causal=is_causal, seed=T)
+
+
 @pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 80, 96, 112, 128, 160, 192, 256, 20, 3])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_fwd_head_dims(cuda_device, D, dtype):
