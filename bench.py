@@ -54,7 +54,42 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", action="store_true", help="short run for rocprofv3 (no CPU leg)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (calibrates FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+COPY_BYTES = 512 << 20  # bytes read (and written) per calibration copy
+
+
+def copy_calibration(steps):
+    """A plain device-to-device copy of COPY_BYTES, `steps` times: under
+    rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch, divided into
+    the known size, gives the scale factor applied to the kernel's counters."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "steps": steps}), flush=True)
+
+
+def load_traffic(config):
+    """HBM bytes per forward launch measured by rocprofv3 --pmc for `config`,
+    from profiles/traffic_<config>.txt (line `traffic_bytes_per_launch = N`),
+    or None when no such measurement is committed."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch"):
+                    return int(float(line.split("=", 1)[1]))
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 def make_inputs(cfg, seed, device, dtype):
@@ -165,6 +200,10 @@ def main():
         )
         sys.exit(2)
 
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
+
     import torch
 
     from quantumdlblocks_amd import _native
@@ -258,7 +297,7 @@ def main():
     else:
         roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4)}
-    roof["traffic"] = None
+    roof["traffic"] = None if backward else load_traffic(args.config)
 
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
