@@ -138,6 +138,13 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
+    // c = min(|s|, 1) (see E::kScaleInSquare); the epilogue divides c back out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    auto pre = [&](float x) __attribute__((always_inline)) {
+        if constexpr (E::kScaleInSquare) return x * sq_pre;
+        else return x;
+    };
 
     u32x4 qr[NQB][KS], dr[NQB][KS];
     float zinv[NQB], nd[NQB];
@@ -249,9 +256,9 @@ void born_bwd_dq16_kernel(BwdArgs p) {
                 for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const float u0 = fmaxf(s[qb][2 * j], 0.f) * fmaf(tt[qb][2 * j], zinv[qb], nd[qb]);
+                        const float u0 = fmaxf(pre(s[qb][2 * j]), 0.f) * fmaf(tt[qb][2 * j], zinv[qb], nd[qb]);
                         const float u1 =
-                            fmaxf(s[qb][2 * j + 1], 0.f) * fmaf(tt[qb][2 * j + 1], zinv[qb], nd[qb]);
+                            fmaxf(pre(s[qb][2 * j + 1]), 0.f) * fmaf(tt[qb][2 * j + 1], zinv[qb], nd[qb]);
                         pk[qb][j] = E::pack(u0, u1);
                     }
                 }
@@ -279,7 +286,7 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     }
 
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = 2.f * sc * fabsf(sc);
+    const float f = 2.f * sc * fabsf(sc) / sq_pre;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const int qi = q0 + qb * 32 + c;
@@ -361,6 +368,13 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
+    // c = min(|s|, 1) (see E::kScaleInSquare); the epilogue divides c back out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    auto pre = [&](float x) __attribute__((always_inline)) {
+        if constexpr (E::kScaleInSquare) return x * sq_pre;
+        else return x;
+    };
 
     u32x4 kr[KS], vr[KS];
 #pragma unroll
@@ -473,7 +487,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
                 uint32_t w2[8], u2[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float a0 = fmaxf(s[2 * j], 0.f), a1 = fmaxf(s[2 * j + 1], 0.f);
+                    const float a0 = fmaxf(pre(s[2 * j]), 0.f), a1 = fmaxf(pre(s[2 * j + 1]), 0.f);
                     const float t0 = a0 * zi[2 * j], t1 = a1 * zi[2 * j + 1];
                     w2[j] = E::pack(t0 * a0, t1 * a1);
                     u2[j] = E::pack(t0 * dp[2 * j], t1 * dp[2 * j + 1]);
@@ -504,8 +518,8 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     if (key < T) {
         uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
         uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
-        const float fk = 2.f * sc * fabsf(sc);
-        const float fv = sc * sc;
+        const float fk = 2.f * sc * fabsf(sc) / sq_pre;
+        const float fv = (sc / sq_pre) * (sc / sq_pre);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll

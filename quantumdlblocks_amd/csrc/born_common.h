@@ -47,8 +47,16 @@ __device__ __forceinline__ uint32_t relu_pk16(uint32_t u) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(x, zero));
 }
 
+// Where the scale enters the 16-bit weights.  bf16 keeps fp32's exponent
+// range, so the scale is folded out of the tile loop (p' = r|r| from the
+// unscaled overlap r, p = s^2 p', restored once per row in the epilogue).
+// fp16 saturates at 65504: it squares c r with c = min(|s|, 1) before the
+// cast (p = (s/c)^2 p').  For |s| < 1 that is the reference's own (s r)^2
+// (flash_born.py:180-183); for |s| >= 1 it is r^2 <= (s r)^2.  Either way a
+// weight overflows only where the reference's overflows too.
 struct BF16 {
     static constexpr int kDtype = 2;
+    static constexpr bool kScaleInSquare = false;
     __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -70,6 +78,7 @@ struct BF16 {
 
 struct F16 {
     static constexpr int kDtype = 1;
+    static constexpr bool kScaleInSquare = true;
     __device__ __forceinline__ static f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);

@@ -83,7 +83,10 @@ void born_fwd16_kernel(FwdArgs p) {
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    // fp16: square min(|s|, 1) r, so no weight overflows unless the
+    // reference's (s r)^2 does too; p = s2 * (accumulated weight).
+    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
 
     // Q^T operand, resident for the whole kernel.
     u32x4 qr[NQB][KS];
@@ -215,7 +218,8 @@ void born_fwd16_kernel(FwdArgs p) {
             for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                    float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
                     uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
                     u = relu_pk16(u);
                     zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
@@ -271,7 +275,7 @@ void born_fwd16_kernel(FwdArgs p) {
     // Epilogue: one query per lane.
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
     float* __restrict__ Zp = p.z + (size_t)bh * T;
-    const float s2 = sc * sc;
+    const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {

@@ -110,6 +110,15 @@ def test_bwd_c1_shape(cuda_device, dtype, is_causal):
     _check_bwd(1, 4, 256, 64, dtype, cuda_device, is_causal=is_causal)
 
 
+@pytest.mark.parametrize("D, window", [(64, 0), (64, 100), (32, 0)])
+@pytest.mark.parametrize("scale", [0.05, -0.3, 8.0])
+def test_bwd_f16_operand_range(cuda_device, D, window, scale):
+    """fp16 dot operands (p/Z and dS) stay in range for small scales with large
+    overlaps, as the reference's do (the kernel scales the overlap by min(|s|, 1))."""
+    std = 4.0 if abs(scale) < 1 else 0.5
+    _check_bwd(1, 2, 300, D, torch.float16, cuda_device, scale=scale, std=std, window_size=window, seed=3)
+
+
 @pytest.mark.parametrize("T", [1, 5, 33, 64, 100, 257])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_bwd_ragged_lengths(cuda_device, T, dtype):

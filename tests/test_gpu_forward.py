@@ -88,6 +88,17 @@ def test_fwd_d64_block_pairs(cuda_device, T, is_causal, dtype, scale):
     _check_fwd(1, 2, T, 64, dtype, cuda_device, scale=scale, is_causal=is_causal, seed=T)
 
 
+@pytest.mark.parametrize("D, window", [(64, 0), (64, 100), (32, 0)])
+@pytest.mark.parametrize("scale", [0.05, -0.3, 8.0])
+def test_fwd_f16_weight_range(cuda_device, D, window, scale):
+    """fp16 weights saturate at 65504.  With |q.k| up to ~600 a small scale
+    keeps the reference's (s q.k)^2 in range, and so must the kernel (fp16
+    squares min(|s|, 1) q.k); with scale 8 the kernel's weights stay in range
+    too (r^2 <= (s r)^2)."""
+    std = 4.0 if abs(scale) < 1 else 0.5
+    _check_fwd(1, 2, 300, D, torch.float16, cuda_device, scale=scale, std=std, window_size=window, seed=3)
+
+
 @pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 80, 96, 112, 128, 160, 192, 256, 20, 3])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_fwd_head_dims(cuda_device, D, dtype):
