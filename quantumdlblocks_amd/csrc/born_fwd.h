@@ -54,6 +54,17 @@ void born_fwd16_kernel(FwdArgs p) {
     __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BN * KSTR];
     __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][BN * VSTR];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
+    // Document-aware tile list (doc_ids given): candidate key tiles are
+    // screened CAP at a time; a tile is kept when its [min, max] document id
+    // range meets the workgroup's query range.  Exact skipping for sorted ids
+    // (compute_document_ids output), conservative for any others.
+    constexpr int CAP = kDoc ? 256 : 1;
+    __shared__ int32_t t_keep[CAP];
+    __shared__ int32_t t_list[CAP];
+    __shared__ int2 t_rng[CAP];
+    __shared__ int2 t_rng_c[CAP];
+    __shared__ int32_t s_qrng[2 * NW];
+    __shared__ int32_t s_count;
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -108,6 +119,32 @@ void born_fwd16_kernel(FwdArgs p) {
     for (int qb = 0; qb < NQB; ++qb) {
         const int row = q0 + qb * 32 + c;
         qdoc[qb] = (has_doc && row < T) ? docb[row] : -1;
+    }
+    // Document-id range of this wave's valid query rows, and of the workgroup's.
+    int wq_lo = INT_MAX, wq_hi = INT_MIN, bq_lo = INT_MAX, bq_hi = INT_MIN;
+    if (kDoc && has_doc) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            if (q0 + qb * 32 + c < T) {
+                wq_lo = min(wq_lo, qdoc[qb]);
+                wq_hi = max(wq_hi, qdoc[qb]);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            wq_lo = min(wq_lo, __shfl_xor(wq_lo, off));
+            wq_hi = max(wq_hi, __shfl_xor(wq_hi, off));
+        }
+        if (lane == 0) {
+            s_qrng[2 * wave] = wq_lo;
+            s_qrng[2 * wave + 1] = wq_hi;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_qrng[2 * w]);
+            bq_hi = max(bq_hi, s_qrng[2 * w + 1]);
+        }
     }
 
     // Key range of this workgroup (flash_born.py:152-154).
@@ -169,10 +206,14 @@ void born_fwd16_kernel(FwdArgs p) {
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
 
-    auto compute = [&](int buf, int key0) {
+    auto compute = [&](int buf, int key0, int2 drng) {
         // Which of this wave's (query, key) pairs can be visible in the tile.
         bool active = q0 < T;
-        bool need_mask = has_doc;
+        if (kDoc && has_doc) active = active && drng.y >= wq_lo && drng.x <= wq_hi;
+        // The document test is needed unless the tile's keys and the wave's
+        // queries all belong to one and the same document.
+        const bool doc_mask = kDoc && has_doc && !(drng.x == drng.y && wq_lo == wq_hi && drng.x == wq_lo);
+        bool need_mask = doc_mask;
         if (causal) {
             active = active && (key0 <= q0 + QW - 1);
             need_mask = need_mask || (key0 + BN - 1 > q0);
@@ -196,19 +237,30 @@ void born_fwd16_kernel(FwdArgs p) {
             }
             if (need_mask) {
                 const int kbase = key0 + nb * 32 + 4 * g;
+                // Document ids of this lane's 16 keys: 4 runs of 4 consecutive keys.
+                int kd[16];
+                if (kDoc && doc_mask) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int4 x = *reinterpret_cast<const int4*>(&doc_lds[buf][nb * 32 + 4 * g + 8 * j]);
+                        kd[4 * j] = x.x;
+                        kd[4 * j + 1] = x.y;
+                        kd[4 * j + 2] = x.z;
+                        kd[4 * j + 3] = x.w;
+                    }
+                }
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     // key = kbase + off(r); visible iff off(r) <= qi - kbase
                     // (causal) and off(r) > qi - kbase - window.
                     const int lim = q0 + qb * 32 + c - kbase;
+                    const int hi = causal ? lim : INT_MAX;
+                    const int lo = window > 0 ? lim - window : INT_MIN;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int off = 8 * (r >> 2) + (r & 3);
-                        bool vis = true;
-                        if (causal) vis = vis && (off <= lim);
-                        if (window > 0) vis = vis && (off > lim - window);
-                        if (kDoc && has_doc)
-                            vis = vis && (doc_lds[buf][kbase - key0 + off] == qdoc[qb]);
+                        bool vis = (off <= hi) && (off > lo);
+                        if (kDoc && doc_mask) vis = vis && (kd[r] == qdoc[qb]);
                         if (!vis) s[qb][r] = 0.f;
                     }
                 }
@@ -219,7 +271,7 @@ void born_fwd16_kernel(FwdArgs p) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
-                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                    if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
                     uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
                     u = relu_pk16(u);
                     zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
@@ -250,26 +302,83 @@ void born_fwd16_kernel(FwdArgs p) {
         }
     };
 
+    // Screen candidate tiles c0 .. c0+nc-1 (document ids given): one tile per
+    // thread, its ids read as 16-byte vectors when aligned (all loads of a
+    // thread independent, so a screening pass costs about one memory
+    // latency); then wave 0 compacts the kept tiles into t_list.
+    static_assert(!kDoc || CAP == NT, "one candidate tile per thread");
+    const bool doc_vec = kDoc && has_doc && ((reinterpret_cast<uintptr_t>(docb) & 15) == 0);
+    auto screen = [&](int c0, int nc) -> int {
+        if (tid < nc) {
+            const int key0 = kv_lo + (c0 + tid) * BN;
+            const int kend = min(key0 + BN, T);
+            int lo = INT_MAX, hi = INT_MIN;
+            if (doc_vec && kend - key0 == BN) {
+#pragma unroll 8
+                for (int j = 0; j < BN / 4; ++j) {
+                    const int4 x = *reinterpret_cast<const int4*>(docb + key0 + 4 * j);
+                    lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
+                    hi = max(hi, max(max(x.x, x.y), max(x.z, x.w)));
+                }
+            } else {
+                for (int key = key0; key < kend; ++key) {
+                    const int d = docb[key];
+                    lo = min(lo, d);
+                    hi = max(hi, d);
+                }
+            }
+            t_rng[tid] = make_int2(lo, hi);
+            t_keep[tid] = (hi >= bq_lo && lo <= bq_hi) ? 1 : 0;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            int count = 0;
+            for (int base0 = 0; base0 < nc; base0 += 64) {
+                const int i = base0 + lane;
+                const bool keep = i < nc && t_keep[i] != 0;
+                const uint64_t m = __ballot(keep);
+                const int pos = count + (int)__builtin_amdgcn_mbcnt_hi(
+                                            (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                if (keep) {
+                    t_list[pos] = c0 + i;
+                    t_rng_c[pos] = t_rng[i];
+                }
+                count += __popcll(m);
+            }
+            if (lane == 0) s_count = count;
+        }
+        __syncthreads();
+        return s_count;
+    };
+    const bool listed = kDoc && has_doc;
+    auto tile_key = [&](int t) -> int { return kv_lo + (listed ? t_list[t] : t) * BN; };
+    auto tile_rng = [&](int t) -> int2 { return listed ? t_rng_c[t] : make_int2(0, 0); };
+
     // Software pipeline, prefetch distance 2: while tile t is consumed from
     // LDS buffer t%2, register set (t+1)%2 holds tile t+1 and tile t+2 is in
     // flight into the other set; each load has two tiles of compute to land.
-    Regs ra, rb;
-    if (ntiles > 0) {
-        load_tile(ra, kv_lo);
-        store_tile(ra, 0);
-    }
-    if (ntiles > 1) load_tile(rb, kv_lo + BN);
-    __syncthreads();
-    for (int t = 0; t < ntiles; t += 2) {
-        if (t + 2 < ntiles) load_tile(ra, kv_lo + (t + 2) * BN);
-        compute(0, kv_lo + t * BN);
-        if (t + 1 < ntiles) store_tile(rb, 1);
+    // With a tile list the pipeline runs once per screened chunk.
+    const int chunk = listed ? CAP : max(ntiles, 1);
+    for (int c0 = 0; c0 < ntiles; c0 += chunk) {
+        const int n = listed ? screen(c0, min(CAP, ntiles - c0)) : ntiles;
+        Regs ra, rb;
+        if (n > 0) {
+            load_tile(ra, tile_key(0));
+            store_tile(ra, 0);
+        }
+        if (n > 1) load_tile(rb, tile_key(1));
         __syncthreads();
-        if (t + 1 >= ntiles) break;
-        if (t + 3 < ntiles) load_tile(rb, kv_lo + (t + 3) * BN);
-        compute(1, kv_lo + (t + 1) * BN);
-        if (t + 2 < ntiles) store_tile(ra, 0);
-        __syncthreads();
+        for (int t = 0; t < n; t += 2) {
+            if (t + 2 < n) load_tile(ra, tile_key(t + 2));
+            compute(0, tile_key(t), tile_rng(t));
+            if (t + 1 < n) store_tile(rb, 1);
+            __syncthreads();
+            if (t + 1 >= n) break;
+            if (t + 3 < n) load_tile(rb, tile_key(t + 3));
+            compute(1, tile_key(t + 1), tile_rng(t + 1));
+            if (t + 2 < n) store_tile(ra, 0);
+            __syncthreads();
+        }
     }
 
     // Epilogue: one query per lane.

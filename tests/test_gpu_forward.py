@@ -120,6 +120,41 @@ def test_fwd_document_mask(cuda_device, dtype, is_causal):
     _check_fwd(3, 2, 300, 64, dtype, cuda_device, is_causal=is_causal, doc=doc)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_unsorted_document_ids(cuda_device, dtype, D, is_causal):
+    """Arbitrary (unsorted, repeating) document ids: the kernels' tile
+    screening by document-id range must stay conservative."""
+    rng = np.random.default_rng(D)
+    doc = rng.integers(0, 4, size=(2, 700)).astype(np.int32)
+    doc[1, 350:] = rng.integers(10, 12, size=350)
+    _check_fwd(2, 2, 700, D, dtype, cuda_device, is_causal=is_causal, doc=doc, seed=D)
+
+
+@pytest.mark.parametrize("T, D", [(20000, 64), (9000, 256)])
+def test_fwd_documents_many_tiles(cuda_device, T, D):
+    """Sorted documents over more candidate key tiles than one screening pass
+    holds (256 tiles): every document, checked against the oracle on its own
+    span (documents do not see each other, so the span is exact)."""
+    from quantumdlblocks_amd import flash_born_attention
+
+    doc = orc.geometric_doc_ids(1, T, 300.0, seed=T)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((1, 2, T, D), seed=7, std=0.5, dtype=torch.bfloat16))
+    out = flash_born_attention(q, k, v, 8.0, doc_ids=torch.as_tensor(doc, device=cuda_device))
+    got = f64(out)
+    qn, kn, vn = f64(q), f64(k), f64(v)
+    ids = doc[0]
+    starts = np.flatnonzero(np.r_[True, ids[1:] != ids[:-1]])
+    ends = np.r_[starts[1:], T]
+    worst = 0.0
+    for s, e in zip(starts, ends):
+        ref, _ = orc.forward(qn[:, :, s:e], kn[:, :, s:e], vn[:, :, s:e], 8.0, True, 1e-12)
+        worst = max(worst, rel_err(got[:, :, s:e], ref))
+    print(f"documents T={T} D={D}: {len(starts)} docs, worst rel={worst:.3e}", flush=True)
+    assert worst <= 2e-2
+
+
 def test_fwd_document_and_window(cuda_device):
     doc = orc.geometric_doc_ids(2, 333, 60.0, seed=2)
     _check_fwd(2, 4, 333, 64, torch.bfloat16, cuda_device, window_size=37, doc=doc)
