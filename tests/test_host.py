@@ -184,3 +184,40 @@ def test_mi355x_launch_meta():
     assert m["BLOCK_M"] == 256 and m["BLOCK_N"] == 64 and m["padded_head_dim"] == 64
     assert get_mi355x_launch_meta(200, torch.float16)["padded_head_dim"] == 224
     assert get_mi355x_launch_meta(64, torch.float32)["mfma"] == "32x32x2f32"
+
+
+def test_integration_install_rebinds_reference_names():
+    """quantumdlblocks_amd.integration.install() rebinds the names the
+    reference's layers bind at import (attention.py:20) and registers the
+    documented module path qdlblocks.kernels.flash_born_triton."""
+    import sys
+    import types
+
+    from quantumdlblocks_amd import flash_born_attention, integration
+    from quantumdlblocks_amd.kernels import flash_born_triton
+
+    names = ["qdlblocks", "qdlblocks.kernels", "qdlblocks.kernels.flash_born", "qdlblocks.layers",
+             "qdlblocks.layers.attention", "qdlblocks.kernels.flash_born_triton"]
+    saved = {n: sys.modules.get(n) for n in names}
+    try:
+        fake = {n: types.ModuleType(n) for n in names[:-1]}
+        sentinel = object()
+        for n in ("qdlblocks", "qdlblocks.kernels", "qdlblocks.layers.attention"):
+            fake[n].flash_born_attention = sentinel
+        fake["qdlblocks.kernels"].HAS_TRITON = False
+        sys.modules.update(fake)
+        patched = integration.install(import_targets=False)
+        assert set(patched) == {"qdlblocks", "qdlblocks.kernels", "qdlblocks.kernels.flash_born",
+                                "qdlblocks.layers.attention"}
+        for n in ("qdlblocks", "qdlblocks.kernels", "qdlblocks.layers.attention", "qdlblocks.kernels.flash_born"):
+            assert sys.modules[n].flash_born_attention is flash_born_attention
+        assert sys.modules["qdlblocks.kernels"].HAS_TRITON is flash_born_triton.HAS_TRITON
+        assert sys.modules["qdlblocks.kernels.flash_born_triton"] is flash_born_triton
+        assert sys.modules["qdlblocks.kernels"].flash_born_triton is flash_born_triton
+        assert not hasattr(sys.modules["qdlblocks.layers.attention"], "get_rdna4_autotune_configs")
+    finally:
+        for n, m in saved.items():
+            if m is None:
+                sys.modules.pop(n, None)
+            else:
+                sys.modules[n] = m
