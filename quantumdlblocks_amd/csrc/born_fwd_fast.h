@@ -18,20 +18,30 @@
 //     length for every pair, so all workgroups carry equal work, and the
 //     second block's Q and first K/V tiles are loaded while the first block
 //     finishes: there is one load burst per workgroup instead of one per
-//     query block.  On the second block the wave -> rows map is mirrored, so
-//     each wave's visible-key count, summed over both blocks, is the same.
+//     query block.
 //   * K/V tiles of both blocks form one sequence through a ring of three LDS
-//     stages: tile u+2 is issued when tile u starts and tile u+1 is waited
-//     for one tile ahead.  One barrier per tile.
+//     stages: tile u+2 is issued right after the barrier that starts tile u,
+//     and tile u is waited for only at that barrier, so every load has two
+//     tiles of compute to land.  One barrier per tile.
+//   * A finished block's rows are normalised, packed to 16 bits, staged in
+//     the wave's own rows of the Q buffer and written back 16 bytes per lane
+//     (8 whole rows per store instruction), right after a barrier, so they
+//     have a full tile of compute to drain before the next wait.
 //   * Per tile the wave runs QK(keys 0-31), then QK(keys 32-63) interleaved
 //     with the first half's elementwise pass, then PV(first half) interleaved
 //     with the second half's elementwise pass, then PV(second half); the
 //     interleave is pinned with sched_group_barrier so MFMA and VALU co-issue.
-//     Every phase's LDS operands are read one phase earlier (the next tile's
-//     first K operands during the last PV), so no MFMA waits on an LDS read.
-//   * Each wave owns 64 consecutive query rows of a block; under causality a
-//     wave skips the tiles past its last row and masks exactly one diagonal
-//     tile (the same code path, instantiated with the causal mask).
+//     Every phase's LDS operands are read one phase earlier (the tile's first
+//     K operands right after its barrier).
+//   * Rows are dealt to waves so that every wave has work in every tile: the
+//     256-row block is four 64-row slices, and wave w owns rows 16w..16w+15 of
+//     each slice.  Its MFMA column block 0 holds slices 0 and 1, block 1
+//     slices 2 and 3 (column c -> slice 2 qb + c / 16, row 16 w + c % 16).
+//     Under causality the block's four diagonal tiles then cost every wave
+//     2, 2, 1 and 1 column blocks (block 0 is fully masked past diagonal tile
+//     1), instead of one wave carrying all four tiles while the others wait
+//     at the barrier.  Diagonal tiles apply the per-element causal mask to
+//     the column blocks they cut.
 #pragma once
 
 #include <type_traits>
@@ -178,7 +188,10 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         }
     };
 
-    int qrow0[NQB];  // first query row of block qb of this wave (current item)
+    static_assert(NQB == 2 && BM == 4 * BN && BN == 64, "two column blocks over four 64-row slices");
+    // Row of MFMA column c within a block: slice 2 qb + c / 16, row 16 w + c % 16.
+    const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
+    int qrow[NQB];  // query row of this lane's column in block qb (current item)
     u32x4 qr[NQB][KS];
     f32x16 oacc[DB][NQB];
     float zacc[NQB][2];
@@ -207,14 +220,24 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         return a;
     };
 
+    // Column-block modes of a tile, passed as integral constants:
+    // kSkip (no visible key: no MFMA, no VALU), kFull, kMasked (causal
+    // mask applied per element).
+    constexpr int kSkip = 0, kFull = 1, kMasked = 2;
+    using Skip = std::integral_constant<int, kSkip>;
+    using Full = std::integral_constant<int, kFull>;
+    using Masked = std::integral_constant<int, kMasked>;
+
     // Elementwise pass over one 32-key block of S^T: p' = relu(x|x|) packed,
-    // z += p'.  Masked keys (causal) are zeroed first when `lim` says so.
-    auto elementwise = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8], auto masked_c, int kbase)
+    // z += p'.  Masked keys (key > query row) are zeroed first.
+    auto elementwise = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8], auto m0, auto m1, int kbase)
         __attribute__((always_inline)) {
+        constexpr int M[NQB] = {decltype(m0)::value, decltype(m1)::value};
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
-            if constexpr (decltype(masked_c)::value) {
-                const int lim = qrow0[qb] + c - kbase;
+            if (M[qb] == kSkip) continue;
+            if (M[qb] == kMasked) {
+                const int lim = qrow[qb] - kbase;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = 0.f;
@@ -235,8 +258,9 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     //   1: S0 = QK(keys 0-31, operands kop)         reads K(keys 32-63) -> kop1
     //   2: S1 = QK(kop1) | elementwise(S0) -> P0    reads V(keys 0-31)  -> vop0
     //   3: O += PV(vop0, P0) | elementwise(S1) -> P1 reads V(keys 32-63) -> vop1
-    //   4: O += PV(vop1, P1)                         reads next tile's K(keys 0-31) -> kop
-    // `msk` applies the causal mask (the wave's diagonal tile).
+    //   4: O += PV(vop1, P1)
+    // kop (K of keys 0-31) is read after the tile's barrier, so a tile only
+    // has to be resident from its own step on.
     static_assert(NB == 2, "two 32-key halves per tile");
     u32x4 kop[KS];
     auto read_k = [&](u32x4 (&dst)[KS], const uint8_t* kb, int nb) __attribute__((always_inline)) {
@@ -249,40 +273,51 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 #pragma unroll
             for (int db = 0; db < DB; ++db) dst[hh][db] = v_operand(vb, nb, hh, db);
     };
-    auto qk_op = [&](const u32x4 (&ops)[KS], f32x16 (&s)[NQB]) __attribute__((always_inline)) {
+    auto qk_op = [&](const u32x4 (&ops)[KS], f32x16 (&s)[NQB], auto m0, auto m1) __attribute__((always_inline)) {
+        constexpr int M[NQB] = {decltype(m0)::value, decltype(m1)::value};
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
+        for (int qb = 0; qb < NQB; ++qb)
+            if (M[qb] != kSkip) s[qb] = zero16();
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(ops[ks], qr[qb][ks], s[qb]);
+            for (int qb = 0; qb < NQB; ++qb)
+                if (M[qb] != kSkip) s[qb] = E::mfma(ops[ks], qr[qb][ks], s[qb]);
     };
-    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8]) __attribute__((always_inline)) {
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8], auto m0, auto m1)
+        __attribute__((always_inline)) {
+        constexpr int M[NQB] = {decltype(m0)::value, decltype(m1)::value};
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
+                    if (M[qb] == kSkip) continue;
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
                     oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
                 }
     };
-    auto tile = [&](const uint8_t* kb, const uint8_t* vb, const uint8_t* kb_next, auto msk, int key0)
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, auto m0, auto m1)
         __attribute__((always_inline)) {
+        constexpr int NA = (decltype(m0)::value != kSkip) + (decltype(m1)::value != kSkip);
         f32x16 s0[NQB], s1[NQB];
         uint32_t pk0[NQB][8], pk1[NQB][8];
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
-        // 1
+        // 1 (MFMA only: issued at raised wave priority, so the two
+        // workgroups sharing a SIMD hand the matrix pipe back and forth
+        // instead of the older one running ahead)
+        __builtin_amdgcn_s_setprio(1);
         read_k(kop1, kb, 1);
-        qk_op(kop, s0);
+        qk_op(kop, s0, m0, m1);
         __builtin_amdgcn_sched_barrier(0);
         // 2
+        __builtin_amdgcn_s_setprio(0);
         read_v(vop0, vb, 0);
-        qk_op(kop1, s1);
-        elementwise(s0, pk0, msk, key0 + 4 * g);
+        qk_op(kop1, s1, m0, m1);
+        elementwise(s0, pk0, m0, m1, key0 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < KS * NQB; ++i) {
+        for (int i = 0; i < KS * NA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
@@ -290,134 +325,195 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         __builtin_amdgcn_sched_barrier(0);
         // 3
         read_v(vop1, vb, 1);
-        pv_op(vop0, pk0);
-        elementwise(s1, pk1, msk, key0 + 32 + 4 * g);
+        pv_op(vop0, pk0, m0, m1);
+        elementwise(s1, pk1, m0, m1, key0 + 32 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 2 * DB * NQB; ++i) {
+        for (int i = 0; i < 2 * DB * NA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x002, 10, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
         }
         __builtin_amdgcn_sched_barrier(0);
-        // 4
-        read_k(kop, kb_next, 0);
-        pv_op(vop1, pk1);
+        // 4 (MFMA only)
+        __builtin_amdgcn_s_setprio(1);
+        pv_op(vop1, pk1, m0, m1);
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
     };
 
-    // Rows 64 wr .. 64 wr + 63 of the Q block in LDS -> B operands of S^T.
-    // The sign of the scale is folded into Q; the asm pins the result in
-    // registers so it is not recomputed inside the tile loop.
-    auto load_q = [&](int wr) __attribute__((always_inline)) {
+    // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
+    // of the scale is folded into Q; the asm pins the result in registers so
+    // it is not recomputed inside the tile loop.
+    auto load_q = [&]() __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const int row = 32 * (NQB * wr + qb) + c;
-                const int pc = (2 * ks + g) ^ (row & 7);
+                const int row = 128 * qb + lr;
+                const int pc = (2 * ks + (ln >> 5)) ^ (row & 7);
                 qr[qb][ks] = *reinterpret_cast<const u32x4*>(q_lds + row * RB + pc * 16) ^ flip;
                 asm volatile("" : "+v"(qr[qb][ks]));
             }
     };
-
-    // Top of iteration u: tile u+1 resident for everyone and tile u-1
-    // consumed; tile u+2 is then issued into the stage tile u-1 held.  The
-    // second item's Q block is issued at the top of iteration 1 (every wave
-    // has read the first item's Q by then) ahead of tile 3, so the full drain
-    // at the top of iteration 2 covers it.
-    const bool early_q = (nitems == 2) && (nt_a >= 3);
-    int st = 0;         // stage of tile u
-    int sti = NST - 1;  // stage of tile u + NST - 1
-    auto advance = [&](int u) __attribute__((always_inline)) {
-        if (u > 0) {
-            wait_vmcnt<0>();
-            __syncthreads();
-        }
-        if (u == 1 && early_q) issue_q(mb_b);
-        if (u + NST - 1 < ntot) issue(u + NST - 1, sti);
-        sti = (sti + 1 == NST) ? 0 : sti + 1;
-    };
-    auto next_stage = [](int s) { return (s + 1 == NST) ? 0 : s + 1; };
-
-    issue_q(mb_a);
-    const int npro = min(NST - 1, ntot);
-    for (int u = 0; u < npro; ++u) issue(u, u);
-    if (npro > 1)
-        wait_vmcnt<2 * LPW>();  // Q and tile 0 landed; tile 1 may be in flight
-    else
-        wait_vmcnt<0>();
-    __syncthreads();
 
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
     float* __restrict__ Zp = p.z + (size_t)bh * T;
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
 
-    int u = 0;
-    for (int it = 0; it < nitems; ++it) {
-        const int mb = it ? mb_b : mb_a;
-        const int wr = it ? (NW - 1 - wave) : wave;
-        const int nt = it ? ntot - nt_a : nt_a;
-        if (it > 0 && !early_q) {  // short first item: fetch the second Q block now
-            issue_q(mb_b);
-            wait_vmcnt<0>();
-            __syncthreads();
-        }
+    // Normalise and store the finished item's rows, in two parts so the
+    // next item's Q can be read in between: pack() normalises the
+    // accumulators into 16-bit pairs (the accumulators die there); put()
+    // writes the packed rows into this wave's own rows of the Q block in LDS
+    // (their Q is already in registers) and reads them back 16 bytes per lane,
+    // so each store instruction writes 8 whole rows (1 KiB contiguous).
+    u32x2 opk[NQB][DB][4];
+    float ztot[NQB];
+    auto pack = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) qrow0[qb] = mb * BM + 32 * (NQB * wr + qb);
-        load_q(wr);
-        read_k(kop, k_lds + st * TB, 0);
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float zl = zacc[qb][0] + zacc[qb][1];
+            ztot[qb] = zl + __shfl_xor(zl, 32);
+            const float rcp = 1.0f / (ztot[qb] + eps_s);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x16& o = oacc[db][qb];
+                    opk[qb][db][j][0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
+                    opk[qb][db][j][1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
+                }
+        }
+    };
+    auto put = [&](int mb) __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+        const int gg = ln >> 5;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const int row = 128 * qb + lr;
+            uint8_t* rb = q_lds + row * RB;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int chunk = 4 * db + j;
+                    *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 7)) << 4) + 8 * gg) = opk[qb][db][j];
+                }
+            const int qi = mb * BM + row;
+            if (gg == 0 && qi < T) Zp[qi] = s2 * ztot[qb] + p.eps;
+        }
+        const int chunk = ln & 7;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
+            const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 7)) << 4));
+            const int qi = mb * BM + row;
+            if (qi < T) *reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8) = x;
+        }
+    };
+    auto start_item = [&](int mb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) qrow[qb] = mb * BM + 128 * qb + lrow;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
+    };
 
-        // Unmasked tiles first, then (causal) the wave's diagonal tile and
-        // the tiles past its rows, which it only keeps in step with the barriers.
-        const int t_diag = kCaus ? min(qrow0[0] / BN, nt) : nt;
+    // Load pipeline.  Issue order: Q of item 0, tiles 0 and 1 (prologue);
+    // then at the top of step u, after the barrier, tile u+2 (and at u == uq
+    // the second item's Q block, ahead of tile uq+2).  At the top of step u each wave waits until
+    // its share of tile u has landed (everything issued before tile u+1),
+    // then the barrier makes the whole tile visible and frees the stage of
+    // tile u-1.  Loads return in order; the only stores before the last
+    // step are the first item's outputs, issued at the top of its successor's
+    // first step, and the wait one step later drains them.
+    // The second item's Q block is issued at the top of step uq, four steps
+    // before that item starts (away from the start-up burst).  With two
+    // items T > 256, so the first item has at least 5 tiles and 1 <= uq;
+    // every wave read the first item's Q at step 0, and the Q block is
+    // resident from step uq + 2 on.
+    constexpr int kTileLoads = 2 * LPW, kQLoads = LQW;
+    const bool early_q = (nitems == 2);
+    const int uq = max(1, nt_a - 4);
+    auto top = [&](int u) __attribute__((always_inline)) {
+        const bool stores_out = (nitems == 2) && (u == nt_a + 1);
+        const int after = stores_out ? 0 : ((u == uq + 1 && early_q) ? kQLoads : 0) + (u + 1 < ntot ? kTileLoads : 0);
+        if (after >= kQLoads + kTileLoads)
+            wait_vmcnt<kQLoads + kTileLoads>();
+        else if (after >= kTileLoads)
+            wait_vmcnt<kTileLoads>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        if (u == uq && early_q) issue_q(mb_b);
+        if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
+    };
+
+    issue_q(mb_a);
+    issue(0, 0);
+    if (ntot > 1) issue(1, 1);
+
+    int u = 0;
+    for (int it = 0; it < nitems; ++it) {
+        const int mb = it ? mb_b : mb_a;
+        const int nt = it ? ntot - nt_a : nt_a;
+        const int t0 = kCaus ? min(mb * (BM / BN), nt) : nt;
+        // The item's first step: the previous item's rows go out right
+        // after this barrier, a full step before the next wait.
+        top(u);
+        if (it > 0) {
+            pack();
+            load_q();  // before the previous item's rows overwrite this wave's Q rows
+            put(mb_a);
+        } else {
+            load_q();
+        }
+        start_item(mb);
+        bool at_top = true;  // top(u) already done for the current step
+        auto stage = [&](int uu, const uint8_t*& kb, const uint8_t*& vb) __attribute__((always_inline)) {
+            // The stage offset is opaque to the optimiser, so it forms each
+            // operand address from it per tile instead of keeping addresses
+            // for all three stages live in registers.
+            int soff = (uu % NST) * TB;
+            asm volatile("" : "+s"(soff));
+            kb = k_lds + soff;
+            vb = v_lds + soff;
+        };
         int t = 0;
-        for (; t < t_diag; ++t, ++u) {
-            advance(u);
-            const int st1 = next_stage(st);
-            tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::false_type{}, t * BN);
-            st = st1;
+        for (; t < t0; ++t, ++u) {
+            if (!at_top) top(u);
+            at_top = false;
+            const uint8_t *kb, *vb;
+            stage(u, kb, vb);
+            read_k(kop, kb, 0);
+            tile(kb, vb, t * BN, Full{}, Full{});
         }
         if constexpr (kCaus) {
-            static_assert(BN == 64 && NQB == 2, "one diagonal tile per wave");
+            // Diagonal tiles 0 and 1: block 0 cut by the mask, block 1 fully
+            // visible; tiles 2 and 3: block 0 fully masked, block 1 cut.
             for (; t < nt; ++t, ++u) {
-                advance(u);
-                const int st1 = next_stage(st);
-                if (t == t_diag) tile(k_lds + st * TB, v_lds + st * TB, k_lds + st1 * TB, std::true_type{}, t * BN);
-                st = st1;
-            }
-        }
-
-        // Epilogue: one query per lane.
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-            const float zl = zacc[qb][0] + zacc[qb][1];
-            const float zt = zl + __shfl_xor(zl, 32);
-            const float rcp = 1.0f / (zt + eps_s);
-            const int qi = qrow0[qb] + c;
-            if (qi < T) {
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int d = db * 32 + 8 * j + 4 * g;
-                        const f32x16& o = oacc[db][qb];
-                        u32x2 w;
-                        w[0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
-                        w[1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
-                        *reinterpret_cast<u32x2*>(O + (size_t)qi * DP + d) = w;
-                    }
-                }
-                if (g == 0) Zp[qi] = s2 * zt + p.eps;
+                if (!at_top) top(u);
+                at_top = false;
+                const uint8_t *kb, *vb;
+                stage(u, kb, vb);
+                read_k(kop, kb, 0);
+                if (t - t0 < 2)
+                    tile(kb, vb, t * BN, Masked{}, Full{});
+                else
+                    tile(kb, vb, t * BN, Skip{}, Masked{});
             }
         }
     }
+    pack();
+    put(nitems == 2 ? mb_b : mb_a);
 }
 
 template <class E, int DP, int MODE>
