@@ -76,16 +76,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // inline asm so the compiler does not treat it as an LDS store it must wait
 // for before every LDS read; completion is tracked by the explicit vmcnt waits
 // and barriers of the pipeline instead.  m0 is saved and restored.
+template <bool kStream = false>
 __device__ __forceinline__ void dma_load16(i32x4 rsrc, uint32_t lds_base, int voffset) {
     int saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voffset), "s"(lds_base), "s"(rsrc)
-        : "memory");
+    if constexpr (kStream) {  // read once: streaming (non-temporal) cache policy
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %2\n\t"
+            "buffer_load_dwordx4 %1, %3, 0 offen nt lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "v"(voffset), "s"(lds_base), "s"(rsrc)
+            : "memory");
+    } else {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %2\n\t"
+            "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "v"(voffset), "s"(lds_base), "s"(rsrc)
+            : "memory");
+    }
 }
 
 template <int DP>
@@ -183,8 +195,8 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         for (int i = 0; i < LQW; ++i) {
             const int slot = (wave * LQW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            dma_load16(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
-                       (mb * BM + row) * RB + ((pc ^ (row & 7)) << 4));
+            dma_load16<true>(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
+                             (mb * BM + row) * RB + ((pc ^ (row & 7)) << 4));
         }
     };
 
@@ -364,12 +376,15 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
 
-    // Normalise and store the finished item's rows, in two parts so the
-    // next item's Q can be read in between: pack() normalises the
-    // accumulators into 16-bit pairs (the accumulators die there); put()
-    // writes the packed rows into this wave's own rows of the Q block in LDS
-    // (their Q is already in registers) and reads them back 16 bytes per lane,
-    // so each store instruction writes 8 whole rows (1 KiB contiguous).
+    // Normalise and store the finished item's rows, in parts so the next
+    // item's Q can be read in between: pack() normalises the accumulators
+    // into 16-bit pairs (the accumulators die there); put_lds() writes them
+    // into this wave's own rows of the Q block in LDS (their Q is already in
+    // registers); flush() reads them back 16 bytes per lane, so each store
+    // instruction writes 8 whole rows (1 KiB contiguous), and stores the row
+    // sums.  Outputs are stored non-temporal: nothing in this kernel reads
+    // them, and dirty lines left in L2 would have to be written back when it
+    // ends.
     u32x2 opk[NQB][DB][4];
     float ztot[NQB];
     auto pack = [&]() __attribute__((always_inline)) {
@@ -388,7 +403,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
                 }
         }
     };
-    auto put = [&](int mb) __attribute__((always_inline)) {
+    auto put_lds = [&]() __attribute__((always_inline)) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
@@ -404,8 +419,16 @@ void born_fwd16_fast_kernel(FwdArgs p) {
                     const int chunk = 4 * db + j;
                     *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 7)) << 4) + 8 * gg) = opk[qb][db][j];
                 }
-            const int qi = mb * BM + row;
-            if (gg == 0 && qi < T) Zp[qi] = s2 * ztot[qb] + p.eps;
+        }
+    };
+    auto flush = [&](int mb) __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const int qi = mb * BM + 128 * qb + lr;
+            if ((ln >> 5) == 0 && qi < T) __builtin_nontemporal_store(s2 * ztot[qb] + p.eps, Zp + qi);
         }
         const int chunk = ln & 7;
 #pragma unroll
@@ -413,7 +436,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
             const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
             const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 7)) << 4));
             const int qi = mb * BM + row;
-            if (qi < T) *reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8) = x;
+            if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
         }
     };
     auto start_item = [&](int mb) __attribute__((always_inline)) {
@@ -429,12 +452,14 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 
     // Load pipeline.  Issue order: Q of item 0, tiles 0 and 1 (prologue);
     // then at the top of step u, after the barrier, tile u+2 (and at u == uq
-    // the second item's Q block, ahead of tile uq+2).  At the top of step u each wave waits until
-    // its share of tile u has landed (everything issued before tile u+1),
-    // then the barrier makes the whole tile visible and frees the stage of
-    // tile u-1.  Loads return in order; the only stores before the last
-    // step are the first item's outputs, issued at the top of its successor's
-    // first step, and the wait one step later drains them.
+    // the second item's Q block, ahead of tile uq+2).  At the top of step u
+    // each wave waits until its share of tile u has landed (everything
+    // issued before tile u+1), then the barrier makes the whole tile visible
+    // and frees the stage of tile u-1.  Loads return in order.  The first
+    // item's rows are written to LDS in the second item's first step and
+    // stored at the top of its second step (after that step's loads are
+    // issued); the only stores before the last step, they are drained by
+    // the wait one step later.
     // The second item's Q block is issued at the top of step uq, four steps
     // before that item starts (away from the start-up burst).  With two
     // items T > 256, so the first item has at least 5 tiles and 1 <= uq;
@@ -444,7 +469,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     const bool early_q = (nitems == 2);
     const int uq = max(1, nt_a - 4);
     auto top = [&](int u) __attribute__((always_inline)) {
-        const bool stores_out = (nitems == 2) && (u == nt_a + 1);
+        const bool stores_out = (nitems == 2) && (u == nt_a + 2);
         const int after = stores_out ? 0 : ((u == uq + 1 && early_q) ? kQLoads : 0) + (u + 1 < ntot ? kTileLoads : 0);
         if (after >= kQLoads + kTileLoads)
             wait_vmcnt<kQLoads + kTileLoads>();
@@ -455,6 +480,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         __syncthreads();
         if (u == uq && early_q) issue_q(mb_b);
         if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
+        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
     };
 
     issue_q(mb_a);
@@ -472,7 +498,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         if (it > 0) {
             pack();
             load_q();  // before the previous item's rows overwrite this wave's Q rows
-            put(mb_a);
+            put_lds();
         } else {
             load_q();
         }
@@ -512,8 +538,10 @@ void born_fwd16_fast_kernel(FwdArgs p) {
             }
         }
     }
+    if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
     pack();
-    put(nitems == 2 ? mb_b : mb_a);
+    put_lds();
+    flush(nitems == 2 ? mb_b : mb_a);
 }
 
 template <class E, int DP, int MODE>
