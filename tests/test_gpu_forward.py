@@ -283,3 +283,51 @@ def test_fwd_config_c4(cuda_device):
 def test_fwd_config_c5_forward(cuda_device):
     """C5's forward: bf16 B16 H16 T2048 D64, N(0,1)."""
     _check_fwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=[(0, 0), (15, 15), (9, 3)])
+
+
+@pytest.mark.parametrize("T", [1024, 2048])
+def test_fwd_repeatable_over_stale_lds(cuda_device, T):
+    """Regression: every K/V tile is read only after its own load has landed.
+
+    A launch on decoy K/V (different values, same shape) leaves other data in
+    the LDS of every CU.  A tile read before its load lands would then pick
+    up decoy rows; the error (a few 1e-3 of a bf16 output) can hide inside the
+    2e-2 tolerance, so the check is bitwise: the kernel is deterministic, and
+    the same inputs must give identical O and Z before and after each decoy
+    launch (an earlier version read its second tile's K operands during its
+    first tile and failed this at T=2048).
+    """
+    from quantumdlblocks_amd import _native
+    from quantumdlblocks_amd.kernels.flash_born import _DTYPE_CODE
+
+    lib = _native.load()
+    B, H, D = 16, 16, 64
+    q, k, v = (x.to(cuda_device, torch.bfloat16).contiguous()
+               for x in seeded_inputs((B, H, T, D), seed=T, std=0.125))
+    kd, vd = (x.to(cuda_device, torch.bfloat16).contiguous()
+              for x in seeded_inputs((B, H, T, D), seed=T + 1, std=4.0, n=2))
+    scale = torch.tensor(8.0, dtype=torch.float32, device=cuda_device)
+    stream = torch.cuda.current_stream(cuda_device).cuda_stream
+    code = _DTYPE_CODE[torch.bfloat16]
+
+    def fwd(kk, vv):
+        out = torch.empty_like(q)
+        z = torch.empty((B, H, T), dtype=torch.float32, device=cuda_device)
+        rc = lib.qdl_flash_born_fwd(code, B, H, T, D, q.data_ptr(), kk.data_ptr(), vv.data_ptr(),
+                                    out.data_ptr(), z.data_ptr(), scale.data_ptr(), 1, None, 1, 0,
+                                    1e-12, stream)
+        _native.check(rc, "qdl_flash_born_fwd")
+        return out, z
+
+    out0, z0 = fwd(k, v)
+    for _ in range(5):
+        fwd(kd, vd)
+        out1, z1 = fwd(k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(out1.view(torch.int16), out0.view(torch.int16))
+        assert torch.equal(z1.view(torch.int32), z0.view(torch.int32))
+    heads = [(0, 0), (15, 15), (7, 9)]
+    got = np.concatenate([f64(out0[b : b + 1, h : h + 1]) for b, h in heads])
+    ref = np.concatenate([orc.forward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
+                                      f64(v[b : b + 1, h : h + 1]), 8.0)[0] for b, h in heads])
+    assert rel_err(got, ref) <= 2e-2
