@@ -1,0 +1,430 @@
+// Flash-Born forward with document ids, head dim D == 64: the C4 path
+// (causal or not, no sliding window).
+//
+// Same arithmetic, row layout and four-phase tile as born_fwd16_fast_kernel
+// (born_fwd_fast.h).  What differs is the set of key tiles a query block
+// visits, which depends on the document ids:
+//   * One 256-row query block per workgroup (two workgroups per CU), the
+//     blocks of the longest key ranges launched first.  Q goes straight from
+//     HBM into registers, so LDS holds only the K/V ring (three stages of a
+//     K tile, a V tile and the tile's 64 key document ids) and the tile list.
+//   * Candidate key tiles (up to the block's last row under causality) are
+//     screened 256 at a time, one thread per tile: a tile is kept when the
+//     [min, max] range of its key document ids meets the block's query range
+//     (exact for sorted ids, i.e. compute_document_ids output; conservative,
+//     still correct, for any others).  Wave 0 compacts the kept tiles, with
+//     their single document id (or "mixed"), into a list in LDS.
+//   * The kept tiles go through the same DMA ring and barrier pipeline as the
+//     fast kernel (tiles of step u+2 issued after the barrier that starts
+//     step u); each stage also receives the tile's key document ids.
+//   * Per wave and column block the tile is unmasked when its keys and the
+//     block's 32 rows all belong to one and the same document and it is off
+//     the causal diagonal; otherwise every element is tested (key > row under
+//     causality, or key document != row document).  Column block 0 is fully
+//     masked in diagonal tiles 2 and 3 (computed anyway: a single tile
+//     instantiation keeps the register count within two waves per SIMD).
+//   * A finished block's rows are staged in the (then idle) ring and written
+//     back 16 bytes per lane, 8 whole rows per store instruction.
+#pragma once
+
+#include <climits>
+#include <type_traits>
+
+#include "born_fwd_fast.h"
+
+namespace qdl {
+
+template <class E, int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void born_fwd16_doc_kernel(FwdArgs p) {
+    static_assert(DP == 64, "tuned for D = 64");
+    constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = 256;
+    constexpr int KS = DP / 16;
+    constexpr int DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per tile row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
+    constexpr int CAP = 256;               // candidate tiles screened per pass (one per thread)
+    // Loads per wave per tile: K, V and a 64-byte slice of the key document ids.
+    constexpr int kTileLoads = 2 * LPW + 1;
+    static_assert(TB % (1024 * NW) == 0 && BN == 64 && BM == 4 * BN, "tile split");
+
+    // One buffer: the K/V ring during the tile loop, the output staging
+    // (256 rows x 128 bytes) once the loop is done.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[NST * BN];  // key document ids per stage
+    __shared__ int32_t t_list[CAP];                                   // kept tiles, ascending
+    __shared__ int32_t t_doc[CAP];                                    // their document id or INT_MIN
+    __shared__ int32_t t_keep[CAP];
+    __shared__ int32_t t_tdoc[CAP];
+    __shared__ int32_t s_qrng[2 * NW];
+    __shared__ int32_t s_count;
+    uint8_t* const k_lds = smem;
+    uint8_t* const v_lds = smem + NST * TB;
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const bool causal = p.is_causal != 0;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    const int mb = causal ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int b = bh / p.H, h = bh % p.H;
+    const int R = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+
+    const size_t base = (size_t)bh * T * DP;
+    const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
+    const int32_t* __restrict__ docb = p.doc + (size_t)b * T;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+    const i32x4 rd = buffer_rsrc(docb, (uint32_t)T * 4u);
+
+    // Rows: column c of block qb -> row R + 128 qb + 64 (c / 16) + 16 wave + c % 16.
+    const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
+    int qrow[NQB], qdoc[NQB];
+    u32x4 qr[NQB][KS];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        qrow[qb] = R + 128 * qb + lrow;
+        const bool ok = qrow[qb] < T;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 x = {0u, 0u, 0u, 0u};
+            if (ok) x = ldg16(Qg + (size_t)qrow[qb] * DP + (2 * ks + g) * 8);
+            qr[qb][ks] = x ^ flip;
+        }
+        qdoc[qb] = ok ? docb[qrow[qb]] : INT_MIN;
+    }
+    // Document range of each column block's valid rows (uniform per wave):
+    // qsd[qb] is the one document of all 32 rows, or INT_MIN + 1 when they
+    // span several (never equal to a tile's document id, or to "mixed").
+    int qsd[NQB];
+    int wlo = INT_MAX, whi = INT_MIN;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        int lo = qrow[qb] < T ? qdoc[qb] : INT_MAX, hi = qrow[qb] < T ? qdoc[qb] : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            lo = min(lo, __shfl_xor(lo, off));
+            hi = max(hi, __shfl_xor(hi, off));
+        }
+        lo = __builtin_amdgcn_readfirstlane(lo);
+        hi = __builtin_amdgcn_readfirstlane(hi);
+        qsd[qb] = (lo == hi) ? lo : INT_MIN + 1;
+        wlo = min(wlo, lo);
+        whi = max(whi, hi);
+    }
+    if (lane == 0) {
+        s_qrng[2 * wave] = wlo;
+        s_qrng[2 * wave + 1] = whi;
+    }
+    __syncthreads();
+    int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        bq_lo = min(bq_lo, s_qrng[2 * w]);
+        bq_hi = max(bq_hi, s_qrng[2 * w + 1]);
+    }
+
+    const int kv_hi = causal ? min(T, R + BM) : T;
+    const int ncand = (kv_hi + BN - 1) / BN;
+    const int t0 = causal ? R / BN : INT_MAX;  // first diagonal tile
+
+    // Screen candidate tiles c0 .. c0+nc-1 into t_list / t_doc; returns the
+    // number kept.  All loads of a thread are independent (one memory latency).
+    const bool doc_vec = (reinterpret_cast<uintptr_t>(docb) & 15) == 0;
+    auto screen = [&](int c0, int nc) -> int {
+        if (tid < nc) {
+            const int key0 = (c0 + tid) * BN;
+            const int kend = min(key0 + BN, T);
+            int lo = INT_MAX, hi = INT_MIN;
+            if (doc_vec && kend - key0 == BN) {
+#pragma unroll 8
+                for (int j = 0; j < BN / 4; ++j) {
+                    const int4 x = *reinterpret_cast<const int4*>(docb + key0 + 4 * j);
+                    lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
+                    hi = max(hi, max(max(x.x, x.y), max(x.z, x.w)));
+                }
+            } else {
+                for (int key = key0; key < kend; ++key) {
+                    const int d = docb[key];
+                    lo = min(lo, d);
+                    hi = max(hi, d);
+                }
+            }
+            t_keep[tid] = (hi >= bq_lo && lo <= bq_hi) ? 1 : 0;
+            t_tdoc[tid] = (lo == hi) ? lo : INT_MIN;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            int count = 0;
+            for (int base0 = 0; base0 < nc; base0 += 64) {
+                const int i = base0 + lane;
+                const bool keep = i < nc && t_keep[i] != 0;
+                const uint64_t m = __ballot(keep);
+                const int pos = count + (int)__builtin_amdgcn_mbcnt_hi(
+                                            (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                if (keep) {
+                    t_list[pos] = c0 + i;
+                    t_doc[pos] = t_tdoc[i];
+                }
+                count += __popcll(m);
+            }
+            if (lane == 0) s_count = count;
+        }
+        __syncthreads();
+        return __builtin_amdgcn_readfirstlane(s_count);
+    };
+
+    // Kept tile u -> stage u % NST: K, V (wave-instruction i writes LDS slots
+    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk') and this
+    // wave's 16 key document ids (lanes 0-3, 16 bytes each).
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        const int st = u % NST;
+        const int key0 = __builtin_amdgcn_readfirstlane(t_list[u]) * BN;
+        uint8_t* kb = k_lds + st * TB;
+        uint8_t* vb = v_lds + st * TB;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (key0 + row) * RB;
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
+        }
+        if (lane < 4) dma_load16(rd, lds_addr(kd_lds + st * BN + wave * 16), (key0 + wave * 16 + lane * 4) * 4);
+    };
+
+    f32x16 oacc[DB][NQB];
+    float zacc[NQB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) oacc[db][qb] = zero16();
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) zacc[qb][0] = zacc[qb][1] = 0.f;
+
+    const int vrow_l = 4 * g + ((lane & 15) >> 2);
+    const int vcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto k_operand = [&](const uint8_t* kb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        const int pc = (2 * ks + g) ^ (row & 7);
+        return *reinterpret_cast<const u32x4*>(kb + row * RB + pc * 16);
+    };
+    auto v_operand = [&](const uint8_t* vb, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + vrow_l;
+        const int col = db * 32 + vcol_l;
+        const int pc = (col >> 3) ^ ((row & 3) << 1);
+        const uint8_t* b0 = vb + row * RB + pc * 16 + (col & 7) * 2;
+        const uint8_t* b1 = vb + (row + 8) * RB + pc * 16 + (col & 7) * 2;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b1));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    // Elementwise pass over one 32-key half of S^T: p' = relu(x|x|) packed,
+    // z += p'.
+    auto elementwise = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
+                zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
+                pk[qb][j] = u;
+            }
+        }
+    };
+    // Zero the masked elements of column block qb in one 32-key half: key
+    // key0h + 4 g + 8 i + k (register 4 i + k) is masked when it lies past
+    // the lane's row (causal) or belongs to another document (kd: this
+    // stage's key document ids).
+    auto apply_mask = [&](f32x16& s, int qb, int key0h, const int32_t* kd) __attribute__((always_inline)) {
+        const int lim = causal ? qrow[qb] - (key0h + 4 * g) : INT_MAX;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int4 d4 = *reinterpret_cast<const int4*>(kd + 4 * g + 8 * i);
+            const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (8 * i + k > lim || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
+        }
+    };
+
+    u32x4 kop[KS];
+    auto read_k = [&](u32x4 (&dst)[KS], const uint8_t* kb, int nb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) dst[ks] = k_operand(kb, nb, ks);
+    };
+    auto read_v = [&](u32x4 (&dst)[2][DB], const uint8_t* vb, int nb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) dst[hh][db] = v_operand(vb, nb, hh, db);
+    };
+    auto qk_op = [&](const u32x4 (&ops)[KS], f32x16 (&s)[NQB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(ops[ks], qr[qb][ks], s[qb]);
+    };
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
+                    oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
+                }
+    };
+    // The fast kernel's four phases (see born_fwd_fast.h), MFMA-only phases at
+    // raised wave priority.  One instantiation for every tile (a second one in
+    // the loop costs more registers than the wave has): the masks are applied
+    // between phases under uniform flags (m0, m1: column block 0 / 1 masked).
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, const int32_t* kd, int key0, bool m0, bool m1)
+        __attribute__((always_inline)) {
+        f32x16 s0[NQB], s1[NQB];
+        uint32_t pk0[NQB][8], pk1[NQB][8];
+        u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
+        __builtin_amdgcn_s_setprio(1);
+        read_k(kop1, kb, 1);
+        qk_op(kop, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        if (m0) apply_mask(s0[0], 0, key0, kd);
+        if (m1) apply_mask(s0[1], 1, key0, kd);
+        __builtin_amdgcn_sched_barrier(0);
+        read_v(vop0, vb, 0);
+        qk_op(kop1, s1);
+        elementwise(s0, pk0);
+#pragma unroll
+        for (int i = 0; i < KS * NQB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (m0) apply_mask(s1[0], 0, key0 + 32, kd + 32);
+        if (m1) apply_mask(s1[1], 1, key0 + 32, kd + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        read_v(vop1, vb, 1);
+        pv_op(vop0, pk0);
+        elementwise(s1, pk1);
+#pragma unroll
+        for (int i = 0; i < 2 * DB * NQB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, 10, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        pv_op(vop1, pk1);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Pipeline over the kept tiles of each screened chunk: tiles 0 and 1
+    // issued up front, tile u+2 right after the barrier that starts step u;
+    // at that barrier each wave has waited for its share of tile u (loads
+    // return in order: only tile u+1's may still be in flight).
+    for (int c0 = 0; c0 < ncand; c0 += CAP) {
+        const int n = screen(c0, min(CAP, ncand - c0));
+        if (n > 0) issue(0);
+        if (n > 1) issue(1);
+        for (int u = 0; u < n; ++u) {
+            if (u + 1 < n)
+                wait_vmcnt<kTileLoads>();
+            else
+                wait_vmcnt<0>();
+            __syncthreads();
+            if (u + 2 < n) issue(u + 2);
+            // Stage offset opaque to the optimiser (addresses formed per tile).
+            int soff = (u % NST) * TB;
+            asm volatile("" : "+s"(soff));
+            const uint8_t* kb = k_lds + soff;
+            const uint8_t* vb = v_lds + soff;
+            const int32_t* kd = kd_lds + (soff / TB) * BN;
+            const int ti = __builtin_amdgcn_readfirstlane(t_list[u]);
+            const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+            read_k(kop, kb, 0);
+            // A column block needs the element test on the causal diagonal
+            // (tiles t0 .. t0+3: block 0 in all four, block 1 in the last two)
+            // and wherever its rows and the tile's keys are not all in one
+            // document.
+            const int rel = ti - t0;  // t0 is INT_MAX without causality
+            const bool m0 = rel >= 0 || td != qsd[0];
+            const bool m1 = rel >= 2 || td != qsd[1];
+            tile(kb, vb, kd, ti * BN, m0, m1);
+        }
+        __syncthreads();  // the list and the ring are reused by the next chunk
+    }
+
+    // Epilogue: normalise, stage this wave's rows in the idle ring (row r at
+    // smem + 128 r, chunks XOR-swizzled by r & 7), read them back 16 bytes
+    // per lane and store 8 whole rows per instruction (non-temporal).
+    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    float* __restrict__ Zp = p.z + (size_t)bh * T;
+    const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
+    const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+    // (The lane index goes through an empty asm so these addresses are formed
+    // here rather than hoisted and kept live across the tile loop.)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+    const int gg = ln >> 5;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const float zl = zacc[qb][0] + zacc[qb][1];
+        const float zt = zl + __shfl_xor(zl, 32);
+        const float rcp = 1.0f / (zt + eps_s);
+        const int row = 128 * qb + lr;
+        uint8_t* rb = smem + row * RB;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x16& o = oacc[db][qb];
+                u32x2 w;
+                w[0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
+                w[1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
+                const int chunk = 4 * db + j;
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 7)) << 4) + 8 * gg) = w;
+            }
+        if (gg == 0 && R + row < T) __builtin_nontemporal_store(s2 * zt + p.eps, Zp + R + row);
+    }
+    const int chunk = ln & 7;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
+        const int qi = R + row;
+        if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
+    }
+}
+
+template <class E, int DP>
+hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace qdl

@@ -1,5 +1,6 @@
 // Forward kernel instantiations for f16 inputs.
 #include "born_fwd.h"
+#include "born_fwd_doc.h"
 #include "born_fwd_fast.h"
 #include "born_launch.h"
 
@@ -10,7 +11,10 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
     const int mode = mask_mode(a.is_causal, a.window, a.doc);
     // Hot path: D == 64 exactly, dense or causal, per-head slice addressable
     // with 32-bit buffer offsets.
-    if (a.D == 64 && mode != kGeneral && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31))
+    const bool addr32 = ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    // Documents (no window): the document-aware fast kernel.
+    if (a.D == 64 && a.doc != nullptr && a.window == 0 && addr32) return launch_fwd16_doc<F16, 64>(a, s);
+    if (a.D == 64 && mode != kGeneral && addr32)
         return mode == kCausal ? launch_fwd16_fast<F16, 64, kCausal>(a, s) : launch_fwd16_fast<F16, 64, kDense>(a, s);
 #define QDL_MODE_BODY(M) return launch_fwd16<F16, DPV, M>(a, s);
 #define QDL_DP_BODY(D_) { constexpr int DPV = D_; QDL_SWITCH_MODE(mode, QDL_MODE_BODY) }
