@@ -265,6 +265,13 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         }
     };
 
+    // Zero the column of every lane whose row is outside the tile's single
+    // document (the tile is off the causal diagonal).
+    auto apply_lane = [&](f32x16& s, bool vis) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = vis ? s[r] : 0.f;
+    };
+
     u32x4 kop[KS];
     auto read_k = [&](u32x4 (&dst)[KS], const uint8_t* kb, int nb) __attribute__((always_inline)) {
 #pragma unroll
@@ -299,8 +306,8 @@ void born_fwd16_doc_kernel(FwdArgs p) {
     // raised wave priority.  One instantiation for every tile (a second one in
     // the loop costs more registers than the wave has): the masks are applied
     // between phases under uniform flags (m0, m1: column block 0 / 1 masked).
-    auto tile = [&](const uint8_t* kb, const uint8_t* vb, const int32_t* kd, int key0, bool m0, bool m1)
-        __attribute__((always_inline)) {
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, const int32_t* kd, int key0, bool m0, bool m1, bool l0,
+                    bool l1, bool v0, bool v1) __attribute__((always_inline)) {
         f32x16 s0[NQB], s1[NQB];
         uint32_t pk0[NQB][8], pk1[NQB][8];
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
@@ -310,7 +317,9 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
         if (m0) apply_mask(s0[0], 0, key0, kd);
+        else if (l0) apply_lane(s0[0], v0);
         if (m1) apply_mask(s0[1], 1, key0, kd);
+        else if (l1) apply_lane(s0[1], v1);
         __builtin_amdgcn_sched_barrier(0);
         read_v(vop0, vb, 0);
         qk_op(kop1, s1);
@@ -323,7 +332,9 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         if (m0) apply_mask(s1[0], 0, key0 + 32, kd + 32);
+        else if (l0) apply_lane(s1[0], v0);
         if (m1) apply_mask(s1[1], 1, key0 + 32, kd + 32);
+        else if (l1) apply_lane(s1[1], v1);
         __builtin_amdgcn_sched_barrier(0);
         read_v(vop1, vb, 1);
         pv_op(vop0, pk0);
@@ -367,12 +378,15 @@ void born_fwd16_doc_kernel(FwdArgs p) {
             read_k(kop, kb, 0);
             // A column block needs the element test on the causal diagonal
             // (tiles t0 .. t0+3: block 0 in all four, block 1 in the last two)
-            // and wherever its rows and the tile's keys are not all in one
-            // document.
+            // and where the tile's keys span several documents.  Off the
+            // diagonal, keys of one document are visible to the rows of that
+            // document and to no other: unless all 32 rows are in it, a
+            // per-lane select clears the other rows' columns.
             const int rel = ti - t0;  // t0 is INT_MAX without causality
-            const bool m0 = rel >= 0 || td != qsd[0];
-            const bool m1 = rel >= 2 || td != qsd[1];
-            tile(kb, vb, kd, ti * BN, m0, m1);
+            const bool mixed = td == INT_MIN;
+            const bool m0 = rel >= 0 || mixed;
+            const bool m1 = rel >= 2 || mixed;
+            tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td);
         }
         __syncthreads();  // the list and the ring are reused by the next chunk
     }
