@@ -25,13 +25,15 @@
 // both layouts, V row-major) -> dscale reduction.
 #pragma once
 
+#include "born_bwd_fast.h"
 #include "born_common.h"
 #include "born_stage.h"
 
 namespace qdl {
 
 // ---------------------------------------------------------------------------
-// Pre-pass: delta_i = dO_i . O_i and delta_i / Z_i, one group of G lanes per row.
+// Pre-pass: -delta_i = -(dO_i . O_i), delta_i / Z_i and 1 / Z_i, one group of
+// G lanes per row.
 // ---------------------------------------------------------------------------
 template <class E, bool F32>
 __global__ __launch_bounds__(256) void born_bwd_delta_kernel(BwdArgs p, int G) {
@@ -64,8 +66,10 @@ __global__ __launch_bounds__(256) void born_bwd_delta_kernel(BwdArgs p, int G) {
     }
     for (int off = G >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (row < nrows && sub == 0) {
-        p.delta[row] = acc;
+        const float zi = 1.0f / p.z[row];
+        p.ndelta[row] = -acc;
         p.delta_z[row] = acc / p.z[row];
+        p.zinv[row] = zi;
     }
 }
 
@@ -363,7 +367,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     const uint16_t* __restrict__ V = reinterpret_cast<const uint16_t*>(p.v) + base;
     const uint16_t* __restrict__ dO = reinterpret_cast<const uint16_t*>(p.dout) + base;
     const float* __restrict__ Zr = p.z + (size_t)bh * T;
-    const float* __restrict__ Dl = p.delta + (size_t)bh * T;
+    const float* __restrict__ NDl = p.ndelta + (size_t)bh * T;
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
@@ -405,7 +409,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         dst.template load<E>(dO, i0, T, D, tid);
         if (tid < BQ) {
             const int i = i0 + tid;
-            ndreg = i < T ? -Dl[i] : 0.f;
+            ndreg = i < T ? NDl[i] : 0.f;
             zireg = i < T ? 1.0f / Zr[i] : 0.f;
             if (kDoc && has_doc) dreg = i < T ? docb[i] : -1;
         }
@@ -753,7 +757,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     const float* __restrict__ V = reinterpret_cast<const float*>(p.v) + base;
     const float* __restrict__ dO = reinterpret_cast<const float*>(p.dout) + base;
     const float* __restrict__ Zr = p.z + (size_t)bh * T;
-    const float* __restrict__ Dl = p.delta + (size_t)bh * T;
+    const float* __restrict__ NDl = p.ndelta + (size_t)bh * T;
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
@@ -801,7 +805,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         dst.load(dO, i0, T, D, tid);
         if (tid < BQ) {
             const int i = i0 + tid;
-            ndreg = i < T ? -Dl[i] : 0.f;
+            ndreg = i < T ? NDl[i] : 0.f;
             zireg = i < T ? 1.0f / Zr[i] : 0.f;
             if (kDoc && has_doc) dreg = i < T ? docb[i] : -1;
         }
@@ -987,14 +991,23 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     hipError_t e = launch_bwd_common_pre<E, false>(a, st);
     if (e != hipSuccess) return e;
     const unsigned BH = (unsigned)(a.B * a.H);
-    {
+    // D == 64, dense or causal, per-head slice addressable with 32-bit buffer
+    // offsets: the fast dK/dV and dQ kernels (born_bwd_fast.h).
+    const bool fast = DP == 64 && a.D == 64 && MODE != kGeneral && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    if constexpr (DP == 64 && MODE != kGeneral) {
+        if (fast) {
+            if ((e = launch_bwd16_dkdv_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
+            if ((e = launch_bwd16_dq_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
+        }
+    }
+    if (!fast) {
         constexpr int BK = C::NW * 32;
         const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH);
         hipLaunchKernelGGL((born_bwd_dkdv16_kernel<E, DP, C::NW, C::KV_BQ, MODE, C::KV_WPE>), grid,
                            dim3(C::NW * 64), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    {
+    if (!fast) {
         constexpr int BM = C::NW * 32 * C::DQ_NQB;
         const dim3 grid((unsigned)((a.T + BM - 1) / BM) * BH);
         hipLaunchKernelGGL((born_bwd_dq16_kernel<E, DP, C::DQ_NQB, C::NW, C::DQ_BN, MODE, C::DQ_WPE>),

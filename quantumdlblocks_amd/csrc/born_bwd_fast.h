@@ -1,0 +1,569 @@
+// Flash-Born backward for head dim D == 64, dense or causal (no window, no
+// document ids): the C5 hot path.  Same arithmetic as born_bwd_dq16_kernel
+// (born_bwd.h); the tiles move and the instruction stream is laid out the way
+// born_fwd_fast.h does it.
+//
+// dQ kernel (queries stationary), one 128-row query block per workgroup,
+// wave w owning rows 32 w .. 32 w + 31 (one MFMA column block):
+//   * Q and dO rows go straight from HBM into registers (B operands of S^T
+//     and dP^T); 1/Z_i and delta_i / Z_i are per-lane scalars.
+//   * K and V tiles of 64 keys go global -> LDS with buffer_load ... lds
+//     through a ring of three stages (tile u+2 issued right after the barrier
+//     that starts tile u).  Each 16-byte chunk c of row r sits at chunk
+//     c ^ f(r) of its LDS row:
+//       K: f(r) = 2 (r & 3) | ((r >> 2) & 1)  -> conflict-free both for the
+//          8-row ds_read_b128 of S^T = K Q^T and for the 4-row
+//          ds_read_b64_tr_b16 of dQ^T = K^T U
+//       V: f(r) = r & 7                        -> 8-row ds_read_b128 of dP^T
+//     (32 banks x 4 bytes).
+//   * Per tile, two 32-key halves in four fenced phases:
+//       1: S0 = K0 Q^T, T0 = V0 dO^T                      (MFMA only)
+//       2: S1, T1 | U0 = relu(S0) (T0 / Z - delta / Z)     reads K0^T
+//       3: dQ^T += K0^T U0 | U1                            reads K1^T
+//       4: dQ^T += K1^T U1                                 (MFMA only)
+//   * Under causality the block's two diagonal tiles are masked per element
+//     for the waves they cut and skipped by the waves they do not reach.
+//   * The finished dQ rows are scaled, packed, staged in the idle ring and
+//     written back 16 bytes per lane (8 whole rows per store instruction).
+#pragma once
+
+#include "born_fwd_fast.h"
+
+namespace qdl {
+
+template <class E, int DP, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void born_bwd16_dq_fast_kernel(BwdArgs p) {
+    static_assert(DP == 64, "tuned for D = 64");
+    static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
+    constexpr int KS = DP / 16;
+    constexpr int DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per tile row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
+    constexpr int kTileLoads = 2 * LPW;
+    static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB, "tile split / staging fits the ring");
+    static_assert(BM == 4 * BN, "four 64-row slices per block");
+    constexpr bool kCaus = (MODE == kCausal);
+
+    // One buffer: the K/V ring during the tile loop, the output staging
+    // (256 rows x 128 bytes) once the loop is done.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+    uint8_t* const k_lds = smem;
+    uint8_t* const v_lds = smem + NST * TB;
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    // Under causality the longest key ranges go first.
+    const int mb = kCaus ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int h = bh % p.H;
+    const int R = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+    // Rows: column c of block qb -> row R + 128 qb + 64 (c / 16) + 16 wave + c % 16.
+    const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
+
+    const size_t base = (size_t)bh * T * DP;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
+    // min(|s|, 1) (see E::kScaleInSquare); the epilogue divides it back out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    // Stationary operands: sign-flipped Q and dO rows of this lane's queries.
+    int qrow[NQB];
+    u32x4 qr[NQB][KS], dr[NQB][KS];
+    float zinv[NQB], nd[NQB];
+    {
+        const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
+        const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            qrow[qb] = R + 128 * qb + lrow;
+            const int qi = qrow[qb];
+            const bool ok = qi < T;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+                if (ok) {
+                    x = ldg16(Qg + (size_t)qi * DP + (2 * ks + g) * 8);
+                    y = ldg16(dOg + (size_t)qi * DP + (2 * ks + g) * 8);
+                }
+                qr[qb][ks] = x ^ flip;
+                dr[qb][ks] = y;
+            }
+            zinv[qb] = ok ? 1.0f / p.z[(size_t)bh * T + qi] : 0.f;
+            nd[qb] = ok ? -p.delta_z[(size_t)bh * T + qi] : 0.f;
+        }
+    }
+
+    const int ntiles = kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN;
+    const int t0 = kCaus ? min(R / BN, ntiles) : ntiles;  // first diagonal tile
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+    auto kswz = [](int r) __attribute__((always_inline)) { return ((r & 3) << 1) | ((r >> 2) & 1); };
+
+    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
+    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        const int st = u % NST;
+        const int key0 = u * BN;
+        uint8_t* kb = k_lds + st * TB;
+        uint8_t* vb = v_lds + st * TB;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (key0 + row) * RB;
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ kswz(row)) << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
+        }
+    };
+
+    // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, dP^T);
+    // K^T: keys nb * 32 + hh * 16 + 4 g + (lane & 15) / 4 (+8), d columns
+    // db * 32 + 16 ((lane >> 4) & 1) + 4 (lane & 3): the key order of the
+    // accumulator layout of U (as P in the forward).
+    const int trow_l = 4 * g + ((lane & 15) >> 2);
+    const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto k_row = [&](const uint8_t* kb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        return *reinterpret_cast<const u32x4*>(kb + row * RB + (((2 * ks + g) ^ kswz(row)) << 4));
+    };
+    auto v_row = [&](const uint8_t* vb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        return *reinterpret_cast<const u32x4*>(vb + row * RB + (((2 * ks + g) ^ (row & 7)) << 4));
+    };
+    auto k_tr = [&](const uint8_t* kb, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + trow_l;
+        const int col = db * 32 + tcol_l;
+        const uint8_t* b0 = kb + row * RB + (((col >> 3) ^ kswz(row)) << 4) + (col & 7) * 2;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0 + 8 * RB));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    f32x16 acc[DB][NQB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) acc[db][qb] = zero16();
+
+    // One 32-key half nb of a tile:
+    //   S^T = K Q^T, T^T = V dO^T       (A = K, V rows; B = Q^T, dO^T)
+    //   U = relu(S^T) (T^T / Z - delta / Z), masked keys zeroed
+    //   dQ^T += K^T U                     (A = K^T, B = U)
+    // MFMAs at raised wave priority, the elementwise pass at normal priority:
+    // the two workgroups sharing a SIMD overlap one's MFMAs with the other's
+    // VALU work.  (Interleaving the column blocks' phases within the wave
+    // measured slower.)  relu is an integer max on the float bits (no NaN
+    // canonicalisation).  One instantiation for every tile (a second one
+    // costs more registers than the wave has): the causal mask of column
+    // block qb is applied under the uniform flag mk[qb].
+    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const bool (&mk)[NQB])
+        __attribute__((always_inline)) {
+        f32x16 s[NQB], t[NQB];
+        uint32_t pk[NQB][8];
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16(), t[qb] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 ko = k_row(kb, nb, ks);
+            const u32x4 vo = v_row(vb, nb, ks);
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                s[qb] = E::mfma(ko, qr[qb][ks], s[qb]);
+                t[qb] = E::mfma(vo, dr[qb][ks], t[qb]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            if (mk[qb]) {
+                const int lim = qrow[qb] - kbase;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                const float a0 = __int_as_float(max(__float_as_int(x0), 0));
+                const float a1 = __int_as_float(max(__float_as_int(x1), 0));
+                pk[qb][j] = E::pack(a0 * fmaf(t[qb][2 * j], zinv[qb], nd[qb]), a1 * fmaf(t[qb][2 * j + 1], zinv[qb], nd[qb]));
+            }
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const u32x4 a = k_tr(kb, nb, hh, db);
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
+                    acc[db][qb] = E::mfma(a, bq, acc[db][qb]);
+                }
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, const bool (&mk)[NQB])
+        __attribute__((always_inline)) {
+        half(kb, vb, 0, key0 + 4 * g, mk);
+        half(kb, vb, 1, key0 + 32 + 4 * g, mk);
+    };
+
+    // Pipeline: tiles 0 and 1 issued up front (tile 1 after the stationary
+    // loads have landed, so the compiler's wait for them does not also wait
+    // for tile 1), tile u+2 right after the barrier that starts step u; at
+    // that barrier each wave has waited for its share of tile u (loads return
+    // in order: only tile u+1's may still be in flight).
+    if (ntiles > 0) issue(0);
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[qb][ks]), "+v"(dr[qb][ks]));
+        asm volatile("" : "+v"(zinv[qb]), "+v"(nd[qb]));
+    }
+    if (ntiles > 1) issue(1);
+    for (int u = 0; u < ntiles; ++u) {
+        if (u + 1 < ntiles)
+            wait_vmcnt<kTileLoads>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        if (u + 2 < ntiles) issue(u + 2);
+        int soff = (u % NST) * TB;
+        asm volatile("" : "+s"(soff));
+        const uint8_t* kb = k_lds + soff;
+        const uint8_t* vb = v_lds + soff;
+        // Diagonal tiles t0, t0+1: block 0 cut by the mask, block 1 fully
+        // visible; t0+2, t0+3: block 0 fully masked (computed, then zeroed
+        // by the mask), block 1 cut.
+        const bool mk[NQB] = {u >= t0, u >= t0 + 2};
+        tile(kb, vb, u * BN, mk);
+    }
+
+    // Epilogue: scale, pack, stage this wave's rows in the idle ring (row r at
+    // smem + 128 r, chunks XOR-swizzled by r & 7), read them back 16 bytes
+    // per lane and store 8 whole rows per instruction.
+    __syncthreads();  // every wave is done with the ring
+    uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
+    const float f = 2.f * sc * fabsf(sc) / sq_pre;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const int row = 128 * qb + lr;
+        uint8_t* rb = smem + row * RB;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x16& o = acc[db][qb];
+                u32x2 w;
+                w[0] = E::pack(o[4 * j] * f, o[4 * j + 1] * f);
+                w[1] = E::pack(o[4 * j + 2] * f, o[4 * j + 3] * f);
+                const int chunk = 4 * db + j;
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 7)) << 4) + 8 * (ln >> 5)) = w;
+            }
+    }
+    const int chunk = ln & 7;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
+        const int q = R + row;
+        if (q < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * DP + chunk * 8));
+    }
+}
+
+template <class E, int DP, int MODE>
+hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
+    constexpr int BM = 256;
+    const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, DP, MODE>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// dK / dV kernel (keys stationary), one 128-key block per workgroup, wave w
+// owning keys 32 w .. 32 w + 31 (one MFMA column block):
+//   * Sign-flipped K and V rows of the wave's keys go straight from HBM into
+//     registers (B operands of S = Q K'^T and dP = dO V^T).
+//   * Query tiles of 64 rows stream through a three-stage LDS ring: Q and dO
+//     (buffer_load ... lds, chunks XOR-swizzled as K in the dQ kernel, so
+//     both the row reads of S / dP and the transposed reads of dK / dV are
+//     conflict-free), plus -delta and 1/Z of the tile's rows (16 lanes each).
+//   * Per 32-query half, in the accumulator layout (one key per lane, 16
+//     queries per lane):
+//       S   = Q K'^T                    (A = Q rows)
+//       dPz = dO V^T - delta            (A = dO rows, accumulator
+//                                        initialised with -delta from LDS)
+//       t = relu(S) / Z_i, W = t relu(S), U = t dPz   (masked queries zeroed)
+//       dV^T += dO^T W,  dK^T += Q^T U  (A = dO^T, Q^T transposed reads)
+//   * The finished dK, dV rows are scaled, packed, staged in the idle ring and
+//     written back 16 bytes per lane.
+template <class E, int DP, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
+    static_assert(DP == 64, "tuned for D = 64");
+    static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
+    constexpr int KS = DP / 16;
+    constexpr int DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per tile row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BQ * RB;            // bytes per Q or dO tile
+    constexpr int SB = 2 * TB + 2 * BQ * 4;  // bytes per stage: Q, dO, -delta, 1/Z
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
+    static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && 2 * BK * RB <= NST * SB, "tile split / staging");
+    constexpr bool kCaus = (MODE == kCausal);
+
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    // Key blocks in ascending order: under causality the first sees the most queries.
+    const int kblk = bid / BH;
+    const int h = bh % p.H;
+    const int K0 = kblk * BK;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+    const int kw0 = K0 + 32 * wave;  // first key of this wave
+    const int key = kw0 + c;         // this lane's key
+
+    const size_t base = (size_t)bh * T * DP;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    // Stationary operands: sign-flipped K and V rows of this lane's key.
+    u32x4 kr[KS], vr[KS];
+    {
+        const uint16_t* __restrict__ Kg = reinterpret_cast<const uint16_t*>(p.k) + base;
+        const uint16_t* __restrict__ Vg = reinterpret_cast<const uint16_t*>(p.v) + base;
+        const bool ok = key < T;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+            if (ok) {
+                x = ldg16(Kg + (size_t)key * DP + (2 * ks + g) * 8);
+                y = ldg16(Vg + (size_t)key * DP + (2 * ks + g) * 8);
+            }
+            kr[ks] = x ^ flip;
+            vr[ks] = y;
+        }
+    }
+
+    const int q_lo = kCaus ? K0 : 0;
+    const int ntiles = (K0 < T) ? (T - q_lo + BQ - 1) / BQ : 0;
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
+    const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
+    const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
+    const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
+    auto swz = [](int r) __attribute__((always_inline)) { return ((r & 3) << 1) | ((r >> 2) & 1); };
+
+    // Tile u -> stage u % NST.  Waves 0 and 1 also bring the tile's -delta
+    // and 1/Z (lanes 0-15, 16 bytes each): one more load per tile.
+    const int kTileLoadsW = 2 * LPW + (wave < 2 ? 1 : 0);
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        uint8_t* sb = smem + (u % NST) * SB;
+        const int i0 = q_lo + u * BQ;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (i0 + row) * RB + ((pc ^ swz(row)) << 4);
+            dma_load16(rq, lds_addr(sb + (wave * LPW + i) * 1024), off);
+            dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
+        }
+        if (wave < 2 && lane < 16)
+            dma_load16(wave == 0 ? rdl : rzi, lds_addr(sb + 2 * TB + wave * BQ * 4), (i0 + 4 * lane) * 4);
+    };
+
+    const int trow_l = 4 * g + ((lane & 15) >> 2);
+    const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // Row reads (A of S and dPz): query row nb * 32 + c, chunk 2 ks + g.
+    auto row_op = [&](const uint8_t* tb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        return *reinterpret_cast<const u32x4*>(tb + row * RB + (((2 * ks + g) ^ swz(row)) << 4));
+    };
+    // Transposed reads (A of dV^T, dK^T): queries nb * 32 + hh * 16 + 4 g +
+    // (lane & 15) / 4 (+8), d columns db * 32 + 16 ((lane >> 4) & 1) + 4 (lane & 3).
+    auto tr_op = [&](const uint8_t* tb, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + trow_l;
+        const int col = db * 32 + tcol_l;
+        const uint8_t* b0 = tb + row * RB + (((col >> 3) ^ swz(row)) << 4) + (col & 7) * 2;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0 + 8 * RB));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    f32x16 acc_v[DB], acc_k[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
+
+    // One 32-query half nb of a tile (rows i0 + nb * 32 + 8 (r / 4) + 4 g +
+    // r % 4 for register r).  One instantiation for every tile; the causal
+    // mask (key past the query) applies under the uniform flag mk.
+    auto half = [&](const uint8_t* sb, int nb, int qbase, bool mk) __attribute__((always_inline)) {
+        const uint8_t* qt = sb;
+        const uint8_t* dt = sb + TB;
+        const float* dl = reinterpret_cast<const float*>(sb + 2 * TB);
+        const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
+        f32x16 s = zero16(), dp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dp[4 * i + k] = d4[k];
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            s = E::mfma(row_op(qt, nb, ks), kr[ks], s);
+            dp = E::mfma(row_op(dt, nb, ks), vr[ks], dp);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        if (mk) {
+            const int lim = qbase - key;  // register r is masked when 8 (r / 4) + r % 4 < -lim
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (8 * (r >> 2) + (r & 3) + lim < 0) s[r] = 0.f;
+        }
+        uint32_t w2[8], u2[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+            for (int k = 0; k < 4; k += 2) {
+                const int r = 4 * i + k;
+                float x0 = s[r], x1 = s[r + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                const float a0 = __int_as_float(max(__float_as_int(x0), 0));
+                const float a1 = __int_as_float(max(__float_as_int(x1), 0));
+                const float t0 = a0 * z4[k], t1 = a1 * z4[k + 1];
+                w2[r >> 1] = E::pack(t0 * a0, t1 * a1);
+                u2[r >> 1] = E::pack(t0 * dp[r], t1 * dp[r + 1]);
+            }
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const u32x4 bw = {w2[4 * hh], w2[4 * hh + 1], w2[4 * hh + 2], w2[4 * hh + 3]};
+            const u32x4 bu = {u2[4 * hh], u2[4 * hh + 1], u2[4 * hh + 2], u2[4 * hh + 3]};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                acc_v[db] = E::mfma(tr_op(dt, nb, hh, db), bw, acc_v[db]);
+                acc_k[db] = E::mfma(tr_op(qt, nb, hh, db), bu, acc_k[db]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Pipeline as in the dQ kernel: tiles 0 and 1 issued up front, tile u+2
+    // right after the barrier that starts step u.
+    if (ntiles > 0) issue(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
+    if (ntiles > 1) issue(1);
+    for (int u = 0; u < ntiles; ++u) {
+        if (u + 1 < ntiles) {
+            if (wave < 2)
+                wait_vmcnt<2 * LPW + 1>();
+            else
+                wait_vmcnt<2 * LPW>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (u + 2 < ntiles) issue(u + 2);
+        const int i0 = q_lo + u * BQ;
+        // This wave's keys kw0 .. kw0+31 against queries i0 .. i0+63.
+        if (kCaus && i0 + BQ - 1 < kw0) continue;  // every query before every key
+        int soff = (u % NST) * SB;
+        asm volatile("" : "+s"(soff));
+        const uint8_t* sb = smem + soff;
+        const bool mk = kCaus && i0 < kw0 + 31;
+        half(sb, 0, i0 + 4 * g, mk);
+        half(sb, 1, i0 + 32 + 4 * g, mk);
+    }
+    (void)kTileLoadsW;
+
+    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre),
+    // packed, staged in the idle ring (rows: dK at 0, dV at 128 rows) and
+    // stored 16 bytes per lane.
+    __syncthreads();
+    const float fk = 2.f * sc * fabsf(sc) / sq_pre;
+    const float fv = (sc / sq_pre) * (sc / sq_pre);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    {
+        const int row = 32 * wave + (ln & 31);
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            uint8_t* rb = smem + (which * BK + row) * RB;
+            const float f = which ? fv : fk;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x16& o = which ? acc_v[db] : acc_k[db];
+                    u32x2 w;
+                    w[0] = E::pack(o[4 * j] * f, o[4 * j + 1] * f);
+                    w[1] = E::pack(o[4 * j + 2] * f, o[4 * j + 3] * f);
+                    const int chunk = 4 * db + j;
+                    *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 7)) << 4) + 8 * (ln >> 5)) = w;
+                }
+        }
+    }
+    uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
+    uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
+    const int chunk = ln & 7;
+#pragma unroll
+    for (int which = 0; which < 2; ++which)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 32 * wave + 8 * i + (ln >> 3);
+            const u32x4 x = *reinterpret_cast<const u32x4*>(smem + (which * BK + row) * RB + ((chunk ^ (row & 7)) << 4));
+            const int kk = K0 + row;
+            if (kk < T)
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * DP + chunk * 8));
+        }
+}
+
+template <class E, int DP, int MODE>
+hipError_t launch_bwd16_dkdv_fast(const BwdArgs& a, hipStream_t st) {
+    constexpr int BK = 128;
+    const dim3 grid((unsigned)((a.T + BK - 1) / BK) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<E, DP, MODE>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace qdl

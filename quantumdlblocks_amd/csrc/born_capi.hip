@@ -131,7 +131,7 @@ int qdl_flash_born_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, co
     a.dq = dq;
     a.dk = dk;
     a.dv = dv;
-    qdl::bwd_workspace_carve(workspace, B, H, T, &a.delta, &a.delta_z, &a.dscale_part);
+    qdl::bwd_workspace_carve(workspace, B, H, T, &a.ndelta, &a.delta_z, &a.zinv, &a.dscale_part);
     a.dscale = dscale;
     a.per_head_scale = n_scale > 1 ? 1 : 0;
     a.B = (int)B;

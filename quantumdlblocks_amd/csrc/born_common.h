@@ -154,8 +154,9 @@ struct BwdArgs {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;          // (B, H, T) workspace: dO . O per row
+    float* ndelta;         // (B, H, T) workspace: -(dO . O) per row
     float* delta_z;        // (B, H, T) workspace: dO . O / Z per row
+    float* zinv;           // (B, H, T) workspace: 1 / Z per row
     double* dscale_part;   // (n_scale, DSCALE_CHUNKS) workspace: dscale partial sums
     float* dscale;         // n_scale outputs
     int per_head_scale;

@@ -47,8 +47,9 @@ hipError_t bwd_launch_f32(const BwdArgs& a, hipStream_t s);
 
 namespace qdl {
 // Backward workspace (each region 256-byte aligned):
-//   delta   = dO . O          (B*H*T fp32)
+//   ndelta  = -(dO . O)       (B*H*T fp32)
 //   delta_z = dO . O / Z      (B*H*T fp32)
+//   zinv    = 1 / Z           (B*H*T fp32)
 //   dscale partial sums       (H * DSCALE_CHUNKS fp64)
 inline int64_t bwd_region_bytes(int64_t B, int64_t H, int64_t T) {
     return ((B * H * T * 4) + 255) / 256 * 256;
@@ -58,15 +59,16 @@ inline int64_t bwd_partial_bytes(int64_t H) {
     return (n + 255) / 256 * 256;
 }
 inline int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t T) {
-    return 2 * bwd_region_bytes(B, H, T) + bwd_partial_bytes(H);
+    return 3 * bwd_region_bytes(B, H, T) + bwd_partial_bytes(H);
 }
-inline void bwd_workspace_carve(void* ws, int64_t B, int64_t H, int64_t T, float** delta,
-                                float** delta_z, double** part) {
+inline void bwd_workspace_carve(void* ws, int64_t B, int64_t H, int64_t T, float** ndelta,
+                                float** delta_z, float** zinv, double** part) {
     char* p = static_cast<char*>(ws);
     const int64_t r = bwd_region_bytes(B, H, T);
-    *delta = reinterpret_cast<float*>(p);
+    *ndelta = reinterpret_cast<float*>(p);
     *delta_z = reinterpret_cast<float*>(p + r);
-    *part = reinterpret_cast<double*>(p + 2 * r);
+    *zinv = reinterpret_cast<float*>(p + 2 * r);
+    *part = reinterpret_cast<double*>(p + 3 * r);
 }
 }  // namespace qdl
 
