@@ -3,8 +3,9 @@
 // (born_bwd.h); the tiles move and the instruction stream is laid out the way
 // born_fwd_fast.h does it.
 //
-// dQ kernel (queries stationary), one 128-row query block per workgroup,
-// wave w owning rows 32 w .. 32 w + 31 (one MFMA column block):
+// dQ kernel (queries stationary), one 256-row query block per workgroup, rows
+// dealt to waves in 16-row slices as in the forward (two MFMA column blocks
+// per wave):
 //   * Q and dO rows go straight from HBM into registers (B operands of S^T
 //     and dP^T); 1/Z_i and delta_i / Z_i are per-lane scalars.
 //   * K and V tiles of 64 keys go global -> LDS with buffer_load ... lds
@@ -16,13 +17,11 @@
 //          ds_read_b64_tr_b16 of dQ^T = K^T U
 //       V: f(r) = r & 7                        -> 8-row ds_read_b128 of dP^T
 //     (32 banks x 4 bytes).
-//   * Per tile, two 32-key halves in four fenced phases:
-//       1: S0 = K0 Q^T, T0 = V0 dO^T                      (MFMA only)
-//       2: S1, T1 | U0 = relu(S0) (T0 / Z - delta / Z)     reads K0^T
-//       3: dQ^T += K0^T U0 | U1                            reads K1^T
-//       4: dQ^T += K1^T U1                                 (MFMA only)
-//   * Under causality the block's two diagonal tiles are masked per element
-//     for the waves they cut and skipped by the waves they do not reach.
+//   * Per 32-key half: S^T, T^T MFMAs (raised wave priority), the elementwise
+//     pass U = relu(S^T) (T^T / Z - delta / Z), then dQ^T += K^T U.  The two
+//     workgroups sharing each SIMD overlap one's MFMAs with the other's VALU.
+//   * Under causality the block's four diagonal tiles are masked per element
+//     (column block 0 in all four, block 1 in the last two).
 //   * The finished dQ rows are scaled, packed, staged in the idle ring and
 //     written back 16 bytes per lane (8 whole rows per store instruction).
 #pragma once
