@@ -47,6 +47,7 @@ extern "C" {
 #define QDL_BORN_E_SCALE (-6)
 #define QDL_BORN_E_WINDOW (-7)
 #define QDL_BORN_E_WORKSPACE (-8)
+#define QDL_BORN_E_TAU (-9)
 
 typedef struct ihipStream_t *qdl_stream_t; /* == hipStream_t */
 
@@ -98,6 +99,52 @@ int qdl_flash_born_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
                        int64_t window_size, double eps, void *dq, void *dk,
                        void *dv, float *dscale, void *workspace,
                        int64_t workspace_bytes, qdl_stream_t stream);
+
+/*
+ * Purified-Born attention (flash_born.py:693-1341): weights
+ *   p_ij = relu(scale_h (q_i.k_j - tau_h))^4 + eps_base relu(q_i.k_j)^2
+ * under the same masks, Z_i = sum_j p_ij + eps, O_i = sum_j p_ij v_j / Z_i.
+ * `tau` holds n_tau fp32 values in device memory (1 or H, like scale).  The
+ * output is fp32 whatever the input dtype, as the reference's kernel writes
+ * an fp32 output (flash_born.py:1102) that its autograd function then casts.
+ */
+
+/* Forward: writes out (B, H, T, D) fp32 and z (B, H, T) fp32.
+ * Replaces the launch of `_flash_purified_born_fwd_kernel[grid](...)` in
+ * `_FlashPurifiedBornAttentionFn.forward` (flash_born.py:1110-1151). */
+int qdl_flash_purified_born_fwd(int dtype, int64_t B, int64_t H, int64_t T,
+                                int64_t D, const void *q, const void *k,
+                                const void *v, float *out, float *z,
+                                const float *scale, int64_t n_scale,
+                                const float *tau, int64_t n_tau,
+                                double eps_base, const int32_t *doc_ids,
+                                int is_causal, int64_t window_size,
+                                double eps, qdl_stream_t stream);
+
+/* Bytes of device workspace qdl_flash_purified_born_bwd needs. */
+int64_t qdl_flash_purified_born_bwd_workspace_size(int dtype, int64_t B,
+                                                   int64_t H, int64_t T,
+                                                   int64_t D);
+
+/* Backward: given the forward's fp32 out and z and the upstream gradient dout
+ * (input dtype), writes dq, dk, dv (input dtype), dscale (n_scale fp32) and
+ * dtau (n_tau fp32), both reduced in a fixed order (deterministic).
+ * Replaces the two launches `_flash_purified_born_bwd_kernel[grid_n](...)`
+ * and `_flash_purified_born_bwd_dq_kernel[grid_m](...)` in
+ * `_FlashPurifiedBornAttentionFn.backward` (flash_born.py:1197-1262) with
+ * the zero-initialised dscale / dtau buffers they accumulate into
+ * (flash_born.py:1178-1179). */
+int qdl_flash_purified_born_bwd(int dtype, int64_t B, int64_t H, int64_t T,
+                                int64_t D, const void *q, const void *k,
+                                const void *v, const float *out,
+                                const void *dout, const float *z,
+                                const float *scale, int64_t n_scale,
+                                const float *tau, int64_t n_tau,
+                                double eps_base, const int32_t *doc_ids,
+                                int is_causal, int64_t window_size, void *dq,
+                                void *dk, void *dv, float *dscale, float *dtau,
+                                void *workspace, int64_t workspace_bytes,
+                                qdl_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,25 @@ How each function is pinned (tests/test_oracle.py):
   * ``backward_magnitudes``: bounds |backward| elementwise, and equals |dv|
     when dO > 0 (every dv term is then non-negative).
   * ``eager_fp32_torch``: against ``forward`` at fp32 tolerance.
+
+Purified-Born attention (flash_born.py:693-1341; the section-8 "next" row):
+
+    u_ij = max(0, g_h (r_ij - tau_h)) M_ij, b_ij = max(0, r_ij) M_ij
+                                                  (flash_born.py:782-796)
+    p_ij = u_ij^4 + eps_base b_ij^2               (flash_born.py:798-799)
+    Z_i  = sum_j p_ij + eps, O_i = sum_j p_ij v_j / Z_i   (801-811)
+    backward (flash_born.py:905-940, 1035-1058), delta_i = dO_i . O_i:
+    dP_ij = (dO_i . v_j - delta_i) / Z_i, du_ij = 4 u_ij^3 dP_ij,
+    dR_ij = g_h du_ij + 2 eps_base b_ij dP_ij,
+    dq = dR K, dk = dR^T Q, dv = (P / Z)^T dO,
+    dg_h = sum du (r - tau), dtau_h = -g_h sum du.
+
+How they are pinned (tests/test_oracle.py): with g = 0 the weights reduce to
+eps_base b^2, i.e. Born attention with scale 1 and eps / eps_base (pinned
+above); with eps_base = 0 and tau = 0 the output is invariant under g > 0;
+brute-force scalar loops on tiny shapes; the gradients against
+torch.autograd of ``purified_eager_fp32_torch`` run in float64 and against
+float64 finite differences (gradcheck), dg and dtau included.
 """
 
 from __future__ import annotations
@@ -63,6 +82,10 @@ __all__ = [
     "eager_fp32_torch",
     "visible_pairs",
     "geometric_doc_ids",
+    "purified_forward",
+    "purified_backward",
+    "purified_backward_magnitudes",
+    "purified_eager_fp32_torch",
 ]
 
 
@@ -249,6 +272,110 @@ def eager_fp32_torch(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, d
         s_v = s_v.view(1, -1, 1, 1)
     scaled = torch.matmul(q.to(v.dtype), k.to(v.dtype).transpose(-1, -2)) * s_v
     prob = torch.relu(scaled).square()
+    if is_causal or window_size > 0 or doc_ids is not None:
+        T = prob.shape[-1]
+        idx = torch.arange(T, device=prob.device)
+        diff = idx[:, None] - idx[None, :]
+        mask = (diff >= 0) if is_causal else torch.ones((T, T), device=prob.device, dtype=torch.bool)
+        if window_size > 0:
+            mask = mask & (diff < int(window_size))
+        mask = mask.view(1, 1, T, T)
+        if doc_ids is not None:
+            mask = mask & (doc_ids[:, None, :, None] == doc_ids[:, None, None, :])
+        prob = prob * mask.to(prob.dtype)
+    w = prob / (torch.sum(prob, dim=-1, keepdim=True) + eps)
+    return torch.matmul(w.to(v.dtype), v)
+
+
+def _purified_parts(q, k, scale, tau, eps_base, is_causal, window_size, doc_ids):
+    q, k = _f64(q), _f64(k)
+    B, H, T, D = q.shape
+    g = _scale_bh(scale, H)
+    t = _scale_bh(tau, H)
+    r = q @ np.swapaxes(k, -1, -2)
+    m = visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
+    u = np.maximum(g * (r - t), 0.0) * m
+    b = np.maximum(r, 0.0) * m
+    p = u**4 + float(eps_base) * b * b
+    return g, t, r, u, b, p
+
+
+def purified_forward(q, k, v, scale, tau, eps_base=0.05, is_causal=True, eps=1e-8, window_size=0, doc_ids=None):
+    """Purified-Born forward in float64 (flash_born.py:771-811).  Returns (O, Z)."""
+    v = _f64(v)
+    _, _, _, _, _, p = _purified_parts(q, k, scale, tau, eps_base, is_causal, window_size, doc_ids)
+    Z = p.sum(-1) + eps
+    return (p @ v) / Z[..., None], Z
+
+
+def purified_backward(q, k, v, scale, tau, do, eps_base=0.05, is_causal=True, eps=1e-8, window_size=0,
+                      doc_ids=None, out=None):
+    """Purified-Born gradients in float64 (flash_born.py:905-940, 1035-1058).
+
+    Returns (dq, dk, dv, dscale, dtau); dscale / dtau hold one value, or H
+    values for a per-head parameter.  ``out``: the forward output handed to
+    the backward (delta_i = dO_i . out_i, flash_born.py:928, 1014);
+    defaults to the exact O.
+    """
+    q64, k64, v64, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    g, t, r, u, b, p = _purified_parts(q64, k64, scale, tau, eps_base, is_causal, window_size, doc_ids)
+    Z = p.sum(-1) + eps
+    O = (p @ v64) / Z[..., None] if out is None else _f64(out)
+    delta = (do * O).sum(-1)
+    dP = (do @ np.swapaxes(v64, -1, -2) - delta[..., None]) / Z[..., None]
+    du = 4.0 * u**3 * dP
+    dR = g * du + 2.0 * float(eps_base) * b * dP
+    dq = dR @ k64
+    dk = np.swapaxes(dR, -1, -2) @ q64
+    dv = np.swapaxes(p / Z[..., None], -1, -2) @ do
+    dg_h = (du * (r - t)).sum(axis=(0, 2, 3))
+    dt_h = (-g * du).sum(axis=(0, 2, 3))
+    dscale = dg_h if np.asarray(scale).size > 1 else np.array([dg_h.sum()])
+    dtau = dt_h if np.asarray(tau).size > 1 else np.array([dt_h.sum()])
+    return dq, dk, dv, dscale, dtau
+
+
+def purified_backward_magnitudes(q, k, v, scale, tau, do, eps_base=0.05, is_causal=True, eps=1e-8,
+                                 window_size=0, doc_ids=None):
+    """Size of the terms each purified gradient sums (every product in
+    absolute value): (dq, dk, dv) shaped like the gradients, then the dscale
+    and dtau term sums shaped like those outputs.  The noise floor for
+    gradients that cancel to ~0."""
+    q64, k64, v64, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    g, t, r, u, b, p = _purified_parts(q64, k64, scale, tau, eps_base, is_causal, window_size, doc_ids)
+    Z = p.sum(-1) + eps
+    O = (p @ v64) / Z[..., None]
+    delta = np.abs(do * O).sum(-1)
+    dP = (np.abs(do) @ np.abs(np.swapaxes(v64, -1, -2)) + delta[..., None]) / Z[..., None]
+    du = 4.0 * u**3 * dP
+    dR = np.abs(g) * du + 2.0 * abs(float(eps_base)) * b * dP
+    ds_h = (du * np.abs(r - t)).sum(axis=(0, 2, 3))
+    dt_h = (np.abs(g) * du).sum(axis=(0, 2, 3))
+    ds = ds_h if np.asarray(scale).size > 1 else np.array([ds_h.sum()])
+    dt = dt_h if np.asarray(tau).size > 1 else np.array([dt_h.sum()])
+    return (dR @ np.abs(k64), np.swapaxes(dR, -1, -2) @ np.abs(q64),
+            np.swapaxes(p / Z[..., None], -1, -2) @ np.abs(do), ds, dt)
+
+
+def purified_eager_fp32_torch(q, k, v, scale, tau, eps_base=0.05, is_causal=True, eps=1e-8, window_size=0,
+                              doc_ids=None):
+    """The reference's eager purified path (flash_born.py:1329-1341) restated
+    op for op, in ``v.dtype`` on the tensors' device, full T x T matmuls."""
+    import torch
+
+    if not isinstance(scale, torch.Tensor):
+        scale = torch.tensor(float(scale), dtype=torch.float32, device=q.device)
+    if not isinstance(tau, torch.Tensor):
+        tau = torch.tensor(float(tau), dtype=torch.float32, device=q.device)
+    s = torch.matmul(q.to(v.dtype), k.to(v.dtype).transpose(-1, -2))
+    g_v = scale.to(s.dtype)
+    if g_v.ndim == 1:
+        g_v = g_v.view(1, -1, 1, 1)
+    t_v = tau.to(s.dtype)
+    if t_v.ndim == 1:
+        t_v = t_v.view(1, -1, 1, 1)
+    u = torch.relu(g_v * (s - t_v))
+    prob = u.square().square() + float(eps_base) * torch.relu(s).square()
     if is_causal or window_size > 0 or doc_ids is not None:
         T = prob.shape[-1]
         idx = torch.arange(T, device=prob.device)

@@ -10,6 +10,7 @@ from .kernels import (
     HAS_TRITON,
     IS_HIP,
     flash_born_attention,
+    flash_purified_born_attention,
     get_flash_born_launch_meta,
     get_mi355x_launch_meta,
     get_rdna4_autotune_configs,
@@ -23,6 +24,7 @@ __all__ = [
     "IS_HIP",
     "compute_document_ids",
     "flash_born_attention",
+    "flash_purified_born_attention",
     "get_flash_born_launch_meta",
     "get_mi355x_launch_meta",
     "get_rdna4_autotune_configs",

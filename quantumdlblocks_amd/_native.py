@@ -28,6 +28,9 @@ EXPORTED_SYMBOLS = (
     "qdl_flash_born_fwd",
     "qdl_flash_born_bwd_workspace_size",
     "qdl_flash_born_bwd",
+    "qdl_flash_purified_born_fwd",
+    "qdl_flash_purified_born_bwd_workspace_size",
+    "qdl_flash_purified_born_bwd",
 )
 
 
@@ -68,6 +71,24 @@ def _bind(lib: ctypes.CDLL) -> None:
         _ptr, _ptr, _i64, _ptr,            # z, scale, n_scale, doc_ids
         _int, _i64, _dbl,                  # is_causal, window_size, eps
         _ptr, _ptr, _ptr, _ptr,            # dq, dk, dv, dscale
+        _ptr, _i64, _ptr,                  # workspace, workspace_bytes, stream
+    ]
+    lib.qdl_flash_purified_born_fwd.restype = _int
+    lib.qdl_flash_purified_born_fwd.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # q, k, v, out (fp32), z
+        _ptr, _i64, _ptr, _i64, _dbl,      # scale, n_scale, tau, n_tau, eps_base
+        _ptr, _int, _i64, _dbl, _ptr,      # doc_ids, is_causal, window_size, eps, stream
+    ]
+    lib.qdl_flash_purified_born_bwd_workspace_size.restype = _i64
+    lib.qdl_flash_purified_born_bwd_workspace_size.argtypes = [_int, _i64, _i64, _i64, _i64]
+    lib.qdl_flash_purified_born_bwd.restype = _int
+    lib.qdl_flash_purified_born_bwd.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # q, k, v, out (fp32), dout
+        _ptr, _ptr, _i64, _ptr, _i64,      # z, scale, n_scale, tau, n_tau
+        _dbl, _ptr, _int, _i64,            # eps_base, doc_ids, is_causal, window_size
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # dq, dk, dv, dscale, dtau
         _ptr, _i64, _ptr,                  # workspace, workspace_bytes, stream
     ]
 

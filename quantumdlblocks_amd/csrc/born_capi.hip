@@ -46,6 +46,7 @@ const char* qdl_flash_born_strerror(int code) {
         case QDL_BORN_E_SCALE: return "scale must hold 1 value or exactly H values";
         case QDL_BORN_E_WINDOW: return "window_size out of range";
         case QDL_BORN_E_WORKSPACE: return "workspace missing or too small";
+        case QDL_BORN_E_TAU: return "tau must hold 1 value or exactly H values";
         default: break;
     }
     if (code > 0) return hipGetErrorString((hipError_t)code);

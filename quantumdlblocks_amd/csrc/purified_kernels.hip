@@ -1,0 +1,46 @@
+// Purified-Born kernel instantiations: element type x padded head dim
+// (32, 64, 128, 256; the host zero-pads D to a multiple of 8 and the kernels
+// bound-check columns past D).
+#include "purified.h"
+
+namespace qdl {
+
+inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
+
+template <class IN>
+static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
+    switch (purified_padded_dim(a.D)) {
+        case 32: return launch_purified_fwd<IN, 32>(a, s);
+        case 64: return launch_purified_fwd<IN, 64>(a, s);
+        case 128: return launch_purified_fwd<IN, 128>(a, s);
+        default: return launch_purified_fwd<IN, 256>(a, s);
+    }
+}
+template <class IN>
+static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
+    switch (purified_padded_dim(a.D)) {
+        case 32: return launch_purified_bwd<IN, 32>(a, s);
+        case 64: return launch_purified_bwd<IN, 64>(a, s);
+        case 128: return launch_purified_bwd<IN, 128>(a, s);
+        default: return launch_purified_bwd<IN, 256>(a, s);
+    }
+}
+
+// dtype codes as in qdl_flash_born.h: 0 fp32, 1 fp16, 2 bf16.
+hipError_t purified_fwd_launch(int dtype, const PurArgs& a, hipStream_t s) {
+    if (dtype == 0) return purified_fwd_dispatch<float>(a, s);
+    if (dtype == 1) return purified_fwd_dispatch<F16>(a, s);
+    return purified_fwd_dispatch<BF16>(a, s);
+}
+hipError_t purified_bwd_launch(int dtype, const PurArgs& a, hipStream_t s) {
+    if (dtype == 0) return purified_bwd_dispatch<float>(a, s);
+    if (dtype == 1) return purified_bwd_dispatch<F16>(a, s);
+    return purified_bwd_dispatch<BF16>(a, s);
+}
+int64_t purified_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
+    const int64_t region = (B * H * T * 4 + 255) / 256 * 256;
+    const int64_t nwg = purified_dkdv_groups((int)B, (int)H, (int)T, purified_padded_dim((int)D));
+    return 2 * region + (2 * nwg * 4 + 255) / 256 * 256;
+}
+
+}  // namespace qdl

@@ -21,11 +21,14 @@ from types import ModuleType
 from .kernels import flash_born_triton as _ours
 
 # Names the reference's flash-Born module exports for this path
-# (src/qdlblocks/kernels/flash_born.py:20-75, 621-690).
+# (src/qdlblocks/kernels/flash_born.py:20-75, 621-690, 1064-1341).
 PATCHED_NAMES = (
     "flash_born_attention",
     "_run_triton_flash_born",
     "_FlashBornAttentionFn",
+    "flash_purified_born_attention",
+    "_run_triton_flash_purified_born",
+    "_FlashPurifiedBornAttentionFn",
     "_apply_window_and_doc_mask",
     "HAS_TRITON",
     "IS_HIP",

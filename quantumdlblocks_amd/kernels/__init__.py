@@ -6,6 +6,7 @@ from .flash_born import (
     HAS_TRITON,
     IS_HIP,
     flash_born_attention,
+    flash_purified_born_attention,
     get_flash_born_launch_meta,
     get_mi355x_launch_meta,
     get_rdna4_autotune_configs,
@@ -16,6 +17,7 @@ __all__ = [
     "HAS_TRITON",
     "IS_HIP",
     "flash_born_attention",
+    "flash_purified_born_attention",
     "get_flash_born_launch_meta",
     "get_mi355x_launch_meta",
     "get_rdna4_autotune_configs",

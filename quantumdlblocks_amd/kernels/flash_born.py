@@ -44,6 +44,7 @@ __all__ = [
     "HAS_HIP_KERNELS",
     "IS_HIP",
     "flash_born_attention",
+    "flash_purified_born_attention",
     "get_flash_born_launch_meta",
     "get_rdna4_autotune_configs",
     "get_mi355x_launch_meta",
@@ -349,3 +350,195 @@ def flash_born_attention(
     if q.is_cuda:
         return _run_triton_flash_born(q, k, v, scale_t, is_causal, eps, window_size=window_size, doc_ids=doc_ids)
     return _eager_born(q, k, v, scale_t, is_causal, eps, window_size, doc_ids)
+
+
+# ---------------------------------------------------------------------------
+# Purified-Born attention (flash_born.py:693-1341)
+# ---------------------------------------------------------------------------
+
+class _FlashPurifiedBornAttentionFn(torch.autograd.Function):
+    """Autograd contract of the reference (flash_born.py:1064-1270).
+
+    forward: computes in the autocast dtype (CUDA autocast active) else
+    ``v.dtype``; the kernel writes an fp32 output, saved for the backward and
+    returned cast to the compute dtype; Z is fp32 with eps.  backward: returns
+    dq, dk, dv in the original input dtypes, dscale and dtau in their
+    parameters' shapes and dtypes, and None for eps_base, is_causal, eps,
+    window_size, doc_ids.
+    """
+
+    @staticmethod
+    def forward(
+        ctx,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        scale: torch.Tensor,
+        tau: torch.Tensor,
+        eps_base: float,
+        is_causal: bool,
+        eps: float,
+        window_size: int = 0,
+        doc_ids: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        lib = _native.load()
+        target = _autocast_dtype(q) or v.dtype
+        if target not in _DTYPE_CODE:
+            raise TypeError(f"flash_purified_born_attention: unsupported dtype {target}")
+        scale_flat = scale.detach().contiguous().view(-1).to(dtype=torch.float32, device=q.device)
+        tau_flat = tau.detach().contiguous().view(-1).to(dtype=torch.float32, device=q.device)
+        _check_inputs(q, k, v, scale_flat, doc_ids)
+        B, H, T, D = q.shape
+        if tau_flat.numel() not in (1, H):
+            raise ValueError(f"tau must hold 1 value or H={H} per-head values, got {tau_flat.numel()}")
+        dp = (D + 7) // 8 * 8
+        q_c = _aligned(_pad_head(q.to(target), dp))
+        k_c = _aligned(_pad_head(k.to(target), dp))
+        v_c = _aligned(_pad_head(v.to(target), dp))
+        if doc_ids is not None:
+            doc_c = _aligned(doc_ids.to(device=q.device, dtype=torch.int32))
+        else:
+            doc_c = torch.empty(0, device=q.device, dtype=torch.int32)
+        out_f32 = torch.empty((B, H, T, dp), dtype=torch.float32, device=q.device)
+        z = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+        window = max(int(window_size), 0)
+        with torch.cuda.device(q.device):
+            rc = lib.qdl_flash_purified_born_fwd(
+                _DTYPE_CODE[target], B, H, T, dp,
+                q_c.data_ptr(), k_c.data_ptr(), v_c.data_ptr(), out_f32.data_ptr(), z.data_ptr(),
+                scale_flat.data_ptr(), scale_flat.numel(), tau_flat.data_ptr(), tau_flat.numel(),
+                float(eps_base), doc_c.data_ptr() if doc_ids is not None else None,
+                1 if is_causal else 0, window, float(eps), _stream_ptr(q.device),
+            )
+        _native.check(rc, "qdl_flash_purified_born_fwd")
+        ctx.save_for_backward(q_c, k_c, v_c, out_f32, z, scale_flat, tau_flat, doc_c)
+        ctx.is_causal = bool(is_causal)
+        ctx.window_size = window
+        ctx.eps_base = float(eps_base)
+        ctx.has_doc_ids = doc_ids is not None
+        ctx.head_dim = D
+        ctx.scale_shape, ctx.scale_dtype = scale.shape, scale.dtype
+        ctx.tau_shape, ctx.tau_dtype = tau.shape, tau.dtype
+        ctx.orig_q_dtype, ctx.orig_k_dtype, ctx.orig_v_dtype = q.dtype, k.dtype, v.dtype
+        out = out_f32 if dp == D else out_f32[..., :D]
+        return out.to(target)
+
+    @staticmethod
+    def backward(ctx, do: torch.Tensor):
+        lib = _native.load()
+        q_c, k_c, v_c, out_f32, z, scale_flat, tau_flat, doc_c = ctx.saved_tensors
+        B, H, T, dp = q_c.shape
+        D = ctx.head_dim
+        do_c = _aligned(_pad_head(do.to(v_c.dtype), dp))
+        dq = torch.empty_like(q_c)
+        dk = torch.empty_like(k_c)
+        dv = torch.empty_like(v_c)
+        dscale = torch.empty(scale_flat.numel(), dtype=torch.float32, device=q_c.device)
+        dtau = torch.empty(tau_flat.numel(), dtype=torch.float32, device=q_c.device)
+        code = _DTYPE_CODE[v_c.dtype]
+        ws_bytes = int(lib.qdl_flash_purified_born_bwd_workspace_size(code, B, H, T, dp))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q_c.device)
+        with torch.cuda.device(q_c.device):
+            rc = lib.qdl_flash_purified_born_bwd(
+                code, B, H, T, dp,
+                q_c.data_ptr(), k_c.data_ptr(), v_c.data_ptr(), out_f32.data_ptr(), do_c.data_ptr(),
+                z.data_ptr(), scale_flat.data_ptr(), scale_flat.numel(), tau_flat.data_ptr(), tau_flat.numel(),
+                ctx.eps_base, doc_c.data_ptr() if ctx.has_doc_ids else None,
+                1 if ctx.is_causal else 0, ctx.window_size,
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dscale.data_ptr(), dtau.data_ptr(),
+                ws.data_ptr(), ws.numel(), _stream_ptr(q_c.device),
+            )
+        _native.check(rc, "qdl_flash_purified_born_bwd")
+        if dp != D:
+            dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+        return (
+            dq.to(ctx.orig_q_dtype),
+            dk.to(ctx.orig_k_dtype),
+            dv.to(ctx.orig_v_dtype),
+            dscale.view(ctx.scale_shape).to(ctx.scale_dtype),
+            dtau.view(ctx.tau_shape).to(ctx.tau_dtype),
+            None,
+            None,
+            None,
+            None,
+            None,
+        )
+
+
+@torch.compiler.disable
+def _run_triton_flash_purified_born(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale_t: torch.Tensor,
+    tau_t: torch.Tensor,
+    eps_base: float,
+    is_causal: bool,
+    eps: float,
+    window_size: int = 0,
+    doc_ids: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Direct entry to the GPU kernels (reference name, flash_born.py:1273-1287)."""
+    return _FlashPurifiedBornAttentionFn.apply(
+        q, k, v, scale_t, tau_t, eps_base, is_causal, eps, int(window_size), doc_ids
+    )
+
+
+_run_hip_flash_purified_born = _run_triton_flash_purified_born
+
+
+def _eager_purified_born(q, k, v, scale_t, tau_t, eps_base, is_causal, eps, window_size, doc_ids):
+    """CPU formulation of the reference (flash_born.py:1329-1341), in ``v.dtype``."""
+    s = torch.matmul(q.to(v.dtype), k.to(v.dtype).transpose(-1, -2))
+    g_v = scale_t.to(s.dtype)
+    if g_v.ndim == 1:
+        g_v = g_v.view(1, -1, 1, 1)
+    t_v = tau_t.to(s.dtype)
+    if t_v.ndim == 1:
+        t_v = t_v.view(1, -1, 1, 1)
+    u = torch.relu(g_v * (s - t_v))
+    prob = u.square().square() + float(eps_base) * torch.relu(s).square()
+    if is_causal or window_size > 0 or doc_ids is not None:
+        prob = _apply_window_and_doc_mask(prob, is_causal, window_size, doc_ids)
+    weights = prob / (prob.sum(dim=-1, keepdim=True) + eps)
+    return torch.matmul(weights.to(v.dtype), v)
+
+
+def flash_purified_born_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float | torch.Tensor | None = None,
+    tau: float | torch.Tensor | None = None,
+    eps_base: float = 0.05,
+    is_causal: bool = True,
+    eps: float = 1e-8,
+    window_size: int = 0,
+    doc_ids: torch.Tensor | None = None,
+    *,
+    gamma_h: float | torch.Tensor | None = None,
+    tau_h: float | torch.Tensor | None = None,
+    causal: bool | None = None,
+) -> torch.Tensor:
+    """Purified-Born attention with the reference's signature (flash_born.py:1290-1341).
+
+    Weights ``relu(scale (q.k - tau))^4 + eps_base relu(q.k)^2`` under the
+    causal / window / document masks, normalised by their sum + eps.
+    ``scale`` (alias ``gamma_h``, default 8.0) and ``tau`` (alias ``tau_h``,
+    default 0.0625) are floats or tensors of 1 or H values; ``causal``
+    overrides ``is_causal``.  GPU tensors run the gfx950 HIP kernels for any
+    head dim up to 256; CPU tensors use the eager formulation.
+    """
+    if scale is None:
+        scale = gamma_h if gamma_h is not None else 8.0
+    if tau is None:
+        tau = tau_h if tau_h is not None else 0.0625
+    if causal is not None:
+        is_causal = bool(causal)
+    scale_t = scale if isinstance(scale, torch.Tensor) else torch.tensor(float(scale), dtype=torch.float32, device=q.device)
+    tau_t = tau if isinstance(tau, torch.Tensor) else torch.tensor(float(tau), dtype=torch.float32, device=q.device)
+    if q.is_cuda:
+        return _run_triton_flash_purified_born(
+            q, k, v, scale_t, tau_t, eps_base, is_causal, eps, window_size=window_size, doc_ids=doc_ids
+        )
+    return _eager_purified_born(q, k, v, scale_t, tau_t, eps_base, is_causal, eps, window_size, doc_ids)

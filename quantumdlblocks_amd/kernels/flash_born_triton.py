@@ -9,9 +9,13 @@ from .flash_born import (  # noqa: F401
     IS_HIP,
     _apply_window_and_doc_mask,
     _FlashBornAttentionFn,
+    _FlashPurifiedBornAttentionFn,
     _run_hip_flash_born,
+    _run_hip_flash_purified_born,
     _run_triton_flash_born,
+    _run_triton_flash_purified_born,
     flash_born_attention,
+    flash_purified_born_attention,
     get_flash_born_launch_meta,
     get_mi355x_launch_meta,
     get_rdna4_autotune_configs,
@@ -22,6 +26,7 @@ __all__ = [
     "HAS_TRITON",
     "IS_HIP",
     "flash_born_attention",
+    "flash_purified_born_attention",
     "get_flash_born_launch_meta",
     "get_mi355x_launch_meta",
     "get_rdna4_autotune_configs",

@@ -1,0 +1,111 @@
+"""GPU parity of purified-Born attention (flash_born.py:693-1341) against the
+float64 oracle on the same (dtype-rounded) inputs: output, dq, dk, dv,
+dscale and dtau, through the public ``flash_purified_born_attention``.
+
+Tolerances (normwise relative error): 2e-2 for bf16 / fp16, 1e-5 for fp32
+outputs (1e-4 for fp32 gradients, whose backward rounds nothing but sums in
+fp32 over long rows).  Gradients that cancel to ~0 are judged against the
+scale of their terms (oracle.purified_backward_magnitudes).  dscale and dtau
+are compared with the oracle's value relative to the sum of their terms'
+magnitudes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import born_oracle as orc
+from util import TOL, f64, max_abs, rel_err, seeded_inputs
+
+pytestmark = pytest.mark.gpu
+
+GTOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+FLOOR = {torch.float32: 1e-6, torch.bfloat16: 1e-4, torch.float16: 1e-4}
+
+
+def _run(q, k, v, do, scale, tau, **kw):
+    from quantumdlblocks_amd import flash_purified_born_attention
+
+    q, k, v = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+    sc = scale.detach().clone().requires_grad_(True)
+    ta = tau.detach().clone().requires_grad_(True)
+    out = flash_purified_born_attention(q, k, v, sc, ta, **kw)
+    out.backward(do)
+    torch.cuda.synchronize()
+    return out, q.grad, k.grad, v.grad, sc.grad, ta.grad
+
+
+CASES = [
+    # (B, H, T, D, dtype, kwargs, scale, tau, std)
+    (2, 3, 130, 64, torch.bfloat16, dict(is_causal=True), 8.0, 0.0625, 0.3),
+    (1, 2, 200, 64, torch.float16, dict(is_causal=True), 8.0, 0.0625, 0.3),
+    (2, 2, 97, 64, torch.float32, dict(is_causal=True), 8.0, 0.0625, 0.3),
+    (1, 4, 150, 128, torch.bfloat16, dict(is_causal=False), [4.0, 6.0, 8.0, 2.0], [0.0, 0.1, -0.1, 0.05], 0.2),
+    (2, 2, 120, 24, torch.bfloat16, dict(is_causal=True, window_size=17), 8.0, [0.1, -0.05], 0.5),
+    (1, 2, 64, 256, torch.float32, dict(is_causal=True), 3.0, 0.0, 0.1),
+    (2, 2, 160, 64, torch.bfloat16, dict(is_causal=True, eps_base=0.2, eps=1e-6), [8.0, 5.0], 0.0625, 0.3),
+    (1, 1, 1, 64, torch.bfloat16, dict(is_causal=True), 8.0, 0.0625, 0.3),
+    (1, 2, 33, 32, torch.float32, dict(is_causal=False, window_size=5), 2.0, -0.3, 0.4),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}D{c[3]}-{str(c[4])[6:]}")
+def test_purified_forward_backward(cuda_device, case):
+    B, H, T, D, dtype, kw, scale, tau, std = case
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=T + D, std=std, n=4, dtype=dtype))
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    out, dq, dk, dv, dsc, dta = _run(q, k, v, do, sc, ta, **kw)
+    assert out.dtype == dtype and dq.dtype == dtype
+    assert dsc.shape == sc.shape and dta.shape == ta.shape
+    okw = dict(eps_base=kw.get("eps_base", 0.05), is_causal=kw.get("is_causal", True), eps=kw.get("eps", 1e-8),
+               window_size=kw.get("window_size", 0))
+    O_ref, _ = orc.purified_forward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau), **okw)
+    e = rel_err(f64(out), O_ref)
+    assert e <= TOL[dtype], f"output rel err {e:.3e} (max abs {max_abs(f64(out), O_ref):.3e})"
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau), f64(do), **okw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau),
+                                           f64(do), **okw)
+    for name, got, want, m in zip(("dq", "dk", "dv"), (dq, dk, dv), ref[:3], mag[:3]):
+        er = rel_err(f64(got), want)
+        ef = max_abs(f64(got), want) / m.max() if m.max() > 0 else max_abs(f64(got), want)
+        assert er <= GTOL[dtype] or ef <= FLOOR[dtype], f"{name}: rel {er:.3e}, vs term scale {ef:.3e}"
+    # dscale / dtau: against the oracle, within the tolerance of their value or
+    # the floor of the magnitude of the terms they sum (they can cancel).
+    for name, got, want, m in (("dscale", dsc, ref[3], mag[3]), ("dtau", dta, ref[4], mag[4])):
+        got = np.atleast_1d(f64(got))
+        err = np.abs(got - want)
+        ok = (err <= GTOL[dtype] * np.abs(want)) | (err <= FLOOR[dtype] * m)
+        assert ok.all(), f"{name}: {got} vs {want} (term scale {m})"
+
+
+def test_purified_documents(cuda_device):
+    B, H, T, D = 2, 2, 300, 64
+    dtype = torch.bfloat16
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=7, std=0.3, n=4, dtype=dtype))
+    docs = orc.geometric_doc_ids(B, T, 40.0, seed=3)
+    doc_t = torch.tensor(docs, dtype=torch.int32, device=cuda_device)
+    sc = torch.tensor(8.0, device=cuda_device)
+    ta = torch.tensor(0.0625, device=cuda_device)
+    out, dq, dk, dv, dsc, dta = _run(q, k, v, do, sc, ta, is_causal=True, doc_ids=doc_t)
+    O_ref, _ = orc.purified_forward(f64(q), f64(k), f64(v), 8.0, 0.0625, 0.05, True, 1e-8, 0, docs)
+    assert rel_err(f64(out), O_ref) <= 2e-2
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), 8.0, 0.0625, f64(do), 0.05, True, 1e-8, 0, docs)
+    for got, want in zip((dq, dk, dv), ref[:3]):
+        assert rel_err(f64(got), want) <= 2e-2
+    assert abs(float(dsc) - ref[3][0]) <= 2e-2 * abs(ref[3][0]) + 1e-12
+    assert abs(float(dta) - ref[4][0]) <= 2e-2 * abs(ref[4][0]) + 1e-12
+
+
+def test_purified_deterministic_and_default_args(cuda_device):
+    from quantumdlblocks_amd import flash_purified_born_attention
+
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((2, 4, 257, 64), seed=11, std=0.3, n=3, dtype=torch.bfloat16))
+    a = flash_purified_born_attention(q, k, v)  # gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8, causal
+    b = flash_purified_born_attention(q, k, v, gamma_h=8.0, tau_h=0.0625, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    O_ref, _ = orc.purified_forward(f64(q), f64(k), f64(v), 8.0, 0.0625, 0.05, True, 1e-8)
+    assert rel_err(f64(a), O_ref) <= 2e-2

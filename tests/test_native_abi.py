@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "qdl_flash_born.h")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(qdl_flash_born_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(qdl_flash_(?:purified_)?born_\w+)\s*\(", text)))
 
 
 def _header_macros():

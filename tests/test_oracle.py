@@ -436,3 +436,107 @@ def test_planted_mistakes_are_caught(clib, kind):
             caught = True
             break
     assert caught, f"planted mistake {kind!r} was not caught by the brute-force pin"
+
+
+# --------------------------------------------------------------------------
+# purified-Born attention (flash_born.py:693-1341)
+# --------------------------------------------------------------------------
+
+def _pur_inputs(seed, B=2, H=3, T=7, D=4, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal((B, H, T, D)) * scale for _ in range(4)]
+
+
+def test_purified_zero_gamma_is_born():
+    # g = 0 leaves eps_base relu(r)^2: Born with scale 1 and eps / eps_base.
+    q, k, v, _ = _pur_inputs(1)
+    docs = np.array([[0, 0, 0, 1, 1, 2, 2], [0, 1, 1, 1, 1, 1, 2]])
+    for causal, window, doc in [(True, 0, None), (False, 3, None), (True, 2, docs)]:
+        O, Z = orc.purified_forward(q, k, v, 0.0, [0.3, -0.2, 0.0], 0.05, causal, 1e-6, window, doc)
+        Ob, Zb = orc.forward(q, k, v, 1.0, causal, 1e-6 / 0.05, window, doc)
+        np.testing.assert_allclose(O, Ob, rtol=1e-12, atol=1e-13)
+        np.testing.assert_allclose(Z, 0.05 * Zb, rtol=1e-12, atol=1e-15)
+
+
+def test_purified_gamma_invariance_without_base():
+    # eps_base = 0, tau = 0: p = g^4 relu(r)^4, so O does not depend on g > 0.
+    q, k, v, _ = _pur_inputs(2)
+    O1, Z1 = orc.purified_forward(q, k, v, 2.0, 0.0, 0.0, True, 0.0)
+    O2, Z2 = orc.purified_forward(q, k, v, 7.0, 0.0, 0.0, True, 0.0)
+    ok = Z1 > 0
+    np.testing.assert_allclose(O1[ok], O2[ok], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(Z2[ok], Z1[ok] * (7.0 / 2.0) ** 4, rtol=1e-12)
+
+
+def test_purified_brute_force_loops():
+    B, H, T, D = 1, 2, 5, 3
+    q, k, v, _ = _pur_inputs(3, B, H, T, D)
+    docs = np.array([[0, 0, 1, 1, 1]])
+    g, tau, eb, eps, W = [1.5, -2.0], [0.1, -0.4], 0.3, 1e-3, 3
+    O, Z = orc.purified_forward(q, k, v, g, tau, eb, True, eps, W, docs)
+    for h in range(H):
+        for i in range(T):
+            num, den = np.zeros(D), 0.0
+            for j in range(T):
+                if not (j <= i and i - j < W and docs[0, i] == docs[0, j]):
+                    continue
+                r = sum(q[0, h, i, d] * k[0, h, j, d] for d in range(D))
+                u = max(0.0, g[h] * (r - tau[h]))
+                p = u ** 4 + eb * max(0.0, r) ** 2
+                num += p * v[0, h, j]
+                den += p
+            den += eps
+            assert abs(Z[0, h, i] - den) <= 1e-12 * max(1.0, den)
+            np.testing.assert_allclose(O[0, h, i], num / den, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("case", [
+    dict(causal=True, window=0, doc=False, per_head=False),
+    dict(causal=False, window=3, doc=False, per_head=True),
+    dict(causal=True, window=0, doc=True, per_head=True),
+])
+def test_purified_backward_matches_autograd(case):
+    B, H, T, D = 2, 3, 6, 4
+    q, k, v, do = _pur_inputs(4, B, H, T, D, 0.8)
+    docs = np.array([[0, 0, 0, 1, 1, 1], [0, 1, 1, 2, 2, 2]]) if case["doc"] else None
+    g = np.array([2.0, 1.5, 3.0]) if case["per_head"] else np.array([2.5])
+    tau = np.array([0.1, -0.2, 0.05]) if case["per_head"] else np.array([0.0625])
+    eb, eps = 0.05, 1e-8
+    ref = orc.purified_backward(q, k, v, g, tau, do, eb, case["causal"], eps, case["window"], docs)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    tg = torch.tensor(g if case["per_head"] else g[0], requires_grad=True)
+    tt = torch.tensor(tau if case["per_head"] else tau[0], requires_grad=True)
+    tdoc = None if docs is None else torch.tensor(docs)
+    out = orc.purified_eager_fp32_torch(tq, tk, tv, tg, tt, eb, case["causal"], eps, case["window"], tdoc)
+    (out * torch.tensor(do)).sum().backward()
+    for got, want in zip(ref[:3], (tq.grad, tk.grad, tv.grad)):
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(ref[3], np.atleast_1d(tg.grad.numpy()), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(ref[4], np.atleast_1d(tt.grad.numpy()), rtol=1e-9, atol=1e-10)
+
+
+def test_purified_statement_gradcheck():
+    # Finite differences pin the torch statement the backward is compared with.
+    B, H, T, D = 1, 2, 4, 3
+    q, k, v, _ = _pur_inputs(5, B, H, T, D, 0.9)
+    args = [torch.tensor(x, requires_grad=True) for x in (q, k, v)]
+    g = torch.tensor([1.7, 2.2], dtype=torch.float64, requires_grad=True)
+    t = torch.tensor([0.05, -0.1], dtype=torch.float64, requires_grad=True)
+    f = lambda q_, k_, v_, g_, t_: orc.purified_eager_fp32_torch(q_, k_, v_, g_, t_, 0.2, True, 1e-6)
+    assert torch.autograd.gradcheck(f, (*args, g, t), eps=1e-6, atol=1e-5, rtol=1e-4)
+
+
+def test_purified_backward_out_argument_and_magnitudes():
+    q, k, v, do = _pur_inputs(6)
+    O, _ = orc.purified_forward(q, k, v, 3.0, 0.1, 0.05, True, 1e-8)
+    base = orc.purified_backward(q, k, v, 3.0, 0.1, do, 0.05, True, 1e-8)
+    same = orc.purified_backward(q, k, v, 3.0, 0.1, do, 0.05, True, 1e-8, out=O)
+    for a, b in zip(base, same):
+        np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-14)
+    # a perturbed output changes delta and so dv stays, dq moves
+    moved = orc.purified_backward(q, k, v, 3.0, 0.1, do, 0.05, True, 1e-8, out=O * 1.01)
+    np.testing.assert_allclose(moved[2], base[2], rtol=1e-12)
+    assert np.abs(moved[0] - base[0]).max() > 1e-6
+    mags = orc.purified_backward_magnitudes(q, k, v, 3.0, 0.1, do, 0.05, True, 1e-8)
+    for g_, m in zip(base, mags):
+        assert np.all(np.abs(g_) <= m * (1 + 1e-12) + 1e-15)
