@@ -14,7 +14,12 @@ average launch against the HBM roof) and ``cpu_baseline`` (the reference's
 eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
 on this host).
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5]
+    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5|p3|p5]
+
+p3 / p5: purified-Born attention (the reference's flash_purified_born_attention,
+gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8) on the C3 / C5 shapes with bf16
+inputs; its kernels contract in fp32 (the reference's P V is an fp32 dot), so
+its roofline is the fp32 MFMA peak.
 """
 
 from __future__ import annotations
@@ -32,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 
 CONFIGS = {
     # name: (B, H, T, D, std, l2norm_qk, doc_mean, backward)
@@ -40,7 +46,12 @@ CONFIGS = {
     "c4": (4, 16, 8192, 64, 1.0, False, 512.0, False),
     "c5fwd": (16, 16, 2048, 64, 1.0, False, None, False),
     "c5": (16, 16, 2048, 64, 1.0, False, None, True),
+    # purified-Born attention on the C3 / C5 shapes
+    "p3": (16, 16, 1024, 64, 0.125, False, None, False),
+    "p5": (16, 16, 2048, 64, 0.125, False, None, True),
 }
+PURIFIED = {"p3", "p5"}
+PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 
 
 def parse_args():
@@ -135,11 +146,15 @@ def visible_pairs(cfg, doc):
     return total
 
 
-def cpu_baseline(cfg, budget_s, seed):
+def cpu_baseline(cfg, budget_s, seed, purified=False):
     """Time the reference's eager CPU path (fp32, full T x T) on a bounded sample."""
     import torch
 
-    from oracle.born_oracle import eager_fp32_torch
+    from oracle.born_oracle import eager_fp32_torch, purified_eager_fp32_torch
+
+    if purified:
+        def eager_fp32_torch(q, k, v, sc):  # noqa: F811  (the purified eager path, same call shape)
+            return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS)
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -184,8 +199,8 @@ def cpu_baseline(cfg, budget_s, seed):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"{n} of the {B * H} (b,h) heads of the same config, fp32, eager "
-                   f"(flash_born.py:681-690 restated), median of 5 runs after 3 warm-ups, "
-                   f"{med * 1e3:.1f} ms per run"),
+                   f"(flash_born.py:{'1329-1341' if purified else '681-690'} restated), median of 5 runs "
+                   f"after 3 warm-ups, {med * 1e3:.1f} ms per run"),
         "cpu_model": cpu_model,
         "seconds_per_run": med,
         "speedup_of_gpu": None,
@@ -218,25 +233,47 @@ def main():
     cfg = CONFIGS[args.config]
     B, H, T, D = cfg[:4]
     backward = cfg[7]
+    purified = args.config in PURIFIED
     steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
 
     sets = []
     doc = None
     for i in range(max(1, args.sets)):
         (q, k, v, do), doc = make_inputs(cfg, args.seed + i, dev, dtype)
-        out = torch.empty_like(q)
+        out = torch.empty(q.shape, dtype=torch.float32, device=dev) if purified else torch.empty_like(q)
         z = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         grads = [torch.empty_like(q) for _ in range(3)] if backward else None
         sets.append((q, k, v, do, out, z, grads))
     scale = torch.tensor(8.0, dtype=torch.float32, device=dev)
+    tau = torch.tensor(PUR_TAU, dtype=torch.float32, device=dev)
+    dtau = torch.empty(1, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     code = _DTYPE_CODE[dtype]
     doc_ptr = doc.data_ptr() if doc is not None else None
     ws = None
     dscale = torch.empty(1, dtype=torch.float32, device=dev)
     if backward:
-        nbytes = int(lib.qdl_flash_born_bwd_workspace_size(code, B, H, T, D, 1))
+        if purified:
+            nbytes = int(lib.qdl_flash_purified_born_bwd_workspace_size(code, B, H, T, D))
+        else:
+            nbytes = int(lib.qdl_flash_born_bwd_workspace_size(code, B, H, T, D, 1))
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+
+    def pur_fwd(s):
+        q, k, v, _, out, z, _ = s
+        rc = lib.qdl_flash_purified_born_fwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             out.data_ptr(), z.data_ptr(), scale.data_ptr(), 1, tau.data_ptr(), 1,
+                                             PUR_EPS_BASE, doc_ptr, 1, 0, PUR_EPS, stream)
+        _native.check(rc, "qdl_flash_purified_born_fwd")
+
+    def pur_bwd(s):
+        q, k, v, do, out, z, (dq, dk, dv) = s
+        rc = lib.qdl_flash_purified_born_bwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             out.data_ptr(), do.data_ptr(), z.data_ptr(), scale.data_ptr(), 1,
+                                             tau.data_ptr(), 1, PUR_EPS_BASE, doc_ptr, 1, 0, dq.data_ptr(),
+                                             dk.data_ptr(), dv.data_ptr(), dscale.data_ptr(), dtau.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), stream)
+        _native.check(rc, "qdl_flash_purified_born_bwd")
 
     def fwd(s):
         q, k, v, _, out, z, _ = s
@@ -255,9 +292,9 @@ def main():
 
     def step(i):
         s = sets[i % len(sets)]
-        fwd(s)
+        (pur_fwd if purified else fwd)(s)
         if backward:
-            bwd(s)
+            (pur_bwd if purified else bwd)(s)
 
     for i in range(warmup):
         step(i)
@@ -285,31 +322,34 @@ def main():
     fwd_flops = 4.0 * D * pairs * H
     flops = fwd_flops * (3.5 if backward else 1.0)
     el = 2  # bf16 bytes
-    fwd_bytes = B * H * T * D * el * 4 + B * H * T * 4  # read Q, K, V; write O (+ Z fp32)
-    bwd_bytes = B * H * T * D * el * 8 + B * H * T * 4  # read Q,K,V,O,dO (+Z); write dQ,dK,dV
+    oel = 4 if purified else el  # the purified output (read back by its backward) is fp32
+    fwd_bytes = B * H * T * D * (el * 3 + oel) + B * H * T * 4  # read Q, K, V; write O (+ Z fp32)
+    bwd_bytes = B * H * T * D * (el * 7 + oel) + B * H * T * 4  # read Q,K,V,O,dO (+Z); write dQ,dK,dV
     nbytes = fwd_bytes + (bwd_bytes if backward else 0)
 
     value = flops / wall_step / 1e12
     achieved_tflops = flops / ev_step / 1e12
     achieved_gbs = nbytes / ev_step / 1e9
     ai = flops / nbytes
-    hbm_bound = ai * PEAK_HBM_GBS / 1e3 < PEAK_BF16_TFLOPS
+    mfma_peak = PEAK_FP32_MFMA_TFLOPS if purified else PEAK_BF16_TFLOPS
+    hbm_bound = ai * PEAK_HBM_GBS / 1e3 < mfma_peak
     if hbm_bound:
         roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved_gbs / PEAK_HBM_GBS, 4)}
     else:
-        roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved_tflops / PEAK_BF16_TFLOPS, 4)}
+        roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": mfma_peak,
+                "unit": "TFLOP/s", "frac": round(achieved_tflops / mfma_peak, 4)}
     roof["traffic"] = None if backward else load_traffic(args.config)
 
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
-        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed)
+        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed, purified)
         cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
 
     name = "fwd" if not backward else "fwd+bwd"
+    kind = "Purified-Born-attn" if purified else "Born-attn"
     line = {
-        "metric": f"Born-attn {name} TFLOP/s + % of bf16 MFMA peak, B{B} H{H} T{T} hd{D}",
+        "metric": f"{kind} {name} TFLOP/s + % of bf16 MFMA peak, B{B} H{H} T{T} hd{D}",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -319,12 +359,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp32 (bf16 inputs)" if purified else "bf16",
         "data": "synthetic (seeded N(0,%g) Q, K, V; %d rotated input sets)" % (cfg[4] ** 2, len(sets)),
         "config": {
             "workload": args.config + (" (headline)" if args.config == "c3" else ""),
             "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
-            "doc_mask": doc is not None, "backward": backward, "scale": 8.0, "eps": 1e-12,
+            "doc_mask": doc is not None, "backward": backward, "scale": 8.0,
+            "eps": PUR_EPS if purified else 1e-12,
+            **({"tau": PUR_TAU, "eps_base": PUR_EPS_BASE} if purified else {}),
         },
         "pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "roofline": roof,
