@@ -988,18 +988,20 @@ hipError_t launch_bwd_common_post(const BwdArgs& a, hipStream_t st);
 template <class E, int DP, int MODE>
 hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     using C = Bwd16Cfg<DP>;
-    hipError_t e = launch_bwd_common_pre<E, false>(a, st);
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
     const unsigned BH = (unsigned)(a.B * a.H);
     // D == 64, dense or causal, per-head slice addressable with 32-bit buffer
-    // offsets: the fast dK/dV and dQ kernels (born_bwd_fast.h).
+    // offsets: the fast dQ kernel (which also forms delta and fills the
+    // workspace, so no pre-pass) and then the fast dK/dV kernel
+    // (born_bwd_fast.h).
     const bool fast = DP == 64 && a.D == 64 && MODE != kGeneral && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
     if constexpr (DP == 64 && MODE != kGeneral) {
         if (fast) {
-            if ((e = launch_bwd16_dkdv_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
             if ((e = launch_bwd16_dq_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
+            if ((e = launch_bwd16_dkdv_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
         }
     }
+    if (!fast && (e = launch_bwd_common_pre<E, false>(a, st)) != hipSuccess) return e;
     if (!fast) {
         constexpr int BK = C::NW * 32;
         const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH);

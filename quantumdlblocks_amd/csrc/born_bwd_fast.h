@@ -78,12 +78,17 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
 
     // Stationary operands: sign-flipped Q and dO rows of this lane's queries.
+    // delta_i = dO_i . O_i is formed here from the stored O (each lane holds
+    // half a row; the other half is in lane ^ 32), and the per-row -delta,
+    // 1/Z and delta/Z the dK/dV kernel and the dscale reduction read are
+    // written to the workspace.
     int qrow[NQB];
     u32x4 qr[NQB][KS], dr[NQB][KS];
     float zinv[NQB], nd[NQB];
     {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
         const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
+        const uint16_t* __restrict__ Og = reinterpret_cast<const uint16_t*>(p.o) + base;
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             qrow[qb] = R + 128 * qb + lrow;
@@ -99,8 +104,26 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
                 qr[qb][ks] = x ^ flip;
                 dr[qb][ks] = y;
             }
-            zinv[qb] = ok ? 1.0f / p.z[(size_t)bh * T + qi] : 0.f;
-            nd[qb] = ok ? -p.delta_z[(size_t)bh * T + qi] : 0.f;
+            float dl = 0.f;
+            if (ok) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const u32x4 o = ldg16(Og + (size_t)qi * DP + (2 * ks + g) * 8);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        dl += E::lo(o[j]) * E::lo(dr[qb][ks][j]) + E::hi(o[j]) * E::hi(dr[qb][ks][j]);
+                }
+            }
+            dl += __shfl_xor(dl, 32);
+            const size_t row = (size_t)bh * T + qi;
+            const float zr = ok ? p.z[row] : 1.f;
+            zinv[qb] = ok ? 1.0f / zr : 0.f;
+            nd[qb] = ok ? -(dl / zr) : 0.f;
+            if (ok && g == 0) {
+                p.ndelta[row] = -dl;
+                p.zinv[row] = zinv[qb];
+                p.delta_z[row] = dl / zr;
+            }
         }
     }
 
