@@ -999,6 +999,10 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
         if (fast) {
             if ((e = launch_bwd16_dq_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
             if ((e = launch_bwd16_dkdv_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;
+            const int nwg = ((a.T + 255) / 256) * a.B * a.H;
+            hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),
+                               0, st, a, nwg);
+            return hipGetLastError();
         }
     }
     if (!fast && (e = launch_bwd_common_pre<E, false>(a, st)) != hipSuccess) return e;

@@ -126,6 +126,23 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
             }
         }
     }
+    // This workgroup's part of dscale = (2/s) eps sum delta / Z (closed form):
+    // its rows' sum, in a fixed order (lanes, then waves), one double per
+    // workgroup.
+    {
+        __shared__ float s_dz[NW];
+        float dz = (g == 0) ? -(nd[0] + nd[1]) : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) dz += __shfl_xor(dz, off);
+        if (lane == 0) s_dz[wave] = dz;
+        __syncthreads();
+        if (tid == 0) {
+            double acc = 0.0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) acc += (double)s_dz[w];
+            p.dscale_part[bid] = acc;
+        }
+    }
 
     const int ntiles = kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN;
     const int t0 = kCaus ? min(R / BN, ntiles) : ntiles;  // first diagonal tile
@@ -313,6 +330,29 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
         const int q = R + row;
         if (q < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * DP + chunk * 8));
+    }
+}
+
+// dscale from the dQ kernel's per-workgroup sums: output o adds, in a fixed
+// order, the partials of the workgroups whose head it covers.
+// (A template, so the translation units of several dtypes can each hold it.)
+template <int kUnused = 0>
+__global__ __launch_bounds__(256) void born_bwd_dscale_groups_kernel(BwdArgs p, int nwg) {
+    __shared__ double red[256];
+    const int o = blockIdx.x;
+    const int BH = p.B * p.H;
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < nwg; i += 256)
+        if (!p.per_head_scale || ((i % BH) % p.H) == o) acc += p.dscale_part[i];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float s = p.scale[o];
+        p.dscale[o] = (s == 0.f) ? 0.f : (float)(2.0 / (double)s * (double)p.eps * red[0]);
     }
 }
 

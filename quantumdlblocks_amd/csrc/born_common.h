@@ -157,7 +157,7 @@ struct BwdArgs {
     float* ndelta;         // (B, H, T) workspace: -(dO . O) per row
     float* delta_z;        // (B, H, T) workspace: dO . O / Z per row
     float* zinv;           // (B, H, T) workspace: 1 / Z per row
-    double* dscale_part;   // (n_scale, DSCALE_CHUNKS) workspace: dscale partial sums
+    double* dscale_part;   // workspace: dscale partial sums (per chunk of rows, or per workgroup)
     float* dscale;         // n_scale outputs
     int per_head_scale;
     int B, H, T, D;
