@@ -147,9 +147,13 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     const int bh = bid % BH;
     const int pr = bid / BH;
     const int h = bh % p.H;
-    // Item 0: query block nmb-1-pr (the longer key range under causality);
-    // item 1: query block pr, when that is a different block.
-    const int mb_a = nmb - 1 - pr, mb_b = pr;
+    // Paired launch (fast_fwd_npair blocks per head): item 0 is query block
+    // nmb-1-pr (the longer key range under causality), item 1 block pr when
+    // that is a different block.  Unpaired launch (nmb blocks per head, for
+    // problems too small to give every CU two paired workgroups): one block
+    // per workgroup, the longest key ranges first.
+    const bool paired = gridDim.x < (unsigned)(nmb * BH);
+    const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
     auto item_tiles = [&](int mb) -> int {
         const int kv_hi = kCaus ? min(T, (mb + 1) * BM) : T;
@@ -547,7 +551,12 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 template <class E, int DP, int MODE>
 hipError_t launch_fwd16_fast(const FwdArgs& a, hipStream_t st) {
     using C = FastFwdCfg<DP>;
-    const dim3 grid((unsigned)fast_fwd_npair(a.T, C::BM) * (unsigned)(a.B * a.H));
+    // Pair query blocks unless that leaves fewer than two workgroups per CU
+    // (256 CUs): then one block per workgroup.
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
+    const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
+    const dim3 grid(npair < 512u ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<E, DP, MODE>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
