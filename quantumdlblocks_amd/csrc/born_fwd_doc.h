@@ -106,6 +106,38 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         }
         qdoc[qb] = ok ? docb[qrow[qb]] : INT_MIN;
     }
+
+    const int kv_hi = causal ? min(T, R + BM) : T;
+    const int ncand = (kv_hi + BN - 1) / BN;
+    const int t0 = causal ? R / BN : INT_MAX;  // first diagonal tile
+
+    // Document-id range of candidate tile `tid` of the first screening chunk,
+    // loaded here so its latency overlaps the Q loads'.  All loads of a
+    // thread are independent (one memory latency).
+    const bool doc_vec = (reinterpret_cast<uintptr_t>(docb) & 15) == 0;
+    auto tile_range = [&](int tile, int& lo, int& hi) __attribute__((always_inline)) {
+        const int key0 = tile * BN;
+        const int kend = min(key0 + BN, T);
+        lo = INT_MAX;
+        hi = INT_MIN;
+        if (doc_vec && kend - key0 == BN) {
+#pragma unroll 8
+            for (int j = 0; j < BN / 4; ++j) {
+                const int4 x = *reinterpret_cast<const int4*>(docb + key0 + 4 * j);
+                lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
+                hi = max(hi, max(max(x.x, x.y), max(x.z, x.w)));
+            }
+        } else {
+            for (int key = key0; key < kend; ++key) {
+                const int d = docb[key];
+                lo = min(lo, d);
+                hi = max(hi, d);
+            }
+        }
+    };
+    int tlo0 = INT_MAX, thi0 = INT_MIN;
+    if (tid < min(CAP, ncand)) tile_range(tid, tlo0, thi0);
+
     // Document range of each column block's valid rows (uniform per wave):
     // qsd[qb] is the one document of all 32 rows, or INT_MIN + 1 when they
     // span several (never equal to a tile's document id, or to "mixed").
@@ -137,32 +169,12 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         bq_hi = max(bq_hi, s_qrng[2 * w + 1]);
     }
 
-    const int kv_hi = causal ? min(T, R + BM) : T;
-    const int ncand = (kv_hi + BN - 1) / BN;
-    const int t0 = causal ? R / BN : INT_MAX;  // first diagonal tile
-
     // Screen candidate tiles c0 .. c0+nc-1 into t_list / t_doc; returns the
-    // number kept.  All loads of a thread are independent (one memory latency).
-    const bool doc_vec = (reinterpret_cast<uintptr_t>(docb) & 15) == 0;
+    // number kept (the first chunk's ranges were loaded up front).
     auto screen = [&](int c0, int nc) -> int {
         if (tid < nc) {
-            const int key0 = (c0 + tid) * BN;
-            const int kend = min(key0 + BN, T);
-            int lo = INT_MAX, hi = INT_MIN;
-            if (doc_vec && kend - key0 == BN) {
-#pragma unroll 8
-                for (int j = 0; j < BN / 4; ++j) {
-                    const int4 x = *reinterpret_cast<const int4*>(docb + key0 + 4 * j);
-                    lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
-                    hi = max(hi, max(max(x.x, x.y), max(x.z, x.w)));
-                }
-            } else {
-                for (int key = key0; key < kend; ++key) {
-                    const int d = docb[key];
-                    lo = min(lo, d);
-                    hi = max(hi, d);
-                }
-            }
+            int lo = tlo0, hi = thi0;
+            if (c0 > 0) tile_range(c0 + tid, lo, hi);
             t_keep[tid] = (hi >= bq_lo && lo <= bq_hi) ? 1 : 0;
             t_tdoc[tid] = (lo == hi) ? lo : INT_MIN;
         }
@@ -253,15 +265,26 @@ void born_fwd16_doc_kernel(FwdArgs p) {
     // key0h + 4 g + 8 i + k (register 4 i + k) is masked when it lies past
     // the lane's row (causal) or belongs to another document (kd: this
     // stage's key document ids).
-    auto apply_mask = [&](f32x16& s, int qb, int key0h, const int32_t* kd) __attribute__((always_inline)) {
-        const int lim = causal ? qrow[qb] - (key0h + 4 * g) : INT_MAX;
+    // A tile of a single document (single, uniform) needs no id compare: the
+    // lane's row sees its keys iff it is in that document (vis), folded into
+    // the causal limit.
+    auto apply_mask = [&](f32x16& s, int qb, int key0h, const int32_t* kd, bool single, bool vis)
+        __attribute__((always_inline)) {
+        int lim = causal ? qrow[qb] - (key0h + 4 * g) : INT_MAX;
+        if (single) {
+            if (!vis) lim = -1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int4 d4 = *reinterpret_cast<const int4*>(kd + 4 * g + 8 * i);
-            const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+            for (int r = 0; r < 16; ++r)
+                if (8 * (r >> 2) + (r & 3) > lim) s[r] = 0.f;
+        } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (8 * i + k > lim || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
+            for (int i = 0; i < 4; ++i) {
+                const int4 d4 = *reinterpret_cast<const int4*>(kd + 4 * g + 8 * i);
+                const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (8 * i + k > lim || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
+            }
         }
     };
 
@@ -307,7 +330,7 @@ void born_fwd16_doc_kernel(FwdArgs p) {
     // the loop costs more registers than the wave has): the masks are applied
     // between phases under uniform flags (m0, m1: column block 0 / 1 masked).
     auto tile = [&](const uint8_t* kb, const uint8_t* vb, const int32_t* kd, int key0, bool m0, bool m1, bool l0,
-                    bool l1, bool v0, bool v1) __attribute__((always_inline)) {
+                    bool l1, bool v0, bool v1, bool single) __attribute__((always_inline)) {
         f32x16 s0[NQB], s1[NQB];
         uint32_t pk0[NQB][8], pk1[NQB][8];
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
@@ -316,9 +339,9 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         qk_op(kop, s0);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
-        if (m0) apply_mask(s0[0], 0, key0, kd);
+        if (m0) apply_mask(s0[0], 0, key0, kd, single, v0);
         else if (l0) apply_lane(s0[0], v0);
-        if (m1) apply_mask(s0[1], 1, key0, kd);
+        if (m1) apply_mask(s0[1], 1, key0, kd, single, v1);
         else if (l1) apply_lane(s0[1], v1);
         __builtin_amdgcn_sched_barrier(0);
         read_v(vop0, vb, 0);
@@ -331,9 +354,9 @@ void born_fwd16_doc_kernel(FwdArgs p) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (m0) apply_mask(s1[0], 0, key0 + 32, kd + 32);
+        if (m0) apply_mask(s1[0], 0, key0 + 32, kd + 32, single, v0);
         else if (l0) apply_lane(s1[0], v0);
-        if (m1) apply_mask(s1[1], 1, key0 + 32, kd + 32);
+        if (m1) apply_mask(s1[1], 1, key0 + 32, kd + 32, single, v1);
         else if (l1) apply_lane(s1[1], v1);
         __builtin_amdgcn_sched_barrier(0);
         read_v(vop1, vb, 1);
@@ -386,7 +409,7 @@ void born_fwd16_doc_kernel(FwdArgs p) {
             const bool mixed = td == INT_MIN;
             const bool m0 = rel >= 0 || mixed;
             const bool m1 = rel >= 2 || mixed;
-            tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td);
+            tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td, !mixed);
         }
         __syncthreads();  // the list and the ring are reused by the next chunk
     }
