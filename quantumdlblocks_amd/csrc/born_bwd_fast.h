@@ -342,8 +342,19 @@ __global__ __launch_bounds__(256) void born_bwd_dscale_groups_kernel(BwdArgs p, 
     const int o = blockIdx.x;
     const int BH = p.B * p.H;
     double acc = 0.0;
-    for (int i = threadIdx.x; i < nwg; i += 256)
-        if (!p.per_head_scale || ((i % BH) % p.H) == o) acc += p.dscale_part[i];
+    // Eight independent loads in flight per thread; each thread still adds
+    // its partials in index order (i, i + 256, i + 512, ...).
+    for (int i0 = threadIdx.x; i0 < nwg; i0 += 8 * 256) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * 256;
+            const bool take = i < nwg && (!p.per_head_scale || ((i % BH) % p.H) == o);
+            v[j] = take ? p.dscale_part[i] : 0.0;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += v[j];
+    }
     red[threadIdx.x] = acc;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
