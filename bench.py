@@ -14,17 +14,24 @@ average launch against the HBM roof) and ``cpu_baseline`` (the reference's
 eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
 on this host).
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5|p3|p5]
+    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5|p3|p5|qk3|qk5]
 
 p3 / p5: purified-Born attention (the reference's flash_purified_born_attention,
 gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8) on the C3 / C5 shapes with bf16
 inputs; its kernels contract in fp32 (the reference's P V is an fp32 dot), so
 its roofline is the fp32 MFMA peak.
+
+qk3 / qk5: the fused Q/K prologue (unitary RoPE then L2 normalisation of Q
+and K, attention.py:573-589), forward (qk3) or forward + backward (qk5), on the
+C3 / C5 shapes, bf16, with Q and K read as the (B, T, H, D) projection output
+viewed as (B, H, T, D).  It is a streaming kernel: its metric is algorithmic
+GB/s against the HBM roof.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -52,6 +59,8 @@ CONFIGS = {
 }
 PURIFIED = {"p3", "p5"}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
+# Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
+PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
 
 
 def parse_args():
@@ -61,7 +70,7 @@ def parse_args():
     # ~15% slower over the first ~20 steps than after ~2000 (~0.1 s of load).
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=2000)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(PROLOGUE))
     ap.add_argument("--sets", type=int, default=4, help="input sets rotated over the timed steps")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg")
@@ -220,6 +229,10 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+
+    if args.config in PROLOGUE:
+        prologue_main(args)
         return
 
     import torch
@@ -381,6 +394,182 @@ def main():
             "achieved_tflops_events": round(achieved_tflops, 2),
             "mfma_frac_events": round(achieved_tflops / PEAK_BF16_TFLOPS, 4),
             "visible_pairs_per_head": pairs,
+            "device": torch.cuda.get_device_name(dev),
+            "torch": torch.__version__,
+            "host": platform.node(),
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
+def prologue_tables(T, n, device=None):
+    """Rotary tables of the reference's UnitaryRoPE with its defaults
+    (isometric.py:87-126: base 10000, every frequency active), fp32 (T, n)."""
+    import torch
+
+    freqs = 1.0 / (10000.0 ** (torch.arange(0, n, dtype=torch.float32) / n))
+    ang = torch.outer(torch.arange(T, dtype=torch.float32), freqs)
+    return torch.cos(ang).to(device), torch.sin(ang).to(device)
+
+
+def prologue_cpu_baseline(B, H, T, D, backward, budget_s, seed):
+    """The reference's eager CPU formulation (oracle/qk_prologue_oracle.py
+    ``eager_torch``, bf16 tensor ops) timed on a bounded sample of heads."""
+    import torch
+
+    from oracle.qk_prologue_oracle import eager_torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator("cpu").manual_seed(seed)
+    cos, sin = prologue_tables(T, D // 2)
+    per_run = max(budget_s / 8.0, 0.05)
+
+    def run(n):
+        q = torch.randn(1, n, T, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, n, T, D, generator=g).to(torch.bfloat16)
+        if backward:
+            q.requires_grad_(True)
+            k.requires_grad_(True)
+        t0 = time.perf_counter()
+        qo = eager_torch(q, cos, sin, 1e-12)
+        ko = eager_torch(k, cos, sin, 1e-12)
+        if backward:
+            torch.autograd.backward([qo, ko], [torch.ones_like(qo), torch.ones_like(ko)])
+        return time.perf_counter() - t0
+
+    run(1)
+    one = run(1)
+    n = int(max(1, min(B * H, per_run / max(one, 1e-6))))
+    for _ in range(3):
+        run(n)
+    times = sorted(run(n) for _ in range(5))
+    med = times[len(times) // 2]
+    rows = 2 * n * T
+    per_row = (2 * D * 2 + 4) + ((3 * D * 2 + 4) if backward else 0)
+    return {
+        "value": rows * per_row / med / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"Q and K of {n} of the {B * H} (b,h) heads, bf16, eager torch "
+                   f"(attention.py:574-589 restated{', with autograd backward' if backward else ''}), "
+                   f"median of 5 runs after 3 warm-ups, {med * 1e3:.1f} ms per run"),
+        "seconds_per_run": med,
+        "speedup_of_gpu": None,
+    }
+
+
+def prologue_main(args):
+    import torch
+
+    from quantumdlblocks_amd import _native
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    B, H, T, D, backward = PROLOGUE[args.config]
+    steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
+    code = _native.DTYPE_BF16
+    cos, sin = prologue_tables(T, D // 2, dev)
+    nf, ld = cos.shape[1], cos.stride(0)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    # (B, T, H, D) projection outputs viewed as (B, H, T, D): strides (T H D, D, H D).
+    st = (ctypes.c_int64 * 3)(T * H * D, D, H * D)
+    cst = (ctypes.c_int64 * 3)(H * T * D, T * D, D)
+    sets = []
+    g = torch.Generator("cpu").manual_seed(args.seed)
+    for i in range(max(1, args.sets)):
+        q = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+        k = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(dev)
+        qo, ko = torch.empty(B, H, T, D, dtype=torch.bfloat16, device=dev), torch.empty(B, H, T, D, dtype=torch.bfloat16, device=dev)
+        qr, kr = torch.empty(B, H, T, device=dev), torch.empty(B, H, T, device=dev)
+        if backward:
+            gq = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(dev)
+            gk = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(dev)
+            dq, dk = torch.empty_like(q), torch.empty_like(k)
+        else:
+            gq = gk = dq = dk = None
+        sets.append((q, k, qo, ko, qr, kr, gq, gk, dq, dk))
+
+    def fwd(s):
+        q, k, qo, ko, qr, kr = s[:6]
+        rc = lib.qdl_flash_born_qk_prologue_fwd(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st,
+                                                cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12,
+                                                qo.data_ptr(), ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), stream)
+        _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
+
+    def bwd(s):
+        q, k, qo, ko, qr, kr, gq, gk, dq, dk = s
+        rc = lib.qdl_flash_born_qk_prologue_bwd(code, B, H, T, D, gq.data_ptr(), gk.data_ptr(), qo.data_ptr(),
+                                                ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), cos.data_ptr(),
+                                                sin.data_ptr(), nf, ld, dq.data_ptr(), st, dk.data_ptr(), st, stream)
+        _native.check(rc, "qdl_flash_born_qk_prologue_bwd")
+
+    def step(i, rotate=True):
+        s = sets[i % len(sets)] if rotate else sets[0]
+        fwd(s)
+        if backward:
+            bwd(s)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    def timed(n_steps, rotate=True):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for i in range(n_steps):
+            step(i, rotate)
+        ev1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_steps, ev0.elapsed_time(ev1) / 1e3 / n_steps
+
+    wall_step, ev_step = timed(steps, True)
+    hot_wall, hot_ev = timed(steps, False)
+    for s in sets:
+        assert torch.isfinite(s[2].float()).all() and torch.isfinite(s[3].float()).all(), "non-finite output"
+    del cst
+
+    rows = 2 * B * H * T
+    table = T * nf * 4 * 2
+    fwd_bytes = rows * (2 * D * 2 + 4) + table  # read q, k; write q', k' and 1/norm; read the tables
+    bwd_bytes = rows * (3 * D * 2 + 4) + table  # read dq', dk', q', k', 1/norm; write dq, dk
+    nbytes = fwd_bytes + (bwd_bytes if backward else 0)
+    value = nbytes / wall_step / 1e9
+    achieved = nbytes / ev_step / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": load_traffic(args.config)}
+    cpu = None
+    if not (args.no_cpu_baseline or args.profile):
+        cpu = prologue_cpu_baseline(B, H, T, D, backward, args.cpu_seconds, args.seed)
+        cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
+    name = "fwd+bwd" if backward else "fwd"
+    line = {
+        "metric": f"Q/K prologue (RoPE + L2 normalise) {name} GB/s, B{B} H{H} T{T} hd{D}",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q, K%s; %d rotated input sets)" % (", dQ', dK'" if backward else "", len(sets)),
+        "config": {"workload": args.config, "batch": B, "heads": H, "seq_len": T, "head_dim": D,
+                   "rope_pairs": nf, "input_layout": "(B, T, H, D) viewed as (B, H, T, D)",
+                   "backward": backward, "eps": 1e-12},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "detail": {
+            "kernel_us_per_step_events": round(ev_step * 1e6, 3),
+            "hot_kernel_us_per_step_events": round(hot_ev * 1e6, 3),
+            "hot_gbs": round(nbytes / hot_wall / 1e9, 1),
+            "algorithmic_bytes": nbytes,
             "device": torch.cuda.get_device_name(dev),
             "torch": torch.__version__,
             "host": platform.node(),

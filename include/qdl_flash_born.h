@@ -48,6 +48,8 @@ extern "C" {
 #define QDL_BORN_E_WINDOW (-7)
 #define QDL_BORN_E_WORKSPACE (-8)
 #define QDL_BORN_E_TAU (-9)
+#define QDL_BORN_E_TABLE (-10)
+#define QDL_BORN_E_ROPEDIM (-11)
 
 typedef struct ihipStream_t *qdl_stream_t; /* == hipStream_t */
 
@@ -145,6 +147,63 @@ int qdl_flash_purified_born_bwd(int dtype, int64_t B, int64_t H, int64_t T,
                                 void *dk, void *dv, float *dscale, float *dtau,
                                 void *workspace, int64_t workspace_bytes,
                                 qdl_stream_t stream);
+
+/*
+ * Q/K prologue of SubspaceProjectorBornAttention.forward (attention.py:573-589,
+ * without the optional wave filter and partial key offset), fused into one
+ * pass per tensor:
+ *   x' = l2_normalize(apply_unitary_rope(x, c, s), eps)       for x in {q, k}
+ * with apply_unitary_rope (functional.py:104-121) rotating column pairs
+ * (i, i + D/2):  y_i = x_i c_ti - x_{i+D/2} s_ti,  y_{i+D/2} = x_i s_ti + x_{i+D/2} c_ti,
+ * and l2_normalize (functional.py:36-80): x' = y / sqrt(sum y^2 + eps), the
+ * sum in fp32.  For 16-bit dtypes every product, sum and c, s themselves are
+ * rounded to the dtype as the reference's tensor ops round them; the norm is
+ * formed in fp32 from the rounded y.
+ *
+ * Row tensors (q, k, dq, dk) are (B, H, T, D) with element strides
+ * strides[0..2] for b, h, t and unit stride along D, so the (B, T, H, D)
+ * output of a Q/K projection is passed without a transposing copy.  q_out,
+ * k_out, dq_out, dk_out are contiguous (B, H, T, D); q_rinv, k_rinv are
+ * contiguous (B, H, T) fp32 holding 1 / sqrt(sum y^2 + eps) per row.
+ * cos_table, sin_table: fp32, row t (t = 0 .. T-1) at t * table_ld; column
+ * i < n_freq holds the angle table for pair i; pairs i >= n_freq are rotated
+ * by angle 0 (cos 1, sin 0), the reference's padding of short tables
+ * (attention.py:574-582).  cos_table == NULL skips the rotation.
+ * Either tensor may be left out by passing NULL for all of its pointers.
+ * D must be even, 2 <= D <= 256.
+ */
+
+/* Forward.  Replaces the apply_unitary_rope and l2_normalize calls on Q and K
+ * at attention.py:583-589 (and the .contiguous() copies at attention.py:516-517
+ * when the projection output is passed strided). */
+int qdl_flash_born_qk_prologue_fwd(int dtype, int64_t B, int64_t H, int64_t T,
+                                   int64_t D, const void *q,
+                                   const int64_t *q_strides, const void *k,
+                                   const int64_t *k_strides,
+                                   const float *cos_table,
+                                   const float *sin_table, int64_t n_freq,
+                                   int64_t table_ld, double eps, void *q_out,
+                                   void *k_out, float *q_rinv, float *k_rinv,
+                                   qdl_stream_t stream);
+
+/* Backward: given the gradients dq_out, dk_out of q_out, k_out, the forward's
+ * outputs and q_rinv, k_rinv, writes dq, dk (strided like the forward's
+ * inputs):  g = (dx' - (dx'.x') x') rinv  (functional.py:50-57, rounded to
+ * the dtype), then the transposed rotation  dx_i = g_i c + g_{i+D/2} s,
+ * dx_{i+D/2} = g_{i+D/2} c - g_i s, each product and sum rounded to the dtype
+ * as autograd's bf16 / fp16 ops round them.  Replaces the autograd backward of
+ * the calls at attention.py:583-589. */
+int qdl_flash_born_qk_prologue_bwd(int dtype, int64_t B, int64_t H, int64_t T,
+                                   int64_t D, const void *dq_out,
+                                   const void *dk_out, const void *q_out,
+                                   const void *k_out, const float *q_rinv,
+                                   const float *k_rinv,
+                                   const float *cos_table,
+                                   const float *sin_table, int64_t n_freq,
+                                   int64_t table_ld, void *dq,
+                                   const int64_t *dq_strides, void *dk,
+                                   const int64_t *dk_strides,
+                                   qdl_stream_t stream);
 
 #ifdef __cplusplus
 }

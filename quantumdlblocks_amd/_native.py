@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "qdl_flash_purified_born_fwd",
     "qdl_flash_purified_born_bwd_workspace_size",
     "qdl_flash_purified_born_bwd",
+    "qdl_flash_born_qk_prologue_fwd",
+    "qdl_flash_born_qk_prologue_bwd",
 )
 
 
@@ -90,6 +92,20 @@ def _bind(lib: ctypes.CDLL) -> None:
         _dbl, _ptr, _int, _i64,            # eps_base, doc_ids, is_causal, window_size
         _ptr, _ptr, _ptr, _ptr, _ptr,      # dq, dk, dv, dscale, dtau
         _ptr, _i64, _ptr,                  # workspace, workspace_bytes, stream
+    ]
+    lib.qdl_flash_born_qk_prologue_fwd.restype = _int
+    lib.qdl_flash_born_qk_prologue_fwd.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr,            # q, q_strides, k, k_strides
+        _ptr, _ptr, _i64, _i64, _dbl,      # cos, sin, n_freq, table_ld, eps
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # q_out, k_out, q_rinv, k_rinv, stream
+    ]
+    lib.qdl_flash_born_qk_prologue_bwd.restype = _int
+    lib.qdl_flash_born_qk_prologue_bwd.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # dq_out, dk_out, q_out, k_out, q_rinv, k_rinv
+        _ptr, _ptr, _i64, _i64,            # cos, sin, n_freq, table_ld
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # dq, dq_strides, dk, dk_strides, stream
     ]
 
 

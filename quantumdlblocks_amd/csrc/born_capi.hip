@@ -47,6 +47,8 @@ const char* qdl_flash_born_strerror(int code) {
         case QDL_BORN_E_WINDOW: return "window_size out of range";
         case QDL_BORN_E_WORKSPACE: return "workspace missing or too small";
         case QDL_BORN_E_TAU: return "tau must hold 1 value or exactly H values";
+        case QDL_BORN_E_TABLE: return "rotary table invalid (n_freq above D/2, table_ld below n_freq, or sin missing)";
+        case QDL_BORN_E_ROPEDIM: return "Q/K prologue head dim must be even and in [2, 256]";
         default: break;
     }
     if (code > 0) return hipGetErrorString((hipError_t)code);

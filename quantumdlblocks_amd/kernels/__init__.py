@@ -11,6 +11,7 @@ from .flash_born import (
     get_mi355x_launch_meta,
     get_rdna4_autotune_configs,
 )
+from .qk_prologue import fused_qk_rope_l2_normalize
 
 __all__ = [
     "HAS_HIP_KERNELS",
@@ -18,6 +19,7 @@ __all__ = [
     "IS_HIP",
     "flash_born_attention",
     "flash_purified_born_attention",
+    "fused_qk_rope_l2_normalize",
     "get_flash_born_launch_meta",
     "get_mi355x_launch_meta",
     "get_rdna4_autotune_configs",

@@ -221,3 +221,29 @@ def test_integration_install_rebinds_reference_names():
                 sys.modules.pop(n, None)
             else:
                 sys.modules[n] = m
+
+
+def test_prologue_cpu_tensors_take_the_eager_formulation():
+    """On CPU tensors the fused prologue is the reference's eager
+    apply_unitary_rope + l2_normalize; it agrees with the oracle's rounding
+    model (rows within one bf16 ulp: only the norm's summation order differs)."""
+    import numpy as np
+
+    from oracle import qk_prologue_oracle as po
+    from quantumdlblocks_amd.kernels.qk_prologue import fused_qk_rope_l2_normalize
+
+    g = torch.Generator().manual_seed(3)
+    B, H, T, D, n = 2, 3, 20, 64, 24
+    q = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16)
+    ang = torch.outer(torch.arange(T, dtype=torch.float32), 0.1 * torch.arange(1, n + 1).float())
+    cos, sin = torch.cos(ang).view(1, 1, T, n), torch.sin(ang).view(1, 1, T, n)
+    qo, ko = fused_qk_rope_l2_normalize(q, k, cos, sin, eps=1e-12)
+    for x, o in ((q, qo), (k, ko)):
+        want, _ = po.prologue_forward(x.float().numpy(), cos[0, 0].numpy(), sin[0, 0].numpy(),
+                                      1e-12, "bf16")
+        got = o.float().numpy()
+        assert o.dtype == torch.bfloat16
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
+    with pytest.raises(ValueError):
+        fused_qk_rope_l2_normalize(q, k[:, :2])

@@ -120,3 +120,45 @@ def test_backward_argument_validation(lib):
     assert bwd(ws=None) == m["QDL_BORN_E_WORKSPACE"]
     assert bwd(ws_bytes=ws - 4) == m["QDL_BORN_E_WORKSPACE"]
     assert bwd(ptr=20) == m["QDL_BORN_E_ALIGN"]
+
+
+def test_qk_prologue_argument_validation(lib):
+    """Rejections of the fused Q/K prologue entry points (before any launch)."""
+    m = _header_macros()
+    st = (ctypes.c_int64 * 3)(16 * 64 * 2, 16 * 64, 64)
+
+    def fwd(**over):
+        a = dict(dtype=2, B=1, H=2, T=16, D=64, q=16, qs=st, k=16, ks=st, cos=16, sin=16,
+                 nf=32, ld=32, eps=1e-12, qo=16, ko=16, qr=16, kr=16)
+        a.update(over)
+        return lib.qdl_flash_born_qk_prologue_fwd(
+            a["dtype"], a["B"], a["H"], a["T"], a["D"], a["q"], a["qs"], a["k"], a["ks"],
+            a["cos"], a["sin"], a["nf"], a["ld"], a["eps"], a["qo"], a["ko"], a["qr"], a["kr"], None)
+
+    def bwd(**over):
+        a = dict(dtype=2, B=1, H=2, T=16, D=64, gq=16, gk=16, qo=16, ko=16, qr=16, kr=16,
+                 cos=16, sin=16, nf=32, ld=32, dq=16, dqs=st, dk=16, dks=st)
+        a.update(over)
+        return lib.qdl_flash_born_qk_prologue_bwd(
+            a["dtype"], a["B"], a["H"], a["T"], a["D"], a["gq"], a["gk"], a["qo"], a["ko"],
+            a["qr"], a["kr"], a["cos"], a["sin"], a["nf"], a["ld"], a["dq"], a["dqs"], a["dk"],
+            a["dks"], None)
+
+    for call in (fwd, bwd):
+        assert call(dtype=4) == m["QDL_BORN_E_DTYPE"]
+        assert call(T=-1) == m["QDL_BORN_E_SHAPE"]
+        assert call(D=63) == m["QDL_BORN_E_ROPEDIM"]
+        assert call(D=258) == m["QDL_BORN_E_ROPEDIM"]
+        assert call(D=0) == m["QDL_BORN_E_ROPEDIM"]
+        assert call(nf=33) == m["QDL_BORN_E_TABLE"]
+        assert call(ld=16) == m["QDL_BORN_E_TABLE"]
+        assert call(sin=None) == m["QDL_BORN_E_NULL"]
+        assert call(B=0) == 0  # empty: nothing to launch
+    assert fwd(eps=-1.0) == m["QDL_BORN_E_SHAPE"]
+    assert fwd(qo=None) == m["QDL_BORN_E_NULL"]
+    assert fwd(kr=None) == m["QDL_BORN_E_NULL"]
+    assert fwd(qs=None) == m["QDL_BORN_E_NULL"]
+    assert fwd(q=None, k=None) == 0  # neither tensor given
+    assert bwd(qo=None) == m["QDL_BORN_E_NULL"]
+    assert bwd(dks=None) == m["QDL_BORN_E_NULL"]
+    assert bwd(gq=None, gk=None) == 0
