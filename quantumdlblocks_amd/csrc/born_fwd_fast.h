@@ -47,6 +47,7 @@
 #include <type_traits>
 
 #include "born_common.h"
+#include "purified_args.h"
 
 namespace qdl {
 
@@ -114,10 +115,21 @@ struct FastFwdCfg {
 __host__ __device__ inline int fast_fwd_nmb(int T, int BM) { return (T + BM - 1) / BM; }
 __host__ __device__ inline int fast_fwd_npair(int T, int BM) { return (fast_fwd_nmb(T, BM) + 1) / 2; }
 
-template <class E, int DP, int MODE>
+// PUR selects the purified-Born weights (flash_born.py:696-811): with r the
+// raw overlap, p = relu(gamma (r - tau))^4 + eps_base relu(r)^2 in fp32,
+// Z = sum p + eps in fp32, O = sum p v / Z written in fp32.  The reference
+// contracts P V in fp32; here each weight is split into two bf16 terms,
+// p = hi + lo with hi = bf16(p), lo = bf16(p - hi) (|p - hi - lo| <= 2^-17 p),
+// and both go through the bf16 MFMA against the exact bf16 V, so the product
+// keeps ~16 bits of each weight at bf16 MFMA rate.  Masked and out-of-range
+// pairs have their weight zeroed (a zero overlap still weighs
+// relu(-gamma tau)^4 when tau < 0).  Output rows are stored straight from the
+// accumulators.
+template <class E, int DP, int MODE, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_fwd16_fast_kernel(FwdArgs p) {
+void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
     constexpr int KS = DP / 16;
@@ -169,7 +181,14 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
+    float pg = 0.f, pgt = 0.f, pse = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        pse = sqrtf(p.eps_base);
+    }
     // fp16: square min(|s|, 1) r, so no weight overflows unless the
     // reference's (s r)^2 does too; p = s2 * (accumulated weight).
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
@@ -208,6 +227,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     // Row of MFMA column c within a block: slice 2 qb + c / 16, row 16 w + c % 16.
     const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
     int qrow[NQB];  // query row of this lane's column in block qb (current item)
+    int mlim[NQB];  // last visible key of a masked column block: the query row (causal) or T - 1
     u32x4 qr[NQB][KS];
     f32x16 oacc[DB][NQB];
     float zacc[NQB][2];
@@ -246,9 +266,40 @@ void born_fwd16_fast_kernel(FwdArgs p) {
 
     // Elementwise pass over one 32-key block of S^T: p' = relu(x|x|) packed,
     // z += p'.  Masked keys (key > query row) are zeroed first.
-    auto elementwise = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8], auto m0, auto m1, int kbase)
-        __attribute__((always_inline)) {
+    constexpr int PW = PUR ? 8 : 1;  // packed low parts of the purified weights
+    auto elementwise = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8], uint32_t (&pl)[NQB][PW], auto m0, auto m1,
+                           int kbase) __attribute__((always_inline)) {
         constexpr int M[NQB] = {decltype(m0)::value, decltype(m1)::value};
+        if constexpr (PUR) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                if (M[qb] == kSkip) continue;
+                const int lim = mlim[qb] - kbase;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float w[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float x = s[qb][2 * j + e];
+                        const float t = fmaf(x, pg, pgt);
+                        const float u = __int_as_float(max(__float_as_int(t), 0));
+                        const float bq = __int_as_float(max(__float_as_int(x * pse), 0));
+                        const float u2 = u * u;
+                        float pw = fmaf(u2, u2, bq * bq);
+                        if (M[qb] == kMasked) {
+                            const int r = 2 * j + e;
+                            if (8 * (r >> 2) + (r & 3) > lim) pw = 0.f;
+                        }
+                        w[e] = pw;
+                    }
+                    zacc[qb][0] += w[0] + w[1];
+                    const uint32_t hi = E::pack(w[0], w[1]);
+                    pk[qb][j] = hi;
+                    pl[qb][j] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             if (M[qb] == kSkip) continue;
@@ -300,8 +351,8 @@ void born_fwd16_fast_kernel(FwdArgs p) {
             for (int qb = 0; qb < NQB; ++qb)
                 if (M[qb] != kSkip) s[qb] = E::mfma(ops[ks], qr[qb][ks], s[qb]);
     };
-    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8], auto m0, auto m1)
-        __attribute__((always_inline)) {
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8], const uint32_t (&pl)[NQB][PW],
+                     auto m0, auto m1) __attribute__((always_inline)) {
         constexpr int M[NQB] = {decltype(m0)::value, decltype(m1)::value};
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
@@ -312,6 +363,11 @@ void born_fwd16_fast_kernel(FwdArgs p) {
                     if (M[qb] == kSkip) continue;
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
                     oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
+                    if constexpr (PUR) {
+                        const u32x4 bl = {pl[qb][4 * hh % PW], pl[qb][(4 * hh + 1) % PW], pl[qb][(4 * hh + 2) % PW],
+                                          pl[qb][(4 * hh + 3) % PW]};
+                        oacc[db][qb] = E::mfma(ops[hh][db], bl, oacc[db][qb]);
+                    }
                 }
     };
     auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, auto m0, auto m1)
@@ -319,6 +375,10 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         constexpr int NA = (decltype(m0)::value != kSkip) + (decltype(m1)::value != kSkip);
         f32x16 s0[NQB], s1[NQB];
         uint32_t pk0[NQB][8], pk1[NQB][8];
+        uint32_t pl0[NQB][PW], pl1[NQB][PW];
+        // VALU instructions interleaved per MFMA (the purified weights cost
+        // about four times the Born ones, and PV issues twice the MFMAs).
+        constexpr int V2 = PUR ? 40 : 10, V3 = PUR ? 20 : 10;
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
         // 1 (MFMA only: issued at raised wave priority, so the two
         // workgroups sharing a SIMD hand the matrix pipe back and forth
@@ -331,28 +391,30 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         __builtin_amdgcn_s_setprio(0);
         read_v(vop0, vb, 0);
         qk_op(kop1, s1, m0, m1);
-        elementwise(s0, pk0, m0, m1, key0 + 4 * g);
+        elementwise(s0, pk0, pl0, m0, m1, key0 + 4 * g);
 #pragma unroll
         for (int i = 0; i < KS * NA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x002, V2, 0);  // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
         }
         __builtin_amdgcn_sched_barrier(0);
-        // 3
-        read_v(vop1, vb, 1);
-        pv_op(vop0, pk0, m0, m1);
-        elementwise(s1, pk1, m0, m1, key0 + 32 + 4 * g);
+        // 3 (purified: V of keys 32-63 is read at the start of 4 instead,
+        // which keeps the phase within the register budget)
+        if constexpr (!PUR) read_v(vop1, vb, 1);
+        pv_op(vop0, pk0, pl0, m0, m1);
+        elementwise(s1, pk1, pl1, m0, m1, key0 + 32 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 2 * DB * NA; ++i) {
+        for (int i = 0; i < (PUR ? 4 : 2) * DB * NA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x002, 10, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, V3, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
         }
         __builtin_amdgcn_sched_barrier(0);
         // 4 (MFMA only)
         __builtin_amdgcn_s_setprio(1);
-        pv_op(vop1, pk1, m0, m1);
+        if constexpr (PUR) read_v(vop1, vb, 1);
+        pv_op(vop1, pk1, pl1, m0, m1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -376,6 +438,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     };
 
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    float* __restrict__ O32 = reinterpret_cast<float*>(p.o) + base;  // purified: fp32 rows
     float* __restrict__ Zp = p.z + (size_t)bh * T;
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
@@ -443,9 +506,32 @@ void born_fwd16_fast_kernel(FwdArgs p) {
             if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
         }
     };
+    // Purified: O = acc / (Z + eps) and Z + eps, fp32, straight from the
+    // accumulators (lane: one query row, 4 consecutive columns per store).
+    auto store_pur = [&](int mb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float zl = zacc[qb][0] + zacc[qb][1];
+            const float zd = zl + __shfl_xor(zl, 32) + p.eps;
+            const int qi = mb * BM + 128 * qb + lrow;
+            if (qi < T) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x16& o = oacc[db][qb];
+                        const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
+                        __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                    }
+                if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
+            }
+        }
+    };
     auto start_item = [&](int mb) __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) qrow[qb] = mb * BM + 128 * qb + lrow;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) mlim[qb] = kCaus ? qrow[qb] : T - 1;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -473,7 +559,9 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     const bool early_q = (nitems == 2);
     const int uq = max(1, nt_a - 4);
     auto top = [&](int u) __attribute__((always_inline)) {
-        const bool stores_out = (nitems == 2) && (u == nt_a + 2);
+        // The first item's rows are stored at step nt_a + 1 (Born, from LDS)
+        // or nt_a (purified, from registers); the next step drains them.
+        const bool stores_out = (nitems == 2) && (u == nt_a + (PUR ? 1 : 2));
         const int after = stores_out ? 0 : ((u == uq + 1 && early_q) ? kQLoads : 0) + (u + 1 < ntot ? kTileLoads : 0);
         if (after >= kQLoads + kTileLoads)
             wait_vmcnt<kQLoads + kTileLoads>();
@@ -484,7 +572,7 @@ void born_fwd16_fast_kernel(FwdArgs p) {
         __syncthreads();
         if (u == uq && early_q) issue_q(mb_b);
         if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
-        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
+        if (!PUR && nitems == 2 && u == nt_a + 1) flush(mb_a);
     };
 
     issue_q(mb_a);
@@ -495,11 +583,16 @@ void born_fwd16_fast_kernel(FwdArgs p) {
     for (int it = 0; it < nitems; ++it) {
         const int mb = it ? mb_b : mb_a;
         const int nt = it ? ntot - nt_a : nt_a;
-        const int t0 = kCaus ? min(mb * (BM / BN), nt) : nt;
+        // Purified, non-causal, T not a multiple of the tile: the last tile
+        // masks the keys past T.
+        const int t0 = kCaus ? min(mb * (BM / BN), nt) : ((PUR && T % BN) ? nt - 1 : nt);
         // The item's first step: the previous item's rows go out right
         // after this barrier, a full step before the next wait.
         top(u);
-        if (it > 0) {
+        if constexpr (PUR) {
+            if (it > 0) store_pur(mb_a);
+            load_q();
+        } else if (it > 0) {
             pack();
             load_q();  // before the previous item's rows overwrite this wave's Q rows
             put_lds();
@@ -540,12 +633,25 @@ void born_fwd16_fast_kernel(FwdArgs p) {
                 else
                     tile(kb, vb, t * BN, Skip{}, Masked{});
             }
+        } else if constexpr (PUR) {
+            for (; t < nt; ++t, ++u) {
+                if (!at_top) top(u);
+                at_top = false;
+                const uint8_t *kb, *vb;
+                stage(u, kb, vb);
+                read_k(kop, kb, 0);
+                tile(kb, vb, t * BN, Masked{}, Masked{});
+            }
         }
     }
-    if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
-    pack();
-    put_lds();
-    flush(nitems == 2 ? mb_b : mb_a);
+    if constexpr (PUR) {
+        store_pur(nitems == 2 ? mb_b : mb_a);
+    } else {
+        if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
+        pack();
+        put_lds();
+        flush(nitems == 2 ? mb_b : mb_a);
+    }
 }
 
 template <class E, int DP, int MODE>
@@ -558,6 +664,19 @@ hipError_t launch_fwd16_fast(const FwdArgs& a, hipStream_t st) {
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     const dim3 grid(npair < 512u ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<E, DP, MODE>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+// Purified-Born forward through the same kernel (bf16, D == 64, dense or
+// causal, no window / documents).
+template <int MODE>
+hipError_t launch_purified_fwd_fast(const PurArgs& a, hipStream_t st) {
+    using C = FastFwdCfg<64>;
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
+    const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
+    const dim3 grid(npair < 512u ? nsingle : npair);
+    hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // Purified-Born kernel instantiations: element type x padded head dim
 // (32, 64, 128, 256; the host zero-pads D to a multiple of 8 and the kernels
 // bound-check columns past D).
+#include "born_fwd_fast.h"
 #include "purified.h"
 
 namespace qdl {
@@ -9,6 +10,9 @@ inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <
 
 template <class IN>
 static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
+    // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
+    if (std::is_same<IN, BF16>::value && a.D == 64 && a.window == 0 && a.doc == nullptr)
+        return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);

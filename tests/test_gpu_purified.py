@@ -109,3 +109,72 @@ def test_purified_deterministic_and_default_args(cuda_device):
     assert torch.equal(a, b)
     O_ref, _ = orc.purified_forward(f64(q), f64(k), f64(v), 8.0, 0.0625, 0.05, True, 1e-8)
     assert rel_err(f64(a), O_ref) <= 2e-2
+
+
+# ---------------------------------------------------------------------------
+# The bf16 D = 64 forward (dense or causal, no window / documents) runs the
+# bf16-MFMA kernel with each weight split into two bf16 terms.  Its error is
+# that of fp32 accumulation (the split keeps ~16 bits of every weight), so it
+# is held to 1e-4 against the float64 oracle on the same bf16 inputs (not just
+# the 2e-2 bf16 bar), and to the fp32-MFMA kernel, which the same inputs reach
+# through an all-zero document id tensor (one document: the same visibility).
+# ---------------------------------------------------------------------------
+FAST_CASES = [
+    # (B, H, T, causal, scale, tau, eps_base, eps, std)
+    (2, 3, 130, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 200, False, 8.0, -0.1, 0.05, 1e-8, 0.3),   # dense, T % 64 != 0, tau < 0: keys past T masked
+    (2, 2, 64, False, [4.0, 9.0], [0.0, 0.2], 0.2, 1e-6, 0.3),
+    (1, 1, 1, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 600, True, [8.0, 5.0], [-0.05, 0.1], 0.05, 1e-8, 0.2),
+    (1, 1, 1000, False, 8.0, -0.2, 0.05, 1e-8, 0.2),
+]
+
+
+def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None):
+    from quantumdlblocks_amd import _native
+
+    lib = _native.load()
+    B, H, T, D = q.shape
+    out = torch.empty((B, H, T, D), dtype=torch.float32, device=q.device)
+    z = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    sc = torch.tensor(np.atleast_1d(np.asarray(scale, dtype=np.float32)), device=q.device)
+    ta = torch.tensor(np.atleast_1d(np.asarray(tau, dtype=np.float32)), device=q.device)
+    rc = lib.qdl_flash_purified_born_fwd(
+        _native.DTYPE_BF16, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), z.data_ptr(),
+        sc.data_ptr(), sc.numel(), ta.data_ptr(), ta.numel(), float(eps_base),
+        doc.data_ptr() if doc is not None else None, int(causal), 0, float(eps),
+        torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(rc, "qdl_flash_purified_born_fwd")
+    torch.cuda.synchronize()
+    return out, z
+
+
+@pytest.mark.parametrize("case", FAST_CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-{'causal' if c[3] else 'dense'}")
+def test_purified_fast_forward(cuda_device, case):
+    B, H, T, causal, scale, tau, eps_base, eps, std = case
+    print(f"purified fast fwd case B{B} H{H} T{T} causal={causal}", flush=True)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 64), seed=T + 5, std=std, n=3,
+                                                          dtype=torch.bfloat16))
+    out, z = _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau),
+                                        eps_base, causal, eps)
+    assert rel_err(f64(out), O_ref) <= 1e-4, rel_err(f64(out), O_ref)
+    assert np.max(np.abs(f64(z) - Z_ref) / Z_ref) <= 1e-4
+    zero_doc = torch.zeros((B, T), dtype=torch.int32, device=cuda_device)
+    out_g, z_g = _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=zero_doc)
+    assert rel_err(f64(out), f64(out_g)) <= 1e-4
+    assert np.max(np.abs(f64(z) - f64(z_g)) / f64(z_g)) <= 1e-4
+
+
+def test_purified_fast_forward_paired_launch(cuda_device):
+    """The C3 shape (B16 H16 T1024): workgroups take two query blocks each;
+    checked on sampled heads against the oracle."""
+    B, H, T = 16, 16, 1024
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 64), seed=3, std=0.125, n=3,
+                                                          dtype=torch.bfloat16))
+    out, z = _pur_fwd_abi(q, k, v, 8.0, 0.0625, 0.05, True, 1e-8)
+    for b, h in ((0, 0), (7, 5), (15, 15), (3, 12)):
+        O_ref, Z_ref = orc.purified_forward(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, h:h + 1]),
+                                            f64(v[b:b + 1, h:h + 1]), 8.0, 0.0625, 0.05, True, 1e-8)
+        assert rel_err(f64(out[b:b + 1, h:h + 1]), O_ref) <= 1e-4
+        assert np.max(np.abs(f64(z[b:b + 1, h:h + 1]) - Z_ref) / Z_ref) <= 1e-4
