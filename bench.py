@@ -18,9 +18,9 @@ on this host).
 
 p3 / p5: purified-Born attention (the reference's flash_purified_born_attention,
 gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8) on the C3 / C5 shapes with bf16
-inputs.  The forward runs on bf16 MFMA with each fp32 weight split into two
-bf16 terms (the reference's P V is an fp32 dot); the backward kernels contract
-in fp32, so p5's roofline is the fp32 MFMA peak.
+inputs, on bf16 MFMA: the forward splits each fp32 weight into two bf16 terms
+(the reference's P V is an fp32 dot); the backward contracts the bf16-rounded
+weights as the reference does.
 
 qk3 / qk5: the fused Q/K prologue (unitary RoPE then L2 normalisation of Q
 and K, attention.py:573-589), forward (qk3) or forward + backward (qk5), on the
@@ -345,9 +345,9 @@ def main():
     achieved_tflops = flops / ev_step / 1e12
     achieved_gbs = nbytes / ev_step / 1e9
     ai = flops / nbytes
-    # The purified forward runs on bf16 MFMA (weights split into two bf16
-    # terms); its backward kernels still contract in fp32.
-    mfma_peak = PEAK_FP32_MFMA_TFLOPS if (purified and backward) else PEAK_BF16_TFLOPS
+    # Every kernel of these configs contracts on bf16 MFMA (the purified
+    # forward splits each fp32 weight into two bf16 terms).
+    mfma_peak = PEAK_BF16_TFLOPS
     hbm_bound = ai * PEAK_HBM_GBS / 1e3 < mfma_peak
     if hbm_bound:
         roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -375,8 +375,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("bf16 fwd, fp32 bwd (bf16 inputs)" if backward else "bf16 (fp32 weights as two bf16 terms)")
-        if purified else "bf16",
+        "dtype": "bf16 (fp32 weights as two bf16 terms in the forward)" if purified else "bf16",
         "data": "synthetic (seeded N(0,%g) Q, K, V; %d rotated input sets)" % (cfg[4] ** 2, len(sets)),
         "config": {
             "workload": args.config + (" (headline)" if args.config == "c3" else ""),

@@ -30,10 +30,17 @@
 
 namespace qdl {
 
-template <class E, int DP, int MODE>
+// PUR: purified-Born gradients (flash_born.py:950-1061): with r the raw
+// overlap, u = relu(gamma (r - tau)), b = relu(r) (zero where masked),
+// dR = (4 gamma u^3 + 2 eps_base b) dP rounded to bf16 as the reference's
+// `.to(k.dtype)` rounds it; O is the forward's fp32 output.  The dscale
+// closed form is Born's only: the purified dgamma / dtau come from the dK/dV
+// kernel.
+template <class E, int DP, int MODE, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_bwd16_dq_fast_kernel(BwdArgs p) {
+void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
@@ -72,10 +79,18 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
     // min(|s|, 1) (see E::kScaleInSquare); the epilogue divides it back out.
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    // Purified: t = gamma r - gamma tau; dR / dP = 4 gamma u^3 + 2 eps_base b.
+    float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+    }
 
     // Stationary operands: sign-flipped Q and dO rows of this lane's queries.
     // delta_i = dO_i . O_i is formed here from the stored O (each lane holds
@@ -88,7 +103,12 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
     {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
         const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
-        const uint16_t* __restrict__ Og = reinterpret_cast<const uint16_t*>(p.o) + base;
+        const uint16_t* __restrict__ Og = nullptr;
+        const float* __restrict__ Og32 = nullptr;
+        if constexpr (PUR)
+            Og32 = p.o_in + base;
+        else
+            Og = reinterpret_cast<const uint16_t*>(p.o) + base;
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             qrow[qb] = R + 128 * qb + lrow;
@@ -108,28 +128,45 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
             if (ok) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const u32x4 o = ldg16(Og + (size_t)qi * DP + (2 * ks + g) * 8);
+                    if constexpr (PUR) {
+                        const f32x4 oa = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * DP + (2 * ks + g) * 8);
+                        const f32x4 ob = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * DP + (2 * ks + g) * 8 + 4);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        dl += E::lo(o[j]) * E::lo(dr[qb][ks][j]) + E::hi(o[j]) * E::hi(dr[qb][ks][j]);
+                        for (int j = 0; j < 4; ++j) {
+                            const float o0 = j < 2 ? oa[2 * j] : ob[2 * j - 4];
+                            const float o1 = j < 2 ? oa[2 * j + 1] : ob[2 * j - 3];
+                            dl += o0 * E::lo(dr[qb][ks][j]) + o1 * E::hi(dr[qb][ks][j]);
+                        }
+                    } else {
+                        const u32x4 o = ldg16(Og + (size_t)qi * DP + (2 * ks + g) * 8);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            dl += E::lo(o[j]) * E::lo(dr[qb][ks][j]) + E::hi(o[j]) * E::hi(dr[qb][ks][j]);
+                    }
                 }
             }
             dl += __shfl_xor(dl, 32);
             const size_t row = (size_t)bh * T + qi;
-            const float zr = ok ? p.z[row] : 1.f;
+            float zr = 1.f;
+            if (ok) {
+                if constexpr (PUR)
+                    zr = p.z_in[row];
+                else
+                    zr = p.z[row];
+            }
             zinv[qb] = ok ? 1.0f / zr : 0.f;
             nd[qb] = ok ? -(dl / zr) : 0.f;
             if (ok && g == 0) {
                 p.ndelta[row] = -dl;
                 p.zinv[row] = zinv[qb];
-                p.delta_z[row] = dl / zr;
+                if constexpr (!PUR) p.delta_z[row] = dl / zr;
             }
         }
     }
     // This workgroup's part of dscale = (2/s) eps sum delta / Z (closed form):
     // its rows' sum, in a fixed order (lanes, then waves), one double per
     // workgroup.
-    {
+    if constexpr (!PUR) {
         __shared__ float s_dz[NW];
         float dz = (g == 0) ? -(nd[0] + nd[1]) : 0.f;
 #pragma unroll
@@ -229,6 +266,28 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
+        if constexpr (PUR) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                const int lim = qrow[qb] - kbase;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float w[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 2 * j + e;
+                        const float x = s[qb][r];
+                        const float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                        const float bb = __int_as_float(max(__float_as_int(x), 0));
+                        const float f = fmaf(p4g, u * u * u, p2e * bb);
+                        float dr_ = f * fmaf(t[qb][r], zinv[qb], nd[qb]);
+                        if (mk[qb] && 8 * (r >> 2) + (r & 3) > lim) dr_ = 0.f;
+                        w[e] = dr_;
+                    }
+                    pk[qb][j] = E::pack(w[0], w[1]);
+                }
+            }
+        } else {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             if (mk[qb]) {
@@ -245,6 +304,7 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
                 const float a1 = __int_as_float(max(__float_as_int(x1), 0));
                 pk[qb][j] = E::pack(a0 * fmaf(t[qb][2 * j], zinv[qb], nd[qb]), a1 * fmaf(t[qb][2 * j + 1], zinv[qb], nd[qb]));
             }
+        }
         }
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -303,7 +363,7 @@ void born_bwd16_dq_fast_kernel(BwdArgs p) {
     // per lane and store 8 whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = 2.f * sc * fabsf(sc) / sq_pre;
+    const float f = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
@@ -392,10 +452,19 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 //       dV^T += dO^T W,  dK^T += Q^T U  (A = dO^T, Q^T transposed reads)
 //   * The finished dK, dV rows are scaled, packed, staged in the idle ring and
 //     written back 16 bytes per lane.
-template <class E, int DP, int MODE>
+// PUR: purified-Born gradients (flash_born.py:812-948): W = p / Z and
+// dR = (4 gamma u^3 + 2 eps_base b) dP, both rounded to bf16 before their
+// contractions as in the reference; each workgroup also writes its partial
+// sums of dgamma = 4 sum u^3 dP (r - tau) and dtau = -4 gamma sum u^3 dP
+// (PurArgs::part; reduced per output in a fixed order afterwards).  Keys
+// past T are left out of those sums (their zero K row still weighs
+// relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
+// workspace read, so they add nothing.
+template <class E, int DP, int MODE, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
-void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
+void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
@@ -428,8 +497,18 @@ void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
+    if constexpr (PUR) {
+        ptau = p.tau[p.per_head_tau ? h : 0];
+        pg = sc;
+        pgt = -sc * ptau;
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+        pe = p.eps_base;
+    }
+    float dg_acc = 0.f, dt_acc = 0.f;  // purified: sum u^3 dP (r - tau), sum u^3 dP
 
     // Stationary operands: sign-flipped K and V rows of this lane's key.
     u32x4 kr[KS], vr[KS];
@@ -523,13 +602,41 @@ void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
+        uint32_t w2[8], u2[8];
+        if constexpr (PUR) {
+            const int lim = qbase - key;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    float ww[2], uu[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 4 * i + k + e;
+                        const float x = s[r];
+                        float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                        float bb = __int_as_float(max(__float_as_int(x), 0));
+                        if (mk && 8 * (r >> 2) + (r & 3) + lim < 0) u = bb = 0.f;
+                        const float u2_ = u * u;
+                        const float dpz = dp[r] * z4[k + e];
+                        const float a = u2_ * u * dpz;
+                        dg_acc = fmaf(a, x - ptau, dg_acc);
+                        dt_acc += a;
+                        ww[e] = fmaf(u2_, u2_, pe * bb * bb) * z4[k + e];
+                        uu[e] = fmaf(p4g, u2_ * u, p2e * bb) * dpz;
+                    }
+                    w2[(4 * i + k) >> 1] = E::pack(ww[0], ww[1]);
+                    u2[(4 * i + k) >> 1] = E::pack(uu[0], uu[1]);
+                }
+            }
+        } else {
         if (mk) {
             const int lim = qbase - key;  // register r is masked when 8 (r / 4) + r % 4 < -lim
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (8 * (r >> 2) + (r & 3) + lim < 0) s[r] = 0.f;
         }
-        uint32_t w2[8], u2[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
@@ -544,6 +651,7 @@ void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
                 w2[r >> 1] = E::pack(t0 * a0, t1 * a1);
                 u2[r >> 1] = E::pack(t0 * dp[r], t1 * dp[r + 1]);
             }
+        }
         }
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -589,12 +697,32 @@ void born_bwd16_dkdv_fast_kernel(BwdArgs p) {
     }
     (void)kTileLoadsW;
 
-    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre),
-    // packed, staged in the idle ring (rows: dK at 0, dV at 128 rows) and
-    // stored 16 bytes per lane.
+    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre;
+    // purified: the accumulators as they are), packed, staged in the idle
+    // ring (rows: dK at 0, dV at 128 rows) and stored 16 bytes per lane.
     __syncthreads();
-    const float fk = 2.f * sc * fabsf(sc) / sq_pre;
-    const float fv = (sc / sq_pre) * (sc / sq_pre);
+    const float fk = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
+    const float fv = PUR ? 1.f : (sc / sq_pre) * (sc / sq_pre);
+    if constexpr (PUR) {
+        // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
+        // waves); keys past T excluded.
+        float a = key < T ? 4.f * dg_acc : 0.f;
+        float t2 = key < T ? -4.f * sc * dt_acc : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off);
+            t2 += __shfl_xor(t2, off);
+        }
+        float* red = reinterpret_cast<float*>(smem + 2 * BK * RB);
+        if (lane == 0) red[wave] = a, red[NW + wave] = t2;
+        __syncthreads();
+        if (tid == 0) {
+            float sa = 0.f, st = 0.f;
+            for (int w = 0; w < NW; ++w) sa += red[w], st += red[NW + w];
+            p.part[bid] = sa;
+            p.part[gridDim.x + bid] = st;
+        }
+    }
     int ln = lane;
     asm volatile("" : "+v"(ln));
     {

@@ -178,3 +178,74 @@ def test_purified_fast_forward_paired_launch(cuda_device):
                                             f64(v[b:b + 1, h:h + 1]), 8.0, 0.0625, 0.05, True, 1e-8)
         assert rel_err(f64(out[b:b + 1, h:h + 1]), O_ref) <= 1e-4
         assert np.max(np.abs(f64(z[b:b + 1, h:h + 1]) - Z_ref) / Z_ref) <= 1e-4
+
+
+# The bf16 D = 64 backward (dense or causal) runs the bf16-MFMA dQ and dK/dV
+# kernels (the reference rounds p/Z and dR to the input dtype before its dots,
+# so these contract bf16 operands as it does).  Held to the bf16 bar against
+# the oracle and to 5e-3 (normwise) against the fp32-MFMA kernels, reached
+# through an all-zero document id tensor; dgamma and dtau likewise.
+FAST_BWD_CASES = [
+    # (B, H, T, causal, scale, tau, eps_base, eps, std)
+    (2, 3, 130, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 200, False, 8.0, -0.1, 0.05, 1e-8, 0.3),
+    (2, 2, 64, False, [4.0, 9.0], [0.0, 0.2], 0.2, 1e-6, 0.3),
+    (1, 1, 1, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 600, True, [8.0, 5.0], [-0.05, 0.1], 0.05, 1e-8, 0.2),
+    (1, 1, 1000, False, 8.0, -0.2, 0.05, 1e-8, 0.2),
+]
+
+
+@pytest.mark.parametrize("case", FAST_BWD_CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-{'causal' if c[3] else 'dense'}")
+def test_purified_fast_backward(cuda_device, case):
+    B, H, T, causal, scale, tau, eps_base, eps, std = case
+    print(f"purified fast bwd case B{B} H{H} T{T} causal={causal}", flush=True)
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 64), seed=T + 9, std=std, n=4,
+                                                              dtype=torch.bfloat16))
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    kw = dict(eps_base=eps_base, is_causal=causal, eps=eps)
+    fast = _run(q, k, v, do, sc, ta, **kw)
+    zero_doc = torch.zeros((B, T), dtype=torch.int32, device=cuda_device)
+    generic = _run(q, k, v, do, sc, ta, doc_ids=zero_doc, **kw)
+    okw = dict(eps_base=eps_base, is_causal=causal, eps=eps)
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau), f64(do), **okw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau),
+                                           f64(do), **okw)
+    for i, name in enumerate(("dq", "dk", "dv")):
+        got, gen, want, m = f64(fast[1 + i]), f64(generic[1 + i]), ref[i], mag[i]
+        er = rel_err(got, want)
+        ef = max_abs(got, want) / m.max() if m.max() > 0 else max_abs(got, want)
+        assert er <= 2e-2 or ef <= 1e-4, f"{name}: rel {er:.3e} vs oracle (term scale {ef:.3e})"
+        eg = rel_err(got, gen)
+        efg = max_abs(got, gen) / m.max() if m.max() > 0 else max_abs(got, gen)
+        assert eg <= 5e-3 or efg <= 1e-4, f"{name}: rel {eg:.3e} vs the fp32-MFMA kernel"
+    for name, got, gen, want, m in (("dscale", fast[4], generic[4], ref[3], mag[3]),
+                                    ("dtau", fast[5], generic[5], ref[4], mag[4])):
+        got = np.atleast_1d(f64(got))
+        gen = np.atleast_1d(f64(gen))
+        ok = (np.abs(got - want) <= 2e-2 * np.abs(want)) | (np.abs(got - want) <= 1e-4 * m)
+        assert ok.all(), f"{name}: {got} vs oracle {want} (term scale {m})"
+        ok = (np.abs(got - gen) <= 5e-3 * np.abs(gen)) | (np.abs(got - gen) <= 1e-4 * m)
+        assert ok.all(), f"{name}: {got} vs fp32-MFMA kernel {gen}"
+
+
+def test_purified_fast_backward_full_size(cuda_device):
+    """The C5 shape (B16 H16 T2048): gradients checked on sampled heads
+    against the oracle; dgamma / dtau against the fp32-MFMA kernels."""
+    B, H, T = 16, 16, 2048
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 64), seed=21, std=0.125, n=4,
+                                                              dtype=torch.bfloat16))
+    sc = torch.tensor(8.0, device=cuda_device)
+    ta = torch.tensor(0.0625, device=cuda_device)
+    fast = _run(q, k, v, do, sc, ta, is_causal=True)
+    zero_doc = torch.zeros((B, T), dtype=torch.int32, device=cuda_device)
+    generic = _run(q, k, v, do, sc, ta, is_causal=True, doc_ids=zero_doc)
+    for b, h in ((0, 0), (9, 13), (15, 15)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ref = orc.purified_backward(f64(q[sl]), f64(k[sl]), f64(v[sl]), 8.0, 0.0625, f64(do[sl]))
+        for i in range(3):
+            assert rel_err(f64(fast[1 + i][sl]), ref[i]) <= 2e-2
+    for i in (4, 5):
+        got, gen = float(fast[i]), float(generic[i])
+        assert abs(got - gen) <= 5e-3 * abs(gen) + 1e-6, (i, got, gen)
