@@ -156,15 +156,20 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const int BH = p.B * p.H;
     const int nmb = fast_fwd_nmb(T, BM);
     const int bid = blockIdx.x;
-    const int bh = bid % BH;
-    const int pr = bid / BH;
-    const int h = bh % p.H;
     // Paired launch (fast_fwd_npair blocks per head): item 0 is query block
     // nmb-1-pr (the longer key range under causality), item 1 block pr when
     // that is a different block.  Unpaired launch (nmb blocks per head, for
     // problems too small to give every CU two paired workgroups): one block
-    // per workgroup, the longest key ranges first.
+    // per workgroup, the longest key ranges first, except that with 257 to
+    // 512 workgroups the second 256 take theirs in ascending length:
+    // workgroups k and k + 256 share a CU (the dispatcher deals workgroups to
+    // the 8 XCDs in turn and fills each XCD's 32 CUs in order), so every CU
+    // pairs a long block with a short one.
     const bool paired = gridDim.x < (unsigned)(nmb * BH);
+    const int item = (!paired && kCaus && bid >= 256 && gridDim.x <= 512u) ? (int)gridDim.x + 255 - bid : bid;
+    const int bh = item % BH;
+    const int pr = item / BH;
+    const int h = bh % p.H;
     const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
     auto item_tiles = [&](int mb) -> int {
