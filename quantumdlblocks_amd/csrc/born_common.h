@@ -114,6 +114,18 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
+// XOR swizzle of the 16-byte chunks of a 128-byte LDS tile row r: chunk c is
+// stored at c ^ lds_swz(r).  LDS serves 64 banks x 4 bytes per cycle; a
+// ds_read_b128 is served 16 lanes at a time and a ds_read_b64(_tr_b16) 32 at
+// a time.  With rows of 128 bytes, two rows of equal parity share their banks,
+// so a row read (lanes on 16 consecutive rows, one logical chunk) is
+// conflict-free when lds_swz takes 8 distinct values on the 8 rows of each
+// parity, and a transposed read (lanes on rows r0..r0+3, r0 % 4 == 0, an
+// aligned group of 4 chunks) when lds_swz(r) ^ lds_swz(r + 2) has bit 2 set
+// for r % 4 in {0, 1}.  Both hold here (2 (r & 3) | ((r >> 2) & 1) meets only
+// the second, r & 7 neither).
+__device__ __forceinline__ int lds_swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }

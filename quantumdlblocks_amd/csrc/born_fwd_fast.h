@@ -8,7 +8,8 @@
 //     staging registers, no staging VALU).  Each wave instruction writes 1 KiB
 //     of LDS contiguously (lane l at base + 16 l), so tiles are dense in LDS
 //     and 16-byte chunks are XOR-swizzled within each row instead of padded:
-//       Q, K: chunk' = chunk ^ (row & 7)    -> 8-row ds_read_b128 conflict-free
+//       K:    chunk' = chunk ^ lds_swz(row) -> row reads conflict-free
+//       Q:    chunk' = chunk ^ (row & 7)    (read once per query block)
 //       V:    chunk' = chunk ^ 2 (row & 3)  -> 4-row ds_read_b64_tr_b16 conflict-free
 //     (32 banks x 4 bytes).  Each lane picks the global chunk that belongs in
 //     its fixed LDS slot.  Rows >= T lie beyond the buffer's num_records and
@@ -214,7 +215,7 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
             const int off = (key0 + row) * RB;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ lds_swz(row)) << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
         }
     };
@@ -246,7 +247,7 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 
     auto k_operand = [&](const uint8_t* kb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
         const int row = nb * 32 + c;
-        const int pc = (2 * ks + g) ^ (row & 7);
+        const int pc = (2 * ks + g) ^ lds_swz(row);
         return *reinterpret_cast<const u32x4*>(kb + row * RB + pc * 16);
     };
     auto v_operand = [&](const uint8_t* vb, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
