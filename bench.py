@@ -223,7 +223,8 @@ def main():
     if args.gpus != 1 or world != 1:
         print(
             "bench.py measures one GPU: this build's flash-Born path runs on a single MI355X "
-            "(the multi-GPU sharding plan is described in DESIGN.md, not built); rerun with --gpus 1",
+            "(sharding (b, h) slices or the sequence over several GPUs is designed, not built); "
+            "rerun with --gpus 1",
             file=sys.stderr,
         )
         sys.exit(2)
