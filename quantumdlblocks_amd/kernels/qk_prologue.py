@@ -20,7 +20,8 @@ that enables them applies them before calling it.
 D (for example the ``(B, T, H, D)`` projection output viewed as
 ``(B, H, T, D)``): the kernel reads them in place, so the ``.contiguous()``
 copies before the prologue are not needed.  The backward writes the input
-gradients with the inputs' own strides.
+gradients with the inputs' own strides when those describe a dense layout
+(a permuted contiguous tensor), else contiguous.
 """
 
 from __future__ import annotations
@@ -110,12 +111,29 @@ def _launch_fwd(x: torch.Tensor, which: int, cos2, sin2, eps: float):
     return out, rinv
 
 
+def _dense_layout(shape, strides) -> bool:
+    """True when (shape, strides) describes a non-overlapping layout without
+    gaps (a permutation of a contiguous tensor): one a gradient may take."""
+    dims = sorted((st, n) for n, st in zip(shape, strides) if n != 1)
+    expect = 1
+    for st, n in dims:
+        if st != expect:
+            return False
+        expect *= n
+    return True
+
+
 def _launch_bwd(g, out, rinv, cos2, sin2, layout, which: int):
-    """Input gradient of one tensor, written with the input's (shape, strides)."""
+    """Input gradient of one tensor, written with the input's (shape, strides)
+    when those are dense (a permuted contiguous tensor, e.g. the projection
+    layout), else contiguous."""
     lib = _native.load()
     B, H, T, D = out.shape
     g = g.to(out.dtype).contiguous()
-    dx = torch.empty_strided(layout[0], layout[1], dtype=out.dtype, device=out.device)
+    if _dense_layout(*layout):
+        dx = torch.empty_strided(layout[0], layout[1], dtype=out.dtype, device=out.device)
+    else:
+        dx = torch.empty(layout[0], dtype=out.dtype, device=out.device)
     st = _strides(dx)
     gs = [None, None]
     ys = [None, None]

@@ -201,3 +201,35 @@ def test_prologue_empty_and_single_tensor(cuda_device):
     torch.cuda.synchronize()
     assert k.grad is not None and torch.isfinite(k.grad.float()).all()
     assert qo.requires_grad is False or qo.grad_fn is not None
+
+
+def test_prologue_gradients_of_sliced_and_expanded_inputs(cuda_device):
+    """Q and K cut from one fused projection (rows with gaps) and an expanded
+    K (stride 0 over heads): gradients equal those of contiguous copies."""
+    from quantumdlblocks_amd.kernels.qk_prologue import fused_qk_rope_l2_normalize
+
+    B, T, H, D = 2, 40, 4, 64
+    g = torch.Generator("cpu").manual_seed(5)
+    qkv = torch.randn(B, T, 3 * H * D, generator=g).to(torch.bfloat16).to(cuda_device).requires_grad_(True)
+    k1 = torch.randn(B, 1, T, D, generator=g).to(torch.bfloat16).to(cuda_device).requires_grad_(True)
+    cos, sin = _tables(T, D // 2)
+    cos, sin = cos.to(cuda_device), sin.to(cuda_device)
+    gq = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(cuda_device)
+    gk = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(cuda_device)
+
+    q = qkv[..., : H * D].view(B, T, H, D).transpose(1, 2)
+    k = k1.expand(B, H, T, D)
+    qo, ko = fused_qk_rope_l2_normalize(q, k, cos, sin)
+    torch.autograd.backward([qo, ko], [gq, gk])
+
+    qkv2 = qkv.detach().clone().requires_grad_(True)
+    k2 = k1.detach().clone().requires_grad_(True)
+    qc = qkv2[..., : H * D].view(B, T, H, D).transpose(1, 2).contiguous()
+    kc = k2.expand(B, H, T, D).contiguous()
+    qo2, ko2 = fused_qk_rope_l2_normalize(qc, kc, cos, sin)
+    torch.autograd.backward([qo2, ko2], [gq, gk])
+    torch.cuda.synchronize()
+    assert torch.equal(qo, qo2) and torch.equal(ko, ko2)
+    assert torch.equal(qkv.grad, qkv2.grad)
+    # The expanded K's gradient is the sum over heads, in autograd's order for both.
+    assert torch.allclose(k1.grad.float(), k2.grad.float(), rtol=0, atol=0)

@@ -247,3 +247,19 @@ def test_prologue_cpu_tensors_take_the_eager_formulation():
         assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30)
     with pytest.raises(ValueError):
         fused_qk_rope_l2_normalize(q, k[:, :2])
+
+
+def test_prologue_gradient_layout_rule():
+    """Input gradients keep the input's strides only for dense layouts."""
+    from quantumdlblocks_amd.kernels.qk_prologue import _dense_layout
+
+    x = torch.empty(2, 8, 4, 16)  # (B, T, H, D)
+    v = x.transpose(1, 2)  # (B, H, T, D) view of the projection layout
+    assert _dense_layout(tuple(v.shape), v.stride())
+    assert _dense_layout((2, 4, 8, 16), torch.empty(2, 4, 8, 16).stride())
+    qkv = torch.empty(2, 8, 3 * 4 * 16)
+    q = qkv[..., : 4 * 16].view(2, 8, 4, 16).transpose(1, 2)  # gaps between rows
+    assert not _dense_layout(tuple(q.shape), q.stride())
+    e = torch.empty(1, 4, 8, 16).expand(2, 4, 8, 16)  # stride 0: overlapping
+    assert not _dense_layout(tuple(e.shape), e.stride())
+    assert _dense_layout((1, 4, 8, 16), (999, 128, 16, 1))  # size-1 dims are free
