@@ -14,7 +14,7 @@ average launch against the HBM roof) and ``cpu_baseline`` (the reference's
 eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
 on this host).
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c5fwd|c5|p3|p5|qk3|qk5]
+    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c4b|c5fwd|c5|p3|p5|qk3|qk5]
 
 p3 / p5: purified-Born attention (the reference's flash_purified_born_attention,
 gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8) on the C3 / C5 shapes with bf16
@@ -52,6 +52,7 @@ CONFIGS = {
     "c2": (32, 4, 1024, 64, 1.0, True, None, False),
     "c3": (16, 16, 1024, 64, 0.125, False, None, False),
     "c4": (4, 16, 8192, 64, 1.0, False, 512.0, False),
+    "c4b": (4, 16, 8192, 64, 1.0, False, 512.0, True),  # C4 with the backward (document-masked training)
     "c5fwd": (16, 16, 2048, 64, 1.0, False, None, False),
     "c5": (16, 16, 2048, 64, 1.0, False, None, True),
     # purified-Born attention on the C3 / C5 shapes

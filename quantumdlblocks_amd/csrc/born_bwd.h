@@ -86,6 +86,82 @@ __device__ __forceinline__ bool visible(int i, int j, bool causal, int window, b
     return v;
 }
 
+// Document ids: the span of candidate tiles a block has to visit.  The
+// block's stationary rows r0 .. r1-1 hold ids in [dlo, dhi]; candidate tile t
+// (t_lo <= t <= t_hi) covers rows t TS .. min(T, t TS + TS) - 1 of the
+// streamed operand.  Returns the first (x) and last (y) candidate whose id
+// range meets [dlo, dhi], x > y when none does.  A visible pair needs equal
+// ids, so no tile outside the span has one: the span is exact for sorted ids
+// (compute_document_ids output) and a superset for any others, and the tiles
+// inside keep their per-element masks.  Every thread of the block calls it
+// (three barriers); red is four ints of LDS.
+template <int TS>
+__device__ int2 doc_tile_span(const int32_t* __restrict__ docb, int T, int r0, int r1, int t_lo, int t_hi,
+                              int32_t* red) {
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
+    auto wave_min = [](int x) {
+        for (int o = 1; o < 64; o <<= 1) x = min(x, __shfl_xor(x, o));
+        return x;
+    };
+    auto wave_max = [](int x) {
+        for (int o = 1; o < 64; o <<= 1) x = max(x, __shfl_xor(x, o));
+        return x;
+    };
+    if (tid == 0) {
+        red[0] = INT_MAX;
+        red[1] = INT_MIN;
+        red[2] = INT_MAX;
+        red[3] = INT_MIN;
+    }
+    __syncthreads();
+    int lo = INT_MAX, hi = INT_MIN;
+    for (int r = r0 + tid; r < r1; r += nt) {
+        const int d = docb[r];
+        lo = min(lo, d);
+        hi = max(hi, d);
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+        atomicMin(&red[0], lo);
+        atomicMax(&red[1], hi);
+    }
+    __syncthreads();
+    const int dlo = red[0], dhi = red[1];
+    const bool vec = (reinterpret_cast<uintptr_t>(docb) & 15) == 0;
+    int first = INT_MAX, last = INT_MIN;
+    for (int t = t_lo + tid; t <= t_hi; t += nt) {
+        const int k0 = t * TS, k1 = min(T, k0 + TS);
+        int a = INT_MAX, z = INT_MIN;
+        if (vec && k1 - k0 == TS) {
+#pragma unroll 8
+            for (int j = 0; j < TS / 4; ++j) {
+                const int4 x = *reinterpret_cast<const int4*>(docb + k0 + 4 * j);
+                a = min(a, min(min(x.x, x.y), min(x.z, x.w)));
+                z = max(z, max(max(x.x, x.y), max(x.z, x.w)));
+            }
+        } else {
+            for (int k = k0; k < k1; ++k) {
+                const int d = docb[k];
+                a = min(a, d);
+                z = max(z, d);
+            }
+        }
+        if (z >= dlo && a <= dhi) {
+            first = min(first, t);
+            last = max(last, t);
+        }
+    }
+    first = wave_min(first);
+    last = wave_max(last);
+    if (lane == 0) {
+        atomicMin(&red[2], first);
+        atomicMax(&red[3], last);
+    }
+    __syncthreads();
+    return make_int2(red[2], red[3]);
+}
+
 // ---------------------------------------------------------------------------
 // dQ, 16-bit.  Queries stationary (like the forward).  Per key tile and wave:
 //   S^T  = K Q'^T          (A = K rows from LDS, B = sign-flipped Q^T in registers)
@@ -113,6 +189,7 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) uint16_t kt_lds[2][DP * TS];
     __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
+    __shared__ int32_t span_red[kDoc ? 4 : 1];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -176,7 +253,15 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     int kv_lo = 0;
     int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
+                                              span_red);
+            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+            if (ntiles > 0) kv_lo = sp.x * BN;
+        }
+    }
 
     KStage kst;
     VStage vst;
@@ -342,6 +427,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) float nd_lds[2][BQ];
     __shared__ __attribute__((aligned(16))) float zi_lds[2][BQ];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BQ : 1];
+    __shared__ int32_t span_red[kDoc ? 4 : 1];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -399,7 +485,15 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     int q_lo = causal ? (k0 & ~(BQ - 1)) : 0;
     int q_hi = T;
     if (window > 0) q_hi = min(T, k0 + BK - 1 + window);
-    const int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
+                                              span_red);
+            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+            if (ntiles > 0) q_lo = sp.x * BQ;
+        }
+    }
 
     Stage qst, dst;
     float ndreg = 0.f, zireg = 0.f;
@@ -564,6 +658,7 @@ void born_bwd_dq32_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) float k_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) float v_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? 2 : 1][kDoc ? BN : 1];
+    __shared__ int32_t span_red[kDoc ? 4 : 1];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -613,7 +708,15 @@ void born_bwd_dq32_kernel(BwdArgs p) {
     int kv_lo = 0;
     int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
+                                              span_red);
+            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+            if (ntiles > 0) kv_lo = sp.x * BN;
+        }
+    }
 
     Stage kst, vst;
     int dreg = -2;
@@ -733,6 +836,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     __shared__ __attribute__((aligned(16))) float nd_lds[NBUF][BQ];
     __shared__ __attribute__((aligned(16))) float zi_lds[NBUF][BQ];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[kDoc ? NBUF : 1][kDoc ? BQ : 1];
+    __shared__ int32_t span_red[kDoc ? 4 : 1];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -795,7 +899,15 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     int q_lo = causal ? (k0 & ~(BQ - 1)) : 0;
     int q_hi = T;
     if (window > 0) q_hi = min(T, k0 + BK - 1 + window);
-    const int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
+                                              span_red);
+            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+            if (ntiles > 0) q_lo = sp.x * BQ;
+        }
+    }
 
     Stage qst, dst;
     float ndreg = 0.f, zireg = 0.f;

@@ -147,6 +147,41 @@ def test_bwd_document_mask(cuda_device, dtype, is_causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_unsorted_document_ids(cuda_device, dtype, D, is_causal):
+    """Arbitrary (unsorted, repeating) document ids: the span of tiles a
+    backward block visits, taken from document-id ranges, must stay a superset
+    of the tiles holding a visible pair."""
+    rng = np.random.default_rng(D + 1)
+    doc = rng.integers(0, 4, size=(2, 700)).astype(np.int32)
+    doc[1, 350:] = rng.integers(10, 12, size=350)
+    _check_bwd(2, 2, 700, D, dtype, cuda_device, is_causal=is_causal, doc=doc, seed=D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_document_tile_edges(cuda_device, dtype, D, is_causal):
+    """Sorted documents whose edges fall on, just before and just after the
+    32-, 64-, 128- and 256-row tile and block edges, one-token documents,
+    negative ids, and a batch row sorted in descending order: the tiles a
+    block's span leaves out must hold no visible pair."""
+    lens = [64, 1, 63, 129, 256, 1, 1, 31, 97, 200, 65, 12, 33]
+    ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
+    doc = np.stack([ids, -ids[::-1]])
+    _check_bwd(2, 2, ids.size, D, dtype, cuda_device, is_causal=is_causal, doc=doc, seed=5)
+
+
+def test_bwd_documents_many_tiles(cuda_device):
+    """Sorted documents over more candidate tiles than a block has threads
+    (fp32, D = 256: one-wave dK/dV blocks, 32-row tiles), so the span's
+    screening loop strides."""
+    doc = orc.geometric_doc_ids(1, 4500, 400.0, seed=9)
+    _check_bwd(1, 1, 4500, 256, torch.float32, cuda_device, doc=doc, std=0.5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_bwd_scales_and_dscale(cuda_device, dtype):
     for scale in (np.array([2.5, 3.2, -0.5, 7.0]), np.array([1.0, 0.0, -8.0, 2.0])):
         _check_bwd(2, 4, 130, 64, dtype, cuda_device, scale=scale, eps=1e-3, std=0.3, check_dscale=True)
