@@ -162,6 +162,16 @@ __device__ int2 doc_tile_span(const int32_t* __restrict__ docb, int T, int r0, i
     return make_int2(red[2], red[3]);
 }
 
+// Documents: whether the n ids of the staged tile (in LDS) and the ids a and
+// b of this lane's stationary rows are all one document, so that the tile
+// needs no per-element document test.  Uniform per wave.
+__device__ __forceinline__ bool one_document(const int32_t* ids, int n, int a, int b) {
+    const int d0 = ids[0];
+    bool same = (a == d0) && (b == d0);
+    for (int i = threadIdx.x & 63; i < n; i += 64) same = same && (ids[i] == d0);
+    return __ballot(!same) == 0;
+}
+
 // ---------------------------------------------------------------------------
 // dQ, 16-bit.  Queries stationary (like the forward).  Per key tile and wave:
 //   S^T  = K Q'^T          (A = K rows from LDS, B = sign-flipped Q^T in registers)
@@ -297,7 +307,8 @@ void born_bwd_dq16_kernel(BwdArgs p) {
         if (more) load_tile(key0 + BN);
 
         bool active = q0 < T;
-        bool need_mask = has_doc;
+        bool need_mask = false;
+        if constexpr (kDoc) need_mask = has_doc && !one_document(doc_lds[buf], BN, qdoc[0], qdoc[NQB - 1]);
         if (causal) {
             active = active && (key0 <= q0 + QW - 1);
             need_mask = need_mask || (key0 + BN - 1 > q0);
@@ -540,7 +551,8 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         if (more) load_tile(i0 + BQ);
 
         bool active = kw0 < T;
-        bool need_mask = has_doc;
+        bool need_mask = false;
+        if constexpr (kDoc) need_mask = has_doc && !one_document(doc_lds[buf], BQ, kdoc, kdoc);
         if (causal) {
             active = active && (i0 + BQ - 1 >= kw0);
             need_mask = need_mask || (i0 < kw0 + 31);
@@ -746,7 +758,8 @@ void born_bwd_dq32_kernel(BwdArgs p) {
         const bool more = (t + 1) < ntiles;
         if (more) load_tile(key0 + BN);
         bool active = q0 < T;
-        bool need_mask = has_doc;
+        bool need_mask = false;
+        if constexpr (kDoc) need_mask = has_doc && !one_document(doc_lds[buf], BN, qdoc, qdoc);
         if (causal) {
             active = active && (key0 <= q0 + QW - 1);
             need_mask = need_mask || (key0 + BN - 1 > q0);
@@ -952,7 +965,8 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         if (NBUF == 2 && more) load_tile(i0 + BQ);
 
         bool active = kw0 < T;
-        bool need_mask = has_doc;
+        bool need_mask = false;
+        if constexpr (kDoc) need_mask = has_doc && !one_document(doc_lds[buf], BQ, kdoc, kdoc);
         if (causal) {
             active = active && (i0 + BQ - 1 >= kw0);
             need_mask = need_mask || (i0 < kw0 + 31);
