@@ -14,7 +14,7 @@ average launch against the HBM roof) and ``cpu_baseline`` (the reference's
 eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
 on this host).
 
-    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c4b|c5fwd|c5|p3|p5|qk3|qk5]
+    python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c4b|c5fwd|c5|p3|p5|p4b|qk3|qk5]
 
 p3 / p5: purified-Born attention (the reference's flash_purified_born_attention,
 gamma 8, tau 0.0625, eps_base 0.05, eps 1e-8) on the C3 / C5 shapes with bf16
@@ -58,8 +58,9 @@ CONFIGS = {
     # purified-Born attention on the C3 / C5 shapes
     "p3": (16, 16, 1024, 64, 0.125, False, None, False),
     "p5": (16, 16, 2048, 64, 0.125, False, None, True),
+    "p4b": (4, 16, 8192, 64, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
 }
-PURIFIED = {"p3", "p5"}
+PURIFIED = {"p3", "p5", "p4b"}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}

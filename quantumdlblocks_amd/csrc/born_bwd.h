@@ -86,92 +86,6 @@ __device__ __forceinline__ bool visible(int i, int j, bool causal, int window, b
     return v;
 }
 
-// Document ids: the span of candidate tiles a block has to visit.  The
-// block's stationary rows r0 .. r1-1 hold ids in [dlo, dhi]; candidate tile t
-// (t_lo <= t <= t_hi) covers rows t TS .. min(T, t TS + TS) - 1 of the
-// streamed operand.  Returns the first (x) and last (y) candidate whose id
-// range meets [dlo, dhi], x > y when none does.  A visible pair needs equal
-// ids, so no tile outside the span has one: the span is exact for sorted ids
-// (compute_document_ids output) and a superset for any others, and the tiles
-// inside keep their per-element masks.  Every thread of the block calls it
-// (three barriers); red is four ints of LDS.
-template <int TS>
-__device__ int2 doc_tile_span(const int32_t* __restrict__ docb, int T, int r0, int r1, int t_lo, int t_hi,
-                              int32_t* red) {
-    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
-    auto wave_min = [](int x) {
-        for (int o = 1; o < 64; o <<= 1) x = min(x, __shfl_xor(x, o));
-        return x;
-    };
-    auto wave_max = [](int x) {
-        for (int o = 1; o < 64; o <<= 1) x = max(x, __shfl_xor(x, o));
-        return x;
-    };
-    if (tid == 0) {
-        red[0] = INT_MAX;
-        red[1] = INT_MIN;
-        red[2] = INT_MAX;
-        red[3] = INT_MIN;
-    }
-    __syncthreads();
-    int lo = INT_MAX, hi = INT_MIN;
-    for (int r = r0 + tid; r < r1; r += nt) {
-        const int d = docb[r];
-        lo = min(lo, d);
-        hi = max(hi, d);
-    }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
-    if (lane == 0) {
-        atomicMin(&red[0], lo);
-        atomicMax(&red[1], hi);
-    }
-    __syncthreads();
-    const int dlo = red[0], dhi = red[1];
-    const bool vec = (reinterpret_cast<uintptr_t>(docb) & 15) == 0;
-    int first = INT_MAX, last = INT_MIN;
-    for (int t = t_lo + tid; t <= t_hi; t += nt) {
-        const int k0 = t * TS, k1 = min(T, k0 + TS);
-        int a = INT_MAX, z = INT_MIN;
-        if (vec && k1 - k0 == TS) {
-#pragma unroll 8
-            for (int j = 0; j < TS / 4; ++j) {
-                const int4 x = *reinterpret_cast<const int4*>(docb + k0 + 4 * j);
-                a = min(a, min(min(x.x, x.y), min(x.z, x.w)));
-                z = max(z, max(max(x.x, x.y), max(x.z, x.w)));
-            }
-        } else {
-            for (int k = k0; k < k1; ++k) {
-                const int d = docb[k];
-                a = min(a, d);
-                z = max(z, d);
-            }
-        }
-        if (z >= dlo && a <= dhi) {
-            first = min(first, t);
-            last = max(last, t);
-        }
-    }
-    first = wave_min(first);
-    last = wave_max(last);
-    if (lane == 0) {
-        atomicMin(&red[2], first);
-        atomicMax(&red[3], last);
-    }
-    __syncthreads();
-    return make_int2(red[2], red[3]);
-}
-
-// Documents: whether the n ids of the staged tile (in LDS) and the ids a and
-// b of this lane's stationary rows are all one document, so that the tile
-// needs no per-element document test.  Uniform per wave.
-__device__ __forceinline__ bool one_document(const int32_t* ids, int n, int a, int b) {
-    const int d0 = ids[0];
-    bool same = (a == d0) && (b == d0);
-    for (int i = threadIdx.x & 63; i < n; i += 64) same = same && (ids[i] == d0);
-    return __ballot(!same) == 0;
-}
-
 // ---------------------------------------------------------------------------
 // dQ, 16-bit.  Queries stationary (like the forward).  Per key tile and wave:
 //   S^T  = K Q'^T          (A = K rows from LDS, B = sign-flipped Q^T in registers)

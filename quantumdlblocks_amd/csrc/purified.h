@@ -137,6 +137,7 @@ void purified_fwd_kernel(PurArgs p) {
     __shared__ __attribute__((aligned(16))) float k_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) float v_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[2][BN];
+    __shared__ int32_t span_red[4];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -177,7 +178,13 @@ void purified_fwd_kernel(PurArgs p) {
     int kv_lo = 0;
     const int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    if (has_doc && ntiles > 0) {
+        const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
+                                          span_red);
+        ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+        if (ntiles > 0) kv_lo = sp.x * BN;
+    }
 
     Stage kst, vst;
     int dreg = -2;
@@ -208,7 +215,7 @@ void purified_fwd_kernel(PurArgs p) {
         const bool more = (t + 1) < ntiles;
         if (more) load_tile(key0 + BN);
         bool active = q0 < T;
-        bool need_mask = has_doc || key0 + BN > T;
+        bool need_mask = (has_doc && !one_document(doc_lds[buf], BN, qdoc, qdoc)) || key0 + BN > T;
         if (causal) {
             active = active && (key0 <= q0 + QW - 1);
             need_mask = need_mask || (key0 + BN - 1 > q0);
@@ -345,6 +352,7 @@ void purified_dkdv_kernel(PurArgs p) {
     __shared__ __attribute__((aligned(16))) float nd_lds[NBUF][BQ];
     __shared__ __attribute__((aligned(16))) float zi_lds[NBUF][BQ];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[NBUF][BQ];
+    __shared__ int32_t span_red[4];
     __shared__ float red[2][NW];
 
     const int T = p.T, D = p.D;
@@ -405,10 +413,16 @@ void purified_dkdv_kernel(PurArgs p) {
 
     // Query range (flash_born.py:885-886; with a window no query past the
     // block's last key + window - 1 sees it, causal or not).
-    const int q_lo = causal ? (k0 & ~(BQ - 1)) : 0;
+    int q_lo = causal ? (k0 & ~(BQ - 1)) : 0;
     int q_hi = T;
     if (window > 0) q_hi = min(T, k0 + BK - 1 + window);
-    const int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
+    if (has_doc && ntiles > 0) {
+        const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
+                                          span_red);
+        ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+        if (ntiles > 0) q_lo = sp.x * BQ;
+    }
 
     Stage qst, dst;
     float ndreg = 0.f, zireg = 0.f;
@@ -449,7 +463,7 @@ void purified_dkdv_kernel(PurArgs p) {
         const bool more = (t + 1) < ntiles;
         if (NBUF == 2 && more) load_tile(i0 + BQ);
         bool active = kw0 < T;
-        bool need_mask = has_doc || key >= T || i0 + BQ > T;
+        bool need_mask = (has_doc && !one_document(doc_lds[buf], BQ, kdoc, kdoc)) || key >= T || i0 + BQ > T;
         if (causal) {
             active = active && (i0 + BQ - 1 >= kw0);
             need_mask = need_mask || (i0 < kw0 + 31);
@@ -585,6 +599,7 @@ void purified_dq_kernel(PurArgs p) {
     __shared__ __attribute__((aligned(16))) float k_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) float v_lds[2][BN * RS];
     __shared__ __attribute__((aligned(16))) int32_t doc_lds[2][BN];
+    __shared__ int32_t span_red[4];
 
     const int T = p.T, D = p.D;
     const int BH = p.B * p.H;
@@ -630,7 +645,13 @@ void purified_dq_kernel(PurArgs p) {
     int kv_lo = 0;
     const int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
+    if (has_doc && ntiles > 0) {
+        const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
+                                          span_red);
+        ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+        if (ntiles > 0) kv_lo = sp.x * BN;
+    }
 
     Stage kst, vst;
     int dreg = -2;
@@ -660,7 +681,7 @@ void purified_dq_kernel(PurArgs p) {
         const bool more = (t + 1) < ntiles;
         if (more) load_tile(key0 + BN);
         bool active = q0 < T;
-        bool need_mask = has_doc || key0 + BN > T;
+        bool need_mask = (has_doc && !one_document(doc_lds[buf], BN, qdoc, qdoc)) || key0 + BN > T;
         if (causal) {
             active = active && (key0 <= q0 + QW - 1);
             need_mask = need_mask || (key0 + BN - 1 > q0);

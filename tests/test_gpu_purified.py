@@ -51,17 +51,18 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}D{c[3]}-{str(c[4])[6:]}")
-def test_purified_forward_backward(cuda_device, case):
+def _check_pur(case, dev, doc=None):
     B, H, T, D, dtype, kw, scale, tau, std = case
-    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=T + D, std=std, n=4, dtype=dtype))
-    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
-    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
-    out, dq, dk, dv, dsc, dta = _run(q, k, v, do, sc, ta, **kw)
+    q, k, v, do = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=T + D, std=std, n=4, dtype=dtype))
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=dev)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=dev)
+    print(f"purified B{B} H{H} T{T} D{D} {dtype} {kw} doc={doc is not None}", flush=True)
+    doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
+    out, dq, dk, dv, dsc, dta = _run(q, k, v, do, sc, ta, doc_ids=doc_t, **kw)
     assert out.dtype == dtype and dq.dtype == dtype
     assert dsc.shape == sc.shape and dta.shape == ta.shape
     okw = dict(eps_base=kw.get("eps_base", 0.05), is_causal=kw.get("is_causal", True), eps=kw.get("eps", 1e-8),
-               window_size=kw.get("window_size", 0))
+               window_size=kw.get("window_size", 0), doc_ids=doc)
     O_ref, _ = orc.purified_forward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau), **okw)
     e = rel_err(f64(out), O_ref)
     assert e <= TOL[dtype], f"output rel err {e:.3e} (max abs {max_abs(f64(out), O_ref):.3e})"
@@ -79,6 +80,44 @@ def test_purified_forward_backward(cuda_device, case):
         err = np.abs(got - want)
         ok = (err <= GTOL[dtype] * np.abs(want)) | (err <= FLOOR[dtype] * m)
         assert ok.all(), f"{name}: {got} vs {want} (term scale {m})"
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}D{c[3]}-{str(c[4])[6:]}")
+def test_purified_forward_backward(cuda_device, case):
+    _check_pur(case, cuda_device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
+    """Arbitrary (unsorted, repeating) document ids, tau < 0 (masked pairs
+    would weigh relu(-gamma tau) > 0): the span of tiles each block visits,
+    from document-id ranges, must keep every tile with a visible pair."""
+    rng = np.random.default_rng(D + 2)
+    doc = rng.integers(0, 4, size=(2, 500)).astype(np.int32)
+    doc[1, 250:] = rng.integers(10, 12, size=250)
+    _check_pur((2, 2, 500, D, dtype, dict(is_causal=is_causal), 8.0, -0.05, 0.3), cuda_device, doc)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_purified_document_tile_edges(cuda_device, dtype, is_causal):
+    """Sorted documents with edges on and next to the 32- and 64-row tile
+    edges, one-token documents, negative ids, one batch row in descending
+    order, and tau < 0."""
+    lens = [64, 1, 63, 129, 32, 1, 1, 31, 97, 65, 12, 33]
+    ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
+    doc = np.stack([ids, -ids[::-1]])
+    _check_pur((2, 2, ids.size, 64, dtype, dict(is_causal=is_causal), [8.0, 4.0], [-0.05, 0.1], 0.3), cuda_device,
+               doc)
+
+
+def test_purified_documents_many_tiles(cuda_device):
+    """Sorted documents over more candidate tiles than a block has threads
+    (fp32, D = 256), so the span's screening loop strides."""
+    doc = orc.geometric_doc_ids(1, 4500, 400.0, seed=4)
+    _check_pur((1, 1, 4500, 256, torch.float32, dict(is_causal=True), 3.0, 0.0, 0.1), cuda_device, doc)
 
 
 def test_purified_documents(cuda_device):
