@@ -158,44 +158,66 @@ def visible_pairs(cfg, doc):
     return total
 
 
-def cpu_baseline(cfg, budget_s, seed, purified=False):
-    """Time the reference's eager CPU path (fp32, full T x T) on a bounded sample."""
+def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None):
+    """Time the reference's eager CPU path (fp32, full T x T) on a bounded sample
+    of the same workload: n heads of batch row 0, its document mask when the
+    config has documents, and the autograd backward when the config has one.
+    The rate counts the flops the GPU line counts (visible pairs; 3.5x the
+    forward's with the backward)."""
+    import numpy as np
     import torch
 
     from oracle.born_oracle import eager_fp32_torch, purified_eager_fp32_torch
 
-    if purified:
-        def eager_fp32_torch(q, k, v, sc):  # noqa: F811  (the purified eager path, same call shape)
-            return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS)
+    backward = cfg[7]
+    doc_row = None if doc is None else torch.as_tensor(np.asarray(doc)[:1], dtype=torch.int32)
+
+    def eager(q, k, v, sc):
+        if purified:
+            return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS, doc_ids=doc_row)
+        return eager_fp32_torch(q, k, v, sc, doc_ids=doc_row)
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     B, H, T, D, std = cfg[:5]
     g = torch.Generator("cpu").manual_seed(seed)
     per_run = max(budget_s / 8.0, 0.05)
+    sc = torch.tensor(8.0)
 
     def sample(n):
-        q, k, v = (torch.randn(1, n, T, D, generator=g) * std for _ in range(3))
-        return q, k, v
+        q, k, v, do = (torch.randn(1, n, T, D, generator=g) * std for _ in range(4))
+        return [x.requires_grad_(backward) for x in (q, k, v)] + [do]
+
+    def step(q, k, v, do):
+        if backward:
+            out = eager(q, k, v, sc)
+            torch.autograd.grad(out, (q, k, v), do)
+        else:
+            with torch.no_grad():
+                eager(q, k, v, sc)
 
     n = 1
-    q, k, v = sample(n)
+    x = sample(n)
     t0 = time.perf_counter()
-    eager_fp32_torch(q, k, v, torch.tensor(8.0))
+    step(*x)
     one = time.perf_counter() - t0
     n = int(max(1, min(B * H, per_run / max(one, 1e-6))))
-    q, k, v = sample(n)
-    sc = torch.tensor(8.0)
+    x = sample(n)
     for _ in range(3):
-        eager_fp32_torch(q, k, v, sc)
+        step(*x)
     times = []
     for _ in range(5):
         t0 = time.perf_counter()
-        eager_fp32_torch(q, k, v, sc)
+        step(*x)
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    flops = 4.0 * D * (T * (T + 1) // 2) * n
+    if doc_row is None:
+        pairs = T * (T + 1) // 2
+    else:
+        _, counts = np.unique(doc_row.numpy()[0], return_counts=True)  # documents are contiguous runs
+        pairs = int((counts * (counts + 1) // 2).sum())
+    flops = 4.0 * D * pairs * n * (3.5 if backward else 1.0)
     cpu_model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -211,7 +233,9 @@ def cpu_baseline(cfg, budget_s, seed, purified=False):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"{n} of the {B * H} (b,h) heads of the same config, fp32, eager "
-                   f"(flash_born.py:{'1329-1341' if purified else '681-690'} restated), median of 5 runs "
+                   f"(flash_born.py:{'1329-1341' if purified else '681-690'} restated)"
+                   f"{', document mask of batch row 0' if doc_row is not None else ''}"
+                   f"{', forward + autograd backward' if backward else ''}, median of 5 runs "
                    f"after 3 warm-ups, {med * 1e3:.1f} ms per run"),
         "cpu_model": cpu_model,
         "seconds_per_run": med,
@@ -362,7 +386,8 @@ def main():
 
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
-        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed, purified)
+        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed, purified,
+                           None if doc is None else doc.cpu().numpy())
         cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
 
     name = "fwd" if not backward else "fwd+bwd"
