@@ -1053,7 +1053,15 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
                            dim3(C::NW * 64), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (!fast) {
+    if (!fast && MODE == kGeneral && a.doc != nullptr && C::DQ_NQB == 2) {
+        // Documents: 128-row query blocks straddle fewer document edges
+        // than 256-row ones, so fewer of their tiles are partly visible.
+        constexpr int BM = C::NW * 32;
+        const dim3 grid((unsigned)((a.T + BM - 1) / BM) * BH);
+        hipLaunchKernelGGL((born_bwd_dq16_kernel<E, DP, 1, C::NW, C::DQ_BN, MODE, C::DQ_WPE>), grid,
+                           dim3(C::NW * 64), 0, st, a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else if (!fast) {
         constexpr int BM = C::NW * 32 * C::DQ_NQB;
         const dim3 grid((unsigned)((a.T + BM - 1) / BM) * BH);
         hipLaunchKernelGGL((born_bwd_dq16_kernel<E, DP, C::DQ_NQB, C::NW, C::DQ_BN, MODE, C::DQ_WPE>),
