@@ -178,14 +178,6 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
     int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
-    if constexpr (kDoc) {
-        if (has_doc && ntiles > 0) {
-            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
-                                              span_red);
-            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
-            if (ntiles > 0) kv_lo = sp.x * BN;
-        }
-    }
 
     KStage kst;
     VStage vst;
@@ -208,17 +200,41 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) acc[db][qb] = zero16();
 
+    // Documents: visit only the span of key tiles whose ids meet the block's
+    // rows'.  Under causality the span ends at the block's diagonal tile (its
+    // last row sees its own key): the span is walked from there downwards,
+    // so the first tile's loads go out before the screening and overlap it.
+    int kstep = BN;
+    bool first_issued = false;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int t_top = kv_lo / BN + ntiles - 1;
+            if (causal) {
+                load_tile(t_top * BN);
+                first_issued = true;
+            }
+            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, t_top, span_red);
+            if (causal) {
+                ntiles = sp.x <= sp.y ? t_top - sp.x + 1 : 0;
+                kv_lo = t_top * BN;
+                kstep = -BN;
+            } else {
+                ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+                if (ntiles > 0) kv_lo = sp.x * BN;
+            }
+        }
+    }
     if (ntiles > 0) {
-        load_tile(kv_lo);
+        if (!first_issued) load_tile(kv_lo);
         store_tile(0);
     }
     __syncthreads();
 
     for (int t = 0; t < ntiles; ++t) {
-        const int key0 = kv_lo + t * BN;
+        const int key0 = kv_lo + t * kstep;
         const int buf = t & 1;
         const bool more = (t + 1) < ntiles;
-        if (more) load_tile(key0 + BN);
+        if (more) load_tile(key0 + kstep);
 
         bool active = q0 < T;
         bool need_mask = false;
@@ -411,14 +427,6 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     int q_hi = T;
     if (window > 0) q_hi = min(T, k0 + BK - 1 + window);
     int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
-    if constexpr (kDoc) {
-        if (has_doc && ntiles > 0) {
-            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
-                                              span_red);
-            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
-            if (ntiles > 0) q_lo = sp.x * BQ;
-        }
-    }
 
     Stage qst, dst;
     float ndreg = 0.f, zireg = 0.f;
@@ -452,8 +460,29 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         dk[db] = zero16();
     }
 
+    // Documents: visit only the span of query tiles whose ids meet the
+    // block's keys'.  Under causality the span starts at q_lo (the query tile
+    // holding key k0 sees it), so that tile's loads go out before the
+    // screening and overlap it.
+    bool first_issued = false;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            if (causal) {
+                load_tile(q_lo);
+                first_issued = true;
+            }
+            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
+                                              span_red);
+            if (causal) {
+                ntiles = sp.x <= sp.y ? sp.y - q_lo / BQ + 1 : 0;
+            } else {
+                ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+                if (ntiles > 0) q_lo = sp.x * BQ;
+            }
+        }
+    }
     if (ntiles > 0) {
-        load_tile(q_lo);
+        if (!first_issued) load_tile(q_lo);
         store_tile(0);
     }
     __syncthreads();
@@ -635,14 +664,6 @@ void born_bwd_dq32_kernel(BwdArgs p) {
     int kv_hi = causal ? min(T, m0 + BM) : T;
     if (window > 0) kv_lo = max(0, m0 - window + 1) & ~(BN - 1);
     int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
-    if constexpr (kDoc) {
-        if (has_doc && ntiles > 0) {
-            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, kv_lo / BN + ntiles - 1,
-                                              span_red);
-            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
-            if (ntiles > 0) kv_lo = sp.x * BN;
-        }
-    }
 
     Stage kst, vst;
     int dreg = -2;
@@ -661,16 +682,40 @@ void born_bwd_dq32_kernel(BwdArgs p) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = zero16();
 
+    // Documents: visit only the span of key tiles whose ids meet the block's
+    // rows'.  Under causality the span ends at the block's diagonal tile (its
+    // last row sees its own key): the span is walked from there downwards,
+    // so the first tile's loads go out before the screening and overlap it.
+    int kstep = BN;
+    bool first_issued = false;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            const int t_top = kv_lo / BN + ntiles - 1;
+            if (causal) {
+                load_tile(t_top * BN);
+                first_issued = true;
+            }
+            const int2 sp = doc_tile_span<BN>(docb, T, m0, min(T, m0 + BM), kv_lo / BN, t_top, span_red);
+            if (causal) {
+                ntiles = sp.x <= sp.y ? t_top - sp.x + 1 : 0;
+                kv_lo = t_top * BN;
+                kstep = -BN;
+            } else {
+                ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+                if (ntiles > 0) kv_lo = sp.x * BN;
+            }
+        }
+    }
     if (ntiles > 0) {
-        load_tile(kv_lo);
+        if (!first_issued) load_tile(kv_lo);
         store_tile(0);
     }
     __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
-        const int key0 = kv_lo + t * BN;
+        const int key0 = kv_lo + t * kstep;
         const int buf = t & 1;
         const bool more = (t + 1) < ntiles;
-        if (more) load_tile(key0 + BN);
+        if (more) load_tile(key0 + kstep);
         bool active = q0 < T;
         bool need_mask = false;
         if constexpr (kDoc) need_mask = has_doc && !one_document(doc_lds[buf], BN, qdoc, qdoc);
@@ -827,14 +872,6 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     int q_hi = T;
     if (window > 0) q_hi = min(T, k0 + BK - 1 + window);
     int ntiles = (q_hi > q_lo && k0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
-    if constexpr (kDoc) {
-        if (has_doc && ntiles > 0) {
-            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
-                                              span_red);
-            ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
-            if (ntiles > 0) q_lo = sp.x * BQ;
-        }
-    }
 
     Stage qst, dst;
     float ndreg = 0.f, zireg = 0.f;
@@ -866,8 +903,29 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         dk[db] = zero16();
     }
 
+    // Documents: visit only the span of query tiles whose ids meet the
+    // block's keys'.  Under causality the span starts at q_lo (the query tile
+    // holding key k0 sees it), so that tile's loads go out before the
+    // screening and overlap it.
+    bool first_issued = false;
+    if constexpr (kDoc) {
+        if (has_doc && ntiles > 0) {
+            if (causal) {
+                load_tile(q_lo);
+                first_issued = true;
+            }
+            const int2 sp = doc_tile_span<BQ>(docb, T, k0, min(T, k0 + BK), q_lo / BQ, q_lo / BQ + ntiles - 1,
+                                              span_red);
+            if (causal) {
+                ntiles = sp.x <= sp.y ? sp.y - q_lo / BQ + 1 : 0;
+            } else {
+                ntiles = sp.x <= sp.y ? sp.y - sp.x + 1 : 0;
+                if (ntiles > 0) q_lo = sp.x * BQ;
+            }
+        }
+    }
     if (ntiles > 0) {
-        load_tile(q_lo);
+        if (!first_issued) load_tile(q_lo);
         store_tile(0);
     }
     __syncthreads();
