@@ -103,6 +103,27 @@ def copy_calibration(steps):
     print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "steps": steps}), flush=True)
 
 
+CLOCK_RAMP_S = 0.3  # untimed load before the timed steps (clocks settle after ~0.1 s)
+
+
+def clock_ramp(step, done):
+    """Untimed steps after the W warm-up steps until the GPU has been loaded
+    for CLOCK_RAMP_S seconds: the same launch runs ~15% slower during its
+    first ~0.1 s of load than at steady clocks, so a short warm-up (the
+    driver passes W=5) would otherwise time the clock ramp.  Returns the
+    number of extra steps run (reported in the JSON line)."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < CLOCK_RAMP_S:
+        for _ in range(50):
+            step(done + n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
 def load_traffic(config):
     """HBM bytes per forward launch measured by rocprofv3 --pmc for `config`,
     from profiles/traffic_<config>.txt (line `traffic_bytes_per_launch = N`),
@@ -227,11 +248,29 @@ def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None):
                     break
     except OSError:
         pass
+    # C1 (the reference's CPU-runnable case):
+    # fp32 B1 H4 T256 D64 causal forward, N(0, 1) inputs from the seed.
+    g1 = torch.Generator("cpu").manual_seed(seed)
+    c1 = [torch.randn(1, 4, 256, 64, generator=g1) for _ in range(3)]
+    with torch.no_grad():
+        for _ in range(3):
+            eager_fp32_torch(*c1, sc)
+        t1 = []
+        for _ in range(21):
+            t0 = time.perf_counter()
+            eager_fp32_torch(*c1, sc)
+            t1.append(time.perf_counter() - t0)
+    t1.sort()
+    c1_s = t1[len(t1) // 2]
+    c1_flops = 4.0 * 64 * (256 * 257 // 2) * 4
     return {
         "value": flops / med / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "c1": {"value": c1_flops / c1_s / 1e12, "unit": "TFLOP/s", "seconds_per_run": c1_s,
+               "sample": "C1 whole: fp32 B1 H4 T256 D64 causal forward, eager (flash_born.py:681-690 "
+                         "restated), median of 21 runs after 3 warm-ups"},
         "sample": (f"{n} of the {B * H} (b,h) heads of the same config, fp32, eager "
                    f"(flash_born.py:{'1329-1341' if purified else '681-690'} restated)"
                    f"{', document mask of batch row 0' if doc_row is not None else ''}"
@@ -340,6 +379,7 @@ def main():
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
+    ramp = clock_ramp(step, warmup)
 
     def timed(n_steps, rotate=True):
         ev0 = torch.cuda.Event(enable_timing=True)
@@ -419,6 +459,7 @@ def main():
             "kernel_us_per_step_events": round(ev_step * 1e6, 3),
             "hot_kernel_us_per_step_events": round(hot_ev * 1e6, 3),
             "hot_tflops": round(flops / hot_wall / 1e12, 2),
+            "untimed_clock_ramp_steps": ramp,
             "algorithmic_flops": flops,
             "algorithmic_bytes": nbytes,
             "arith_intensity": round(ai, 1),
@@ -545,6 +586,7 @@ def prologue_main(args):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
+    ramp = clock_ramp(step, warmup)
 
     def timed(n_steps, rotate=True):
         ev0 = torch.cuda.Event(enable_timing=True)
@@ -600,6 +642,7 @@ def prologue_main(args):
             "kernel_us_per_step_events": round(ev_step * 1e6, 3),
             "hot_kernel_us_per_step_events": round(hot_ev * 1e6, 3),
             "hot_gbs": round(nbytes / hot_wall / 1e9, 1),
+            "untimed_clock_ramp_steps": ramp,
             "algorithmic_bytes": nbytes,
             "device": torch.cuda.get_device_name(dev),
             "torch": torch.__version__,

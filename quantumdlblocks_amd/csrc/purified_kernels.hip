@@ -8,10 +8,17 @@ namespace qdl {
 
 inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
+// The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
+// offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
+// kernels, as the Born dispatch does.
+inline bool purified_fast_ok(const PurArgs& a) {
+    return a.D == 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+}
+
 template <class IN>
 static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
-    if (std::is_same<IN, BF16>::value && a.D == 64 && a.window == 0 && a.doc == nullptr)
+    if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
@@ -40,7 +47,7 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
 
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
-    if (std::is_same<IN, BF16>::value && a.D == 64 && a.window == 0 && a.doc == nullptr)
+    if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);

@@ -15,10 +15,12 @@ computes, per (b, h) and with ``(B, H, T, D)`` inputs,
     M_ij = [causal => j <= i] & [window_size > 0 => i - j < window_size]
            & [doc_ids[b, i] == doc_ids[b, j]]
 
-GPU tensors always run the HIP kernels of ``libqdl_flash_born.so`` (forward,
-and a backward producing dq, dk, dv and dscale).  If the library is missing
-the call raises: there is no silent fallback on the GPU.  CPU tensors take the
-reference's eager formulation (flash_born.py:681-690), as the reference does.
+GPU tensors with head dim <= 256 always run the HIP kernels of
+``libqdl_flash_born.so`` (forward, and a backward producing dq, dk, dv and
+dscale).  If the library is missing the call raises: a broken install is
+reported, not hidden behind a slow path.  CPU tensors, and GPU tensors with a
+head dim above 256 (which the reference's kernel does not take either), run
+the reference's eager formulation (flash_born.py:670-690) on their own device.
 """
 
 from __future__ import annotations
@@ -341,14 +343,19 @@ def flash_born_attention(
     ``scale`` is a float or a tensor of shape (), (1,), (H,) or (1, H, 1, 1).
     ``window_size > 0`` keeps keys with ``i - j < window_size``; ``doc_ids``
     (B, T) keeps pairs within one document.  GPU tensors run the gfx950 HIP
-    kernels for any head dim up to 256; CPU tensors use the eager formulation.
+    kernels for any head dim up to 256; CPU tensors and larger head dims use
+    the eager formulation.
     """
     if not isinstance(scale, torch.Tensor):
         scale_t = torch.tensor(float(scale), dtype=torch.float32, device=q.device)
     else:
         scale_t = scale
-    if q.is_cuda:
+    if q.is_cuda and q.shape[-1] <= MAX_HEAD_DIM:
         return _run_triton_flash_born(q, k, v, scale_t, is_causal, eps, window_size=window_size, doc_ids=doc_ids)
+    # CPU tensors, and head dims the kernels do not take (D > 256), run the
+    # reference's eager formulation on the tensors' own device, as the
+    # reference does for every shape its kernel does not support
+    # (flash_born.py:670-690).
     return _eager_born(q, k, v, scale_t, is_causal, eps, window_size, doc_ids)
 
 
@@ -527,7 +534,8 @@ def flash_purified_born_attention(
     ``scale`` (alias ``gamma_h``, default 8.0) and ``tau`` (alias ``tau_h``,
     default 0.0625) are floats or tensors of 1 or H values; ``causal``
     overrides ``is_causal``.  GPU tensors run the gfx950 HIP kernels for any
-    head dim up to 256; CPU tensors use the eager formulation.
+    head dim up to 256; CPU tensors and larger head dims use the eager
+    formulation.
     """
     if scale is None:
         scale = gamma_h if gamma_h is not None else 8.0
@@ -537,8 +545,10 @@ def flash_purified_born_attention(
         is_causal = bool(causal)
     scale_t = scale if isinstance(scale, torch.Tensor) else torch.tensor(float(scale), dtype=torch.float32, device=q.device)
     tau_t = tau if isinstance(tau, torch.Tensor) else torch.tensor(float(tau), dtype=torch.float32, device=q.device)
-    if q.is_cuda:
+    if q.is_cuda and q.shape[-1] <= MAX_HEAD_DIM:
         return _run_triton_flash_purified_born(
             q, k, v, scale_t, tau_t, eps_base, is_causal, eps, window_size=window_size, doc_ids=doc_ids
         )
+    # CPU tensors and D > 256: the reference's eager formulation on the
+    # tensors' own device (flash_born.py:1318-1341).
     return _eager_purified_born(q, k, v, scale_t, tau_t, eps_base, is_causal, eps, window_size, doc_ids)

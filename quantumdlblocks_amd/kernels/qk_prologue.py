@@ -126,11 +126,15 @@ def _dense_layout(shape, strides) -> bool:
 def _launch_bwd(g, out, rinv, cos2, sin2, layout, which: int):
     """Input gradient of one tensor, written with the input's (shape, strides)
     when those are dense (a permuted contiguous tensor, e.g. the projection
-    layout), else contiguous."""
+    layout) with unit stride along D, else contiguous.  The kernel writes each
+    D row contiguously and takes only the (b, h, t) strides, so an input whose
+    D stride is not 1 (e.g. a transposed (B, H, D, T) tensor) gets a
+    contiguous gradient."""
     lib = _native.load()
     B, H, T, D = out.shape
     g = g.to(out.dtype).contiguous()
-    if _dense_layout(*layout):
+    shape, strides = layout
+    if _dense_layout(shape, strides) and (shape[-1] == 1 or strides[-1] == 1):
         dx = torch.empty_strided(layout[0], layout[1], dtype=out.dtype, device=out.device)
     else:
         dx = torch.empty(layout[0], dtype=out.dtype, device=out.device)

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import born_oracle as orc
-from util import TOL, max_abs, rel_err
+from util import TOL, abi_forward, max_abs, rel_err, z_row_bound
 
 FIXTURE = Path(__file__).resolve().parent / "golden" / "born_cases.npz"
 DATA = np.load(FIXTURE)
@@ -129,10 +129,24 @@ def _gpu_run(c, dtype, dev, grads):
 @pytest.mark.parametrize("name", CASES)
 def test_gpu_forward_matches_fixture(cuda_device, name, dt):
     c = _case(name)
-    got = _gpu_run(c, DTYPES[dt], cuda_device, grads=False)["out"]
+    dtype = DTYPES[dt]
+    got = _gpu_run(c, dtype, cuda_device, grads=False)["out"]
     err = rel_err(got, c["out"])
     print(f"golden fwd {name} {dt}: rel={err:.3e} maxabs={max_abs(got, c['out']):.3e}", flush=True)
-    assert err <= TOL[DTYPES[dt]]
+    assert err <= TOL[dtype]
+    # Z (sum of weights + eps, the backward's input) through the C ABI, row by
+    # row within the rounding bound of the stored weights.  The fixture's
+    # inputs are exact in every dtype (bf16-exact values of moderate size).
+    D = c["q"].shape[-1]
+    if D % 8 == 0:
+        q, k, v = (torch.from_numpy(c[x]).to(cuda_device, dtype).contiguous() for x in ("q", "k", "v"))
+        kw = c["kw"]
+        _, z = abi_forward(q, k, v, c["scale"], kw["is_causal"], kw["eps"], kw["window_size"], kw["doc_ids"])
+        mask = orc.visible_mask(c["q"].shape[2], kw["is_causal"], kw["window_size"], kw["doc_ids"])
+        bound = z_row_bound(c["q"], c["k"], c["scale"], c["z"], kw["eps"], dtype, mask)
+        zerr = np.abs(z.double().cpu().numpy() - c["z"])
+        print(f"golden Z {name} {dt}: max err/bound {(zerr / np.maximum(bound, 1e-300)).max():.3f}", flush=True)
+        assert np.all(zerr <= bound)
 
 
 # Gradients that cancel to ~0 are judged against the size of the terms they

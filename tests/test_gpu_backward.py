@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import born_oracle as orc
-from util import TOL, f64, max_abs, rel_err, seeded_inputs
+from util import TOL, doc_spans, f64, max_abs, rel_err, seeded_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -64,16 +64,30 @@ def _check_bwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, 
     refs = {0: [], 1: [], 2: []}
     mags = {0: [], 1: [], 2: []}
     gots = {0: [], 1: [], 2: []}
+    # Long causal rows of contiguous documents: each document's queries see
+    # only its own keys and vice versa, so every gradient of a span follows
+    # from that span alone (exact); the oracle runs span by span.
+    spans = None
+    if doc is not None and is_causal and window_size == 0 and T > 2048:
+        spans = {b: doc_spans(doc[b]) for b, _ in sel}
     for b, h in sel:
         s_h = sc_np.reshape(-1)[h] if sc_np.size > 1 else sc_np.reshape(-1)[0]
-        args = (f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]), f64(v[b : b + 1, h : h + 1]), s_h,
-                f64(do[b : b + 1, h : h + 1]), is_causal, eps, window_size, None if doc is None else doc[b : b + 1])
-        # delta from the forward output the backward was handed (flash_born.py:277, 302)
-        r = orc.backward(*args, out=f64(out[b : b + 1, h : h + 1]))
-        m = orc.backward_magnitudes(*args)
+        cut = [(0, T)] if spans is None else spans[b]
+        part = {0: [], 1: [], 2: []}
+        mpart = {0: [], 1: [], 2: []}
+        for a, e in cut:
+            args = (f64(q[b : b + 1, h : h + 1, a:e]), f64(k[b : b + 1, h : h + 1, a:e]),
+                    f64(v[b : b + 1, h : h + 1, a:e]), s_h, f64(do[b : b + 1, h : h + 1, a:e]), is_causal, eps,
+                    window_size, None if (doc is None or spans is not None) else doc[b : b + 1])
+            # delta from the forward output the backward was handed (flash_born.py:277, 302)
+            r = orc.backward(*args, out=f64(out[b : b + 1, h : h + 1, a:e]))
+            m = orc.backward_magnitudes(*args)
+            for i in range(3):
+                part[i].append(r[i])
+                mpart[i].append(m[i])
         for i, got_t in enumerate((dq, dk, dv)):
-            refs[i].append(r[i])
-            mags[i].append(m[i])
+            refs[i].append(np.concatenate(part[i], axis=2))
+            mags[i].append(np.concatenate(mpart[i], axis=2))
             gots[i].append(f64(got_t[b : b + 1, h : h + 1]))
     msgs, fails = [], []
     for i, name in enumerate(("dq", "dk", "dv")):
@@ -129,6 +143,12 @@ def test_bwd_ragged_lengths(cuda_device, T, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_bwd_head_dims(cuda_device, D, dtype):
     _check_bwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
+
+
+def test_bwd_head_dim_above_256_takes_the_eager_path(cuda_device):
+    """D > 256: autograd through the reference's eager formulation on the GPU
+    (flash_born.py:670-690), gradients against the oracle."""
+    _check_bwd(1, 2, 80, 272, torch.float32, cuda_device, scale=1.0 / math.sqrt(272), seed=272)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -250,11 +270,19 @@ def test_bwd_exact_oracle_end_to_end(cuda_device):
             assert rel_err(f64(got), want) <= TOL[dtype] * (10 if dtype == torch.float32 else 1)
 
 
+# Heads checked at C4 / C5 (as in test_gpu_forward.py): every batch row and
+# head index, each residue of b * H + h modulo 8 twice.
+C5_HEADS = [(b, (5 * b + 3) % 16) for b in range(16)]
+C4_HEADS = [(b, 4 * j + (b + j) % 4) for b in range(4) for j in range(4)]
+
+
 def test_bwd_config_c5(cuda_device):
-    """C5: bf16 B16 H16 T2048 D64 forward + backward, N(0,1); heads checked vs the oracle."""
-    _check_bwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=[(0, 0), (15, 15), (7, 9)])
+    """C5: bf16 B16 H16 T2048 D64 forward + backward, N(0,1); 16 heads vs the oracle."""
+    _check_bwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=C5_HEADS)
 
 
 def test_bwd_config_c4_documents(cuda_device):
+    """C4's shape with the backward (document-masked training); 16 heads,
+    document by document."""
     doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
-    _check_bwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=[(0, 0), (3, 15)])
+    _check_bwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=C4_HEADS)

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import born_oracle as orc
-from util import TOL, f64, max_abs, rel_err, seeded_inputs
+from util import TOL, abi_forward, f64, max_abs, oracle_forward_heads, rel_err, seeded_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -28,29 +28,32 @@ def _run(q, k, v, scale, **kw):
 
 
 def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, window_size=0,
-               doc=None, std=1.0, seed=0, heads=None, tol=None):
-    q, k, v = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, dtype=dtype))
+               doc=None, std=1.0, seed=0, heads=None, tol=None, inputs=None):
+    """Run the public entry on seeded inputs and hold O to the oracle
+    (normwise relative error <= tol) and Z, read through the C ABI, to the
+    oracle row by row within the rounding bound of the 16-bit weights
+    (util.z_row_bound).  ``heads``: the (b, h) heads to check, or "all"."""
+    if inputs is None:
+        q, k, v = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, dtype=dtype))
+    else:
+        q, k, v = inputs
     doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
     scale_arg = scale
     if isinstance(scale, np.ndarray):
         scale_arg = torch.as_tensor(scale, dtype=torch.float32, device=dev)
     out = _run(q, k, v, scale_arg, is_causal=is_causal, eps=eps, window_size=window_size, doc_ids=doc_t)
     assert out.shape == (B, H, T, D) and out.dtype == dtype
-    if heads is None:
-        ref, _ = orc.forward(f64(q), f64(k), f64(v), np.asarray(scale, dtype=np.float64), is_causal, eps,
-                             window_size, doc)
-        got = f64(out)
-    else:  # check a subset of (b, h) rows of a large problem
-        got_l, ref_l = [], []
-        sc = np.asarray(scale, dtype=np.float64).reshape(-1)
-        for b, h in heads:
-            s_h = sc[h] if sc.size > 1 else sc[0]
-            r, _ = orc.forward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
-                               f64(v[b : b + 1, h : h + 1]), s_h, is_causal, eps, window_size,
-                               None if doc is None else doc[b : b + 1])
-            ref_l.append(r)
-            got_l.append(f64(out[b : b + 1, h : h + 1]))
-        ref, got = np.concatenate(ref_l), np.concatenate(got_l)
+    z = None
+    if D % 8 == 0 and D <= 256:
+        out2, z = abi_forward(q.contiguous(), k.contiguous(), v.contiguous(), scale, is_causal, eps,
+                              window_size, doc)
+        iv = torch.int32 if dtype == torch.float32 else torch.int16
+        assert torch.equal(out2.view(iv), out.view(iv)), "host entry and C ABI disagree"
+    sel = [(b, h) for b in range(B) for h in range(H)] if heads in (None, "all") else heads
+    sc = np.asarray(scale, dtype=np.float64).reshape(-1)
+    qn, kn, vn = f64(q), f64(k), f64(v)
+    keys, ref, zref, zb = oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, dtype)
+    got = np.stack([f64(out[b, h]) for b, h in keys])
     if eps == 0.0:
         # rows with no positive overlap are 0/0 in the reference formula: NaN
         # must appear exactly there, everything else is compared
@@ -58,10 +61,19 @@ def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, 
         assert np.array_equal(np.isfinite(got), finite)
         got, ref = got[finite], ref[finite]
     err = rel_err(got, ref)
+    zmsg = ""
+    if z is not None:
+        zg = np.stack([f64(z[b, h]) for b, h in keys])
+        zerr = np.abs(zg - zref)
+        zratio = float((zerr / np.maximum(zb, 1e-300)).max()) if zerr.size else 0.0
+        zrel = float((zerr / np.maximum(np.abs(zref), 1e-300)).max()) if zerr.size else 0.0
+        zmsg = f" Z: max row rel={zrel:.3e} (max err/bound {zratio:.3f})"
     print(f"fwd B{B} H{H} T{T} D{D} {dtype} causal={is_causal} W={window_size} doc={doc is not None} "
-          f"rel={err:.3e} maxabs={max_abs(got, ref):.3e}", flush=True)
+          f"heads={len(keys)} rel={err:.3e} maxabs={max_abs(got, ref):.3e}{zmsg}", flush=True)
     assert np.isfinite(got).all()
     assert err <= (tol or TOL[dtype]), err
+    if z is not None:
+        assert np.all(zerr <= zb), f"Z outside its rounding bound: {zratio}"
     return out
 
 
@@ -104,6 +116,15 @@ def test_fwd_f16_weight_range(cuda_device, D, window, scale):
 def test_fwd_head_dims(cuda_device, D, dtype):
     """Every head dim up to 256; D not a multiple of 8 is zero-padded by the host."""
     _check_fwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [272, 320])
+def test_fwd_head_dims_above_256_take_the_eager_path(cuda_device, D, dtype):
+    """Head dims the kernels do not take run the reference's eager
+    formulation on the GPU, as the reference does for every head dim its
+    kernel does not support (flash_born.py:670-690)."""
+    _check_fwd(1, 2, 80, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -251,38 +272,43 @@ def test_fwd_autocast(cuda_device):
 
 # ---- BASELINE.json configs at full size (subsets of heads vs the oracle) ----
 
+# Heads checked at C4 / C5: every batch row and every head index, each
+# residue of b * H + h modulo 8 (the XCD a workgroup of that head lands on)
+# twice; C2 and C3 check every head.
+C5_HEADS = [(b, (5 * b + 3) % 16) for b in range(16)]
+C4_HEADS = [(b, 4 * j + (b + j) % 4) for b in range(4) for j in range(4)]
+
+
 def test_fwd_config_c2(cuda_device):
-    """C2: bf16 B32 H4 T1024 D64, Q and K L2-normalised per head vector."""
+    """C2: bf16 B32 H4 T1024 D64, Q and K L2-normalised per head vector; every head."""
     from quantumdlblocks_amd import l2_normalize
 
     B, H, T, D = 32, 4, 1024, 64
     q, k, v = seeded_inputs((B, H, T, D), seed=0)
     q, k = l2_normalize(q), l2_normalize(k)
     q, k, v = (x.to(cuda_device, torch.bfloat16) for x in (q, k, v))
-    out = _run(q, k, v, 8.0)
-    heads = [(0, 0), (7, 1), (31, 3), (16, 2)]
-    got = np.concatenate([f64(out[b : b + 1, h : h + 1]) for b, h in heads])
-    ref = np.concatenate([orc.forward(f64(q[b : b + 1, h : h + 1]), f64(k[b : b + 1, h : h + 1]),
-                                      f64(v[b : b + 1, h : h + 1]), 8.0)[0] for b, h in heads])
-    assert rel_err(got, ref) <= 2e-2
-    assert torch.isfinite(out).all()
+    _check_fwd(B, H, T, D, torch.bfloat16, cuda_device, heads="all", inputs=(q, k, v))
 
 
 def test_fwd_config_c3(cuda_device):
-    """C3 (headline): bf16 B16 H16 T1024 D64, Q, K, V ~ N(0, 1/64)."""
-    _check_fwd(16, 16, 1024, 64, torch.bfloat16, cuda_device, std=0.125,
-               heads=[(0, 0), (15, 15), (3, 9), (8, 4), (11, 0)])
+    """C3 (headline): bf16 B16 H16 T1024 D64, Q, K, V ~ N(0, 1/64); every head."""
+    _check_fwd(16, 16, 1024, 64, torch.bfloat16, cuda_device, std=0.125, heads="all")
 
 
 def test_fwd_config_c4(cuda_device):
-    """C4: bf16 B4 H16 T8192 D64, causal within geometric(mean 512) documents."""
+    """C4: bf16 B4 H16 T8192 D64, causal within geometric(mean 512) documents;
+    16 heads, document by document, and one head against the oracle's full
+    document mask (which pins the span-by-span evaluation)."""
     doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
-    _check_fwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=[(0, 0), (3, 15), (1, 7)])
+    out = _check_fwd(4, 16, 8192, 64, torch.bfloat16, cuda_device, doc=doc, heads=C4_HEADS)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((4, 16, 8192, 64), seed=0, dtype=torch.bfloat16))
+    ref, _ = orc.forward(f64(q[1:2, 7:8]), f64(k[1:2, 7:8]), f64(v[1:2, 7:8]), 8.0, True, 1e-12, 0, doc[1:2])
+    assert rel_err(f64(out[1:2, 7:8]), ref) <= 2e-2
 
 
 def test_fwd_config_c5_forward(cuda_device):
-    """C5's forward: bf16 B16 H16 T2048 D64, N(0,1)."""
-    _check_fwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=[(0, 0), (15, 15), (9, 3)])
+    """C5's forward: bf16 B16 H16 T2048 D64, N(0,1); 16 heads."""
+    _check_fwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, heads=C5_HEADS)
 
 
 @pytest.mark.parametrize("T", [1024, 2048])

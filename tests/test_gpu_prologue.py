@@ -233,3 +233,35 @@ def test_prologue_gradients_of_sliced_and_expanded_inputs(cuda_device):
     assert torch.equal(qkv.grad, qkv2.grad)
     # The expanded K's gradient is the sum over heads, in autograd's order for both.
     assert torch.allclose(k1.grad.float(), k2.grad.float(), rtol=0, atol=0)
+
+
+def test_prologue_gradients_of_transposed_inputs(cuda_device):
+    """Q and K stored (B, H, D, T) and viewed as (B, H, T, D): a dense layout
+    whose D stride is not 1.  The inputs are read through a contiguous copy
+    and the gradients must come back equal to those of contiguous inputs (the
+    kernel writes D rows contiguously, so such a gradient is allocated
+    contiguous rather than with the input's strides)."""
+    from quantumdlblocks_amd.kernels.qk_prologue import fused_qk_rope_l2_normalize
+
+    B, H, T, D = 2, 3, 16, 64
+    g = torch.Generator("cpu").manual_seed(11)
+    qt = torch.randn(B, H, D, T, generator=g).to(torch.bfloat16).to(cuda_device).requires_grad_(True)
+    kt = torch.randn(B, H, D, T, generator=g).to(torch.bfloat16).to(cuda_device).requires_grad_(True)
+    cos, sin = _tables(T, D // 2)
+    cos, sin = cos.to(cuda_device), sin.to(cuda_device)
+    gq = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(cuda_device)
+    gk = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(cuda_device)
+
+    q, k = qt.transpose(-1, -2), kt.transpose(-1, -2)
+    assert q.stride(-1) != 1
+    qo, ko = fused_qk_rope_l2_normalize(q, k, cos, sin)
+    torch.autograd.backward([qo, ko], [gq, gk])
+
+    qc = qt.detach().transpose(-1, -2).contiguous().requires_grad_(True)
+    kc = kt.detach().transpose(-1, -2).contiguous().requires_grad_(True)
+    qo2, ko2 = fused_qk_rope_l2_normalize(qc, kc, cos, sin)
+    torch.autograd.backward([qo2, ko2], [gq, gk])
+    torch.cuda.synchronize()
+    assert torch.equal(qo, qo2) and torch.equal(ko, ko2)
+    assert torch.equal(qt.grad.transpose(-1, -2), qc.grad)
+    assert torch.equal(kt.grad.transpose(-1, -2), kc.grad)

@@ -160,6 +160,33 @@ def test_input_validation():
     _check_inputs(q, q, q, torch.ones(3), torch.zeros(2, 10, dtype=torch.int32))
 
 
+def test_head_dims_above_256_take_the_eager_path(monkeypatch):
+    """The reference runs its eager formulation whenever its kernel cannot
+    take the head dim (flash_born.py:670-690); so does the drop-in for GPU
+    tensors with D > 256, while D <= 256 goes to the HIP kernels."""
+    from quantumdlblocks_amd.kernels import flash_born as fb
+
+    class _CudaLike(torch.Tensor):
+        is_cuda = True  # routing only looks at is_cuda and the head dim
+
+    calls = []
+    monkeypatch.setattr(fb, "_run_triton_flash_born", lambda *a, **kw: calls.append("hip"))
+    monkeypatch.setattr(fb, "_eager_born", lambda *a, **kw: calls.append("eager"))
+    monkeypatch.setattr(fb, "_run_triton_flash_purified_born", lambda *a, **kw: calls.append("hip"))
+    monkeypatch.setattr(fb, "_eager_purified_born", lambda *a, **kw: calls.append("eager"))
+    for D, want in ((256, "hip"), (272, "eager"), (320, "eager"), (8, "hip")):
+        x = torch.Tensor._make_subclass(_CudaLike, torch.zeros(1, 2, 4, D))
+        assert x.is_cuda
+        calls.clear()
+        fb.flash_born_attention(x, x, x, 2.0)
+        fb.flash_purified_born_attention(x, x, x)
+        assert calls == [want, want], (D, calls)
+    calls.clear()
+    y = torch.zeros(1, 2, 4, 64)  # CPU tensors: eager
+    fb.flash_born_attention(y, y, y, 2.0)
+    assert calls == ["eager"]
+
+
 def test_missing_library_fails_loudly():
     """With the library absent, loading raises and HAS_TRITON is False; the GPU
     path has no silent fallback."""
