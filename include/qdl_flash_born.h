@@ -50,6 +50,12 @@ extern "C" {
 #define QDL_BORN_E_TAU (-9)
 #define QDL_BORN_E_TABLE (-10)
 #define QDL_BORN_E_ROPEDIM (-11)
+#define QDL_BORN_E_SCRATCH (-12)
+
+/* Size of the fixed device array qdl_flash_born_bwd_noalloc takes its
+ * workspace from (one per GPU): 16 MiB, enough for B * H * T up to about
+ * 1.39 million rows (C5's B16 H16 T2048 needs 6.3 MB). */
+#define QDL_BORN_BWD_SCRATCH_BYTES (16 * 1024 * 1024)
 
 typedef struct ihipStream_t *qdl_stream_t; /* == hipStream_t */
 
@@ -101,6 +107,33 @@ int qdl_flash_born_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
                        int64_t window_size, double eps, void *dq, void *dk,
                        void *dv, float *dscale, void *workspace,
                        int64_t workspace_bytes, qdl_stream_t stream);
+
+/*
+ * Backward pass that allocates nothing: qdl_flash_born_bwd with the
+ * workspace taken from a fixed device array of QDL_BORN_BWD_SCRATCH_BYTES
+ * inside the library instead of from the caller.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It calls no hipMalloc, hipFree or allocating
+ * library routine; the caller still passes every input and output.  Each GPU
+ * holds its own array until the process ends; its device address is looked
+ * up on the first call on that GPU, so call with the device of `stream`
+ * current.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams or threads) race.  A problem whose workspace
+ * (qdl_flash_born_bwd_workspace_size) exceeds QDL_BORN_BWD_SCRATCH_BYTES is
+ * rejected with QDL_BORN_E_SCRATCH before any HIP call; otherwise arguments,
+ * results and return codes are those of qdl_flash_born_bwd.
+ */
+int qdl_flash_born_bwd_noalloc(int dtype, int64_t B, int64_t H, int64_t T,
+                               int64_t D, const void *q, const void *k,
+                               const void *v, const void *out,
+                               const void *dout, const float *z,
+                               const float *scale, int64_t n_scale,
+                               const int32_t *doc_ids, int is_causal,
+                               int64_t window_size, double eps, void *dq,
+                               void *dk, void *dv, float *dscale,
+                               qdl_stream_t stream);
 
 /*
  * Purified-Born attention (flash_born.py:693-1341): weights

@@ -20,6 +20,10 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
 
+# Size of the fixed device array qdl_flash_born_bwd_noalloc uses
+# (QDL_BORN_BWD_SCRATCH_BYTES in the header).
+BWD_SCRATCH_BYTES = 16 * 1024 * 1024
+
 # Every symbol the header declares (checked by tests/test_native_abi.py).
 EXPORTED_SYMBOLS = (
     "qdl_flash_born_version",
@@ -28,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "qdl_flash_born_fwd",
     "qdl_flash_born_bwd_workspace_size",
     "qdl_flash_born_bwd",
+    "qdl_flash_born_bwd_noalloc",
     "qdl_flash_purified_born_fwd",
     "qdl_flash_purified_born_bwd_workspace_size",
     "qdl_flash_purified_born_bwd",
@@ -74,6 +79,14 @@ def _bind(lib: ctypes.CDLL) -> None:
         _int, _i64, _dbl,                  # is_causal, window_size, eps
         _ptr, _ptr, _ptr, _ptr,            # dq, dk, dv, dscale
         _ptr, _i64, _ptr,                  # workspace, workspace_bytes, stream
+    ]
+    lib.qdl_flash_born_bwd_noalloc.restype = _int
+    lib.qdl_flash_born_bwd_noalloc.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # q, k, v, out, dout
+        _ptr, _ptr, _i64, _ptr,            # z, scale, n_scale, doc_ids
+        _int, _i64, _dbl,                  # is_causal, window_size, eps
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # dq, dk, dv, dscale, stream
     ]
     lib.qdl_flash_purified_born_fwd.restype = _int
     lib.qdl_flash_purified_born_fwd.argtypes = [

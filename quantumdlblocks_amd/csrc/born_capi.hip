@@ -49,6 +49,9 @@ const char* qdl_flash_born_strerror(int code) {
         case QDL_BORN_E_TAU: return "tau must hold 1 value or exactly H values";
         case QDL_BORN_E_TABLE: return "rotary table invalid (n_freq above D/2, table_ld below n_freq, or sin missing)";
         case QDL_BORN_E_ROPEDIM: return "Q/K prologue head dim must be even and in [2, 256]";
+        case QDL_BORN_E_SCRATCH:
+            return "problem needs more backward workspace than the fixed 16 MiB array of "
+                   "qdl_flash_born_bwd_noalloc (use qdl_flash_born_bwd with a caller workspace)";
         default: break;
     }
     if (code > 0) return hipGetErrorString((hipError_t)code);
