@@ -238,6 +238,39 @@ int qdl_flash_born_qk_prologue_bwd(int dtype, int64_t B, int64_t H, int64_t T,
                                    const int64_t *dk_strides,
                                    qdl_stream_t stream);
 
+/*
+ * Forward with the Q/K prologue folded into the attention kernel's loads:
+ *   q' = l2_normalize(apply_unitary_rope(q, c, s)), k' likewise (exactly as
+ *   qdl_flash_born_qk_prologue_fwd computes them), then Born attention of
+ *   (q', k', v) as qdl_flash_born_fwd computes it.
+ * q, k: raw rows with (b, h, t) element strides (q_strides, k_strides: host
+ * arrays of 3, unit stride along D), e.g. the (B, T, H, D) projection output;
+ * v, out: contiguous (B, H, T, D); the tables and norm_eps as for the
+ * prologue; scale, doc_ids, is_causal, window_size, eps as for the forward.
+ * Also writes q_out, k_out (contiguous (B, H, T, D), the normalised rows) and
+ * q_rinv, k_rinv (1/norm per row), which the backward needs.  For bf16 with
+ * D == 64, no documents and no window, one kernel normalises each query
+ * block as it is loaded and each key tile in LDS before its use, so the
+ * normalised Q and K are never read back from memory; other cases run the
+ * prologue kernel and then the attention kernels (same results).
+ * Replaces the apply_unitary_rope + l2_normalize calls on Q and K
+ * (attention.py:583-589) together with the flash_born_attention call that
+ * consumes them (attention.py:704-713, flash_born.py:475-513).
+ */
+int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T,
+                                   int64_t D, const void *q,
+                                   const int64_t *q_strides, const void *k,
+                                   const int64_t *k_strides, const void *v,
+                                   const float *cos_table,
+                                   const float *sin_table, int64_t n_freq,
+                                   int64_t table_ld, double norm_eps,
+                                   const float *scale, int64_t n_scale,
+                                   const int32_t *doc_ids, int is_causal,
+                                   int64_t window_size, double eps, void *out,
+                                   float *z, void *q_out, void *k_out,
+                                   float *q_rinv, float *k_rinv,
+                                   qdl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

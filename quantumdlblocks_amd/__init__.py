@@ -10,6 +10,7 @@ from .kernels import (
     HAS_TRITON,
     IS_HIP,
     flash_born_attention,
+    flash_born_attention_qk_prologue,
     flash_purified_born_attention,
     fused_qk_rope_l2_normalize,
     get_flash_born_launch_meta,
@@ -26,6 +27,7 @@ __all__ = [
     "apply_unitary_rope",
     "compute_document_ids",
     "flash_born_attention",
+    "flash_born_attention_qk_prologue",
     "flash_purified_born_attention",
     "fused_qk_rope_l2_normalize",
     "get_flash_born_launch_meta",

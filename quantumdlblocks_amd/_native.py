@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "qdl_flash_purified_born_bwd",
     "qdl_flash_born_qk_prologue_fwd",
     "qdl_flash_born_qk_prologue_bwd",
+    "qdl_flash_born_fwd_qk_prologue",
 )
 
 
@@ -112,6 +113,15 @@ def _bind(lib: ctypes.CDLL) -> None:
         _ptr, _ptr, _ptr, _ptr,            # q, q_strides, k, k_strides
         _ptr, _ptr, _i64, _i64, _dbl,      # cos, sin, n_freq, table_ld, eps
         _ptr, _ptr, _ptr, _ptr, _ptr,      # q_out, k_out, q_rinv, k_rinv, stream
+    ]
+    lib.qdl_flash_born_fwd_qk_prologue.restype = _int
+    lib.qdl_flash_born_fwd_qk_prologue.argtypes = [
+        _int, _i64, _i64, _i64, _i64,      # dtype, B, H, T, D
+        _ptr, _ptr, _ptr, _ptr, _ptr,      # q, q_strides, k, k_strides, v
+        _ptr, _ptr, _i64, _i64, _dbl,      # cos, sin, n_freq, table_ld, norm_eps
+        _ptr, _i64, _ptr, _int, _i64, _dbl,  # scale, n_scale, doc_ids, is_causal, window_size, eps
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,  # out, z, q_out, k_out, q_rinv, k_rinv
+        _ptr,                              # stream
     ]
     lib.qdl_flash_born_qk_prologue_bwd.restype = _int
     lib.qdl_flash_born_qk_prologue_bwd.argtypes = [

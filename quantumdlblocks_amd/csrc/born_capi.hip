@@ -154,4 +154,71 @@ int qdl_flash_born_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, co
     }
 }
 
+int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, const void* q,
+                                   const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                   const void* v, const float* cos_table, const float* sin_table,
+                                   int64_t n_freq, int64_t table_ld, double norm_eps, const float* scale,
+                                   int64_t n_scale, const int32_t* doc_ids, int is_causal,
+                                   int64_t window_size, double eps, void* out, float* z, void* q_out,
+                                   void* k_out, float* q_rinv, float* k_rinv, qdl_stream_t stream) {
+    int rc = check_common(dtype, B, H, T, D, n_scale, window_size, eps);
+    if (rc != QDL_BORN_OK) return rc;
+    if (cos_table && (!sin_table || n_freq < 0 || n_freq > D / 2 || table_ld < n_freq)) return QDL_BORN_E_TABLE;
+    if (!(norm_eps >= 0.0)) return QDL_BORN_E_SHAPE;
+    if (B * H * T == 0) return QDL_BORN_OK;
+    if (!q || !k || !v || !q_strides || !k_strides || !out || !z || !scale || !q_out || !k_out || !q_rinv ||
+        !k_rinv)
+        return QDL_BORN_E_NULL;
+    if (!aligned16(v) || !aligned16(out) || !aligned16(q_out) || !aligned16(k_out)) return QDL_BORN_E_ALIGN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // The fused kernel: bf16, D = 64, dense or causal, raw rows 16-byte
+    // aligned with (T + 256) rows of their time stride within 32-bit offsets.
+    auto rows_ok = [&](const void* p, const int64_t* st) {
+        return aligned16(p) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[2] >= D &&
+               (T + 256) * st[2] * 2 < ((int64_t)1 << 31);
+    };
+    if (dtype == QDL_BORN_DTYPE_BF16 && D == 64 && !doc_ids && window_size == 0 && rows_ok(q, q_strides) &&
+        rows_ok(k, k_strides) && (!cos_table || n_freq >= 1) && (T + 256) * D * 2 < ((int64_t)1 << 31)) {
+        qdl::FwdProArgs a;
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.o = out;
+        a.z = z;
+        a.scale = scale;
+        a.doc = nullptr;
+        a.per_head_scale = n_scale > 1 ? 1 : 0;
+        a.B = (int)B;
+        a.H = (int)H;
+        a.T = (int)T;
+        a.D = (int)D;
+        a.is_causal = is_causal ? 1 : 0;
+        a.window = 0;
+        a.eps = (float)eps;
+        a.q_sb = q_strides[0];
+        a.q_sh = q_strides[1];
+        a.q_st = q_strides[2];
+        a.k_sb = k_strides[0];
+        a.k_sh = k_strides[1];
+        a.k_st = k_strides[2];
+        a.cos = cos_table;
+        a.sin = cos_table ? sin_table : nullptr;
+        a.ld = (int)table_ld;
+        a.nfreq = (int)n_freq;
+        a.norm_eps = (float)norm_eps;
+        a.q_out = q_out;
+        a.k_out = k_out;
+        a.q_rinv = q_rinv;
+        a.k_rinv = k_rinv;
+        return hip_status(qdl::fwd_prologue_launch_bf16(a, s));
+    }
+    // Every other case: the prologue kernel, then the attention kernels on
+    // its output (the same rows and results, two launches).
+    rc = qdl_flash_born_qk_prologue_fwd(dtype, B, H, T, D, q, q_strides, k, k_strides, cos_table, sin_table,
+                                        n_freq, table_ld, norm_eps, q_out, k_out, q_rinv, k_rinv, stream);
+    if (rc != QDL_BORN_OK) return rc;
+    return qdl_flash_born_fwd(dtype, B, H, T, D, q_out, k_out, v, out, z, scale, n_scale, doc_ids, is_causal,
+                              window_size, eps, stream);
+}
+
 }  // extern "C"

@@ -24,4 +24,9 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
+hipError_t fwd_prologue_launch_bf16(const FwdProArgs& a, hipStream_t s) {
+    if (a.D != 64 || a.doc != nullptr || a.window != 0) return hipErrorInvalidValue;
+    return a.is_causal ? launch_fwd16_fast_prologue<kCausal>(a, s) : launch_fwd16_fast_prologue<kDense>(a, s);
+}
+
 }  // namespace qdl

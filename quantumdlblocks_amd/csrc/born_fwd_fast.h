@@ -126,11 +126,13 @@ __host__ __device__ inline int fast_fwd_npair(int T, int BM) { return (fast_fwd_
 // pairs have their weight zeroed (a zero overlap still weighs
 // relu(-gamma tau)^4 when tau < 0).  Output rows are stored straight from the
 // accumulators.
-template <class E, int DP, int MODE, bool PUR = false>
+template <class E, int DP, int MODE, bool PUR = false, bool PRO = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
+void born_fwd16_fast_kernel(
+    typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
     static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
+    static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
     constexpr int KS = DP / 16;
@@ -200,8 +202,20 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
-    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
-    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    // Bytes between consecutive Q / K rows: RB, or the raw rows' time stride
+    // when the prologue is fused (the host keeps (T + 256) rows of it within
+    // 32-bit offsets).
+    uint32_t qrow_b = RB, krow_b = RB;
+    size_t qbase = base, kbase_el = base;
+    if constexpr (PRO) {
+        const int b = bh / p.H;
+        qrow_b = (uint32_t)p.q_st * 2u;
+        krow_b = (uint32_t)p.k_st * 2u;
+        qbase = (size_t)b * p.q_sb + (size_t)h * p.q_sh;
+        kbase_el = (size_t)b * p.k_sb + (size_t)h * p.k_sh;
+    }
+    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + qbase, (uint32_t)T * qrow_b);
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + kbase_el, (uint32_t)T * krow_b);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
 
     // Tile u of the block's sequence -> stage st: wave-instruction i writes
@@ -215,7 +229,8 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
             const int off = (key0 + row) * RB;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ lds_swz(row)) << 4));
+            const int koff = PRO ? (key0 + row) * (int)krow_b : off;
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), koff + ((pc ^ lds_swz(row)) << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
         }
     };
@@ -225,7 +240,7 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             const int slot = (wave * LQW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
             dma_load16<true>(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
-                             (mb * BM + row) * RB + ((pc ^ (row & 7)) << 4));
+                             (mb * BM + row) * (int)qrow_b + ((pc ^ (row & 7)) << 4));
         }
     };
 
@@ -428,19 +443,191 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
     // of the scale is folded into Q; the asm pins the result in registers so
     // it is not recomputed inside the tile loop.
-    auto load_q = [&]() __attribute__((always_inline)) {
+    // Fused Q/K prologue (PRO): x' = l2_normalize(rope(x)) with the rounding
+    // of the standalone prologue kernel (qk_prologue.hip), so the rows are
+    // bit-identical to its output: each table entry, product, sum and
+    // difference rounded to bf16, the fp32 sum of squares accumulated pair by
+    // pair and then across the row's four 8-pair chunks as ((c0 + c1) +
+    // (c2 + c3)), 1/norm = 1/sqrt(sum + eps) correctly rounded from double.
+    // Chunk c of a row (columns 8c .. 8c+7) rotates against chunk c + 4.
+    // The prologue's parameters are re-read from the kernel argument segment
+    // where they are used (scalar loads), rather than held in registers
+    // through the tile loop, whose scalar and vector registers are all taken.
+    typedef const __attribute__((address_space(4))) FwdProArgs* KargPtr;
+    auto pro_args = [&]() __attribute__((always_inline)) -> KargPtr {
+        KargPtr ka = (KargPtr)(__builtin_amdgcn_kernarg_segment_ptr());
+        asm volatile("" : "+s"(ka));
+        return ka;
+    };
+    // Rotate the 8 pairs (a[v], b[v]) of columns i0 .. i0+7 of row t; returns
+    // the pairs' sum of squares.  ya, yb: the rotated (bf16-exact) values.
+    // Rows past T hold zeros (any table row gives zeros); pairs past nfreq
+    // rotate by angle 0.
+    auto rope8 = [&](const u32x4& a, const u32x4& b, int t, int i0, u32x4& ya, u32x4& yb)
+        __attribute__((always_inline)) -> float {
+#pragma clang fp contract(off)
+        float ss = 0.f;
+        if constexpr (PRO) {
+            KargPtr ka = pro_args();
+            float cs[8], sn[8];
+            const bool rot = ka->cos != nullptr;
+            if (rot) {
+                const int nf = ka->nfreq, ld = ka->ld;
+                const int tt = min(t, T - 1);
+                const float* cr = ka->cos + (size_t)tt * ld;
+                const float* sr = ka->sin + (size_t)tt * ld;
+                const bool vec = ((reinterpret_cast<uintptr_t>(ka->cos) | reinterpret_cast<uintptr_t>(ka->sin)) & 15) == 0 &&
+                                 (ld & 3) == 0 && i0 + 8 <= nf;
+                if (vec) {
+#pragma unroll
+                    for (int v = 0; v < 8; v += 4) {
+                        const f32x4 x = *reinterpret_cast<const f32x4*>(cr + i0 + v);
+                        const f32x4 y = *reinterpret_cast<const f32x4*>(sr + i0 + v);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            cs[v + e] = x[e];
+                            sn[v + e] = y[e];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        const int idx = min(i0 + v, nf - 1);
+                        const float x = cr[idx], y = sr[idx];
+                        cs[v] = (i0 + v < nf) ? x : 1.f;
+                        sn[v] = (i0 + v < nf) ? y : 0.f;
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 8; v += 2) {
+                    const uint32_t uc = BF16::pack(cs[v], cs[v + 1]), us = BF16::pack(sn[v], sn[v + 1]);
+                    cs[v] = BF16::lo(uc);
+                    cs[v + 1] = BF16::hi(uc);
+                    sn[v] = BF16::lo(us);
+                    sn[v + 1] = BF16::hi(us);
+                }
+            }
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                float y1[2], y2[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float x1 = e ? BF16::hi(a[w]) : BF16::lo(a[w]);
+                    const float x2 = e ? BF16::hi(b[w]) : BF16::lo(b[w]);
+                    if (rot) {
+                        const int v = 2 * w + e;
+                        const float r0 = BF16::lo(BF16::pack(x1 * cs[v], 0.f));
+                        const float r1 = BF16::lo(BF16::pack(x2 * sn[v], 0.f));
+                        const float r2 = BF16::lo(BF16::pack(x1 * sn[v], 0.f));
+                        const float r3 = BF16::lo(BF16::pack(x2 * cs[v], 0.f));
+                        y1[e] = BF16::lo(BF16::pack(r0 - r1, 0.f));
+                        y2[e] = BF16::lo(BF16::pack(r2 + r3, 0.f));
+                    } else {
+                        y1[e] = x1;
+                        y2[e] = x2;
+                    }
+                    ss = fmaf(y1[e], y1[e], fmaf(y2[e], y2[e], ss));
+                }
+                ya[w] = BF16::pack(y1[0], y1[1]);
+                yb[w] = BF16::pack(y2[0], y2[1]);
+            }
+        }
+        return ss;
+    };
+    auto rinv_of = [&](float ss) __attribute__((always_inline)) -> float {
+        float ne = 0.f;
+        if constexpr (PRO) ne = pro_args()->norm_eps;
+        const float se = ss + ne;
+        return (float)(1.0 / sqrt((double)se));
+    };
+    auto scale_row = [&](u32x4& y, float rinv) __attribute__((always_inline)) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) y[w] = BF16::pack(BF16::lo(y[w]) * rinv, BF16::hi(y[w]) * rinv);
+    };
+    // Normalise K tile uu (landed and visible) in place in its LDS stage: four
+    // threads per key row, thread j holding chunks j and j + 4.  The
+    // workgroup whose first item spans every key writes the rows and their
+    // 1/norm out for the backward.
+    auto norm_k = [&](int uu) __attribute__((always_inline)) {
+        if constexpr (PRO) {
+            int soff = (uu % NST) * TB;
+            asm volatile("" : "+s"(soff));
+            uint8_t* kb = k_lds + soff;
+            const int key0 = (uu < nt_a ? uu : uu - nt_a) * BN;
+            // Per-lane values formed here, not hoisted out of the tile loop
+            // (the loop has no registers to spare for them).
+            int tl = tid;
+            asm volatile("" : "+v"(tl));
+            const int r = tl >> 2, j = tl & 3;
+            const int sw = lds_swz(r);
+            u32x4* pa = reinterpret_cast<u32x4*>(kb + r * RB + ((j ^ sw) << 4));
+            u32x4* pb = reinterpret_cast<u32x4*>(kb + r * RB + (((j + 4) ^ sw) << 4));
+            const u32x4 a = *pa, b = *pb;
+            u32x4 ya, yb;
+            const int t = key0 + r;
+            float ss = rope8(a, b, t, 8 * j, ya, yb);
+            ss += __shfl_xor(ss, 1);
+            ss += __shfl_xor(ss, 2);
+            const float rinv = rinv_of(ss);
+            scale_row(ya, rinv);
+            scale_row(yb, rinv);
+            *pa = ya;
+            *pb = yb;
+            if (mb_a == nmb - 1 && uu < nt_a && t < T) {
+                KargPtr ka = pro_args();
+                uint16_t* ko = reinterpret_cast<uint16_t*>(ka->k_out) + ((size_t)bh * T + t) * DP;
+                *reinterpret_cast<u32x4*>(ko + 8 * j) = ya;
+                *reinterpret_cast<u32x4*>(ko + 32 + 8 * j) = yb;
+                if (j == 0) ka->k_rinv[(size_t)bh * T + t] = rinv;
+            }
+        }
+    };
+
+    auto load_q = [&](int mb) __attribute__((always_inline)) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb)
+        for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const int row = 128 * qb + lr;
                 const int pc = (2 * ks + (ln >> 5)) ^ (row & 7);
-                qr[qb][ks] = *reinterpret_cast<const u32x4*>(q_lds + row * RB + pc * 16) ^ flip;
+                qr[qb][ks] = *reinterpret_cast<const u32x4*>(q_lds + row * RB + pc * 16);
+            }
+            if constexpr (PRO) {
+                // The lane holds chunks g, 2 + g (ks 0, 1) and their partners
+                // 4 + g, 6 + g (ks 2, 3); the other half-wave the rest of the row.
+                const int gg = ln >> 5;
+                const int t = mb * BM + 128 * qb + lr;
+                u32x4 y0, y1, y2, y3;
+                const float pa = rope8(qr[qb][0], qr[qb][2], t, 8 * gg, y0, y2);
+                const float pb = rope8(qr[qb][1], qr[qb][3], t, 8 * (2 + gg), y1, y3);
+                const float s01 = pa + __shfl_xor(pa, 32);
+                const float s23 = pb + __shfl_xor(pb, 32);
+                const float rinv = rinv_of(s01 + s23);
+                scale_row(y0, rinv);
+                scale_row(y1, rinv);
+                scale_row(y2, rinv);
+                scale_row(y3, rinv);
+                qr[qb][0] = y0;
+                qr[qb][1] = y1;
+                qr[qb][2] = y2;
+                qr[qb][3] = y3;
+                if (t < T) {
+                    KargPtr ka = pro_args();
+                    uint16_t* qo = reinterpret_cast<uint16_t*>(ka->q_out) + ((size_t)bh * T + t) * DP;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) *reinterpret_cast<u32x4*>(qo + 8 * (2 * ks + gg)) = qr[qb][ks];
+                    if (gg == 0) ka->q_rinv[(size_t)bh * T + t] = rinv;
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                qr[qb][ks] ^= flip;
                 asm volatile("" : "+v"(qr[qb][ks]));
             }
+        }
     };
 
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
@@ -564,7 +751,29 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     constexpr int kTileLoads = 2 * LPW, kQLoads = LQW;
     const bool early_q = (nitems == 2);
     const int uq = max(1, nt_a - 4);
+    // Fused prologue: K tile u + 1 is normalised in place during step u, so
+    // at the top of step u everything issued so far (tiles u and u + 1) has
+    // to have landed; tile u + 2 then has one step to land.  Tile 0 is
+    // normalised at the top of step 0, behind one more barrier.
+    auto top_pro = [&](int u) __attribute__((always_inline)) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (u == uq && early_q) issue_q(mb_b);
+        if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
+        if (u == 0) {
+            norm_k(0);
+            if (ntot > 1) norm_k(1);
+            __syncthreads();
+        } else if (u + 1 < ntot) {
+            norm_k(u + 1);
+        }
+        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
+    };
     auto top = [&](int u) __attribute__((always_inline)) {
+        if constexpr (PRO) {
+            top_pro(u);
+            return;
+        }
         // The first item's rows are stored at step nt_a + 1 (Born, from LDS)
         // or nt_a (purified, from registers); the next step drains them.
         const bool stores_out = (nitems == 2) && (u == nt_a + (PUR ? 1 : 2));
@@ -597,13 +806,13 @@ void born_fwd16_fast_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         top(u);
         if constexpr (PUR) {
             if (it > 0) store_pur(mb_a);
-            load_q();
+            load_q(mb);
         } else if (it > 0) {
             pack();
-            load_q();  // before the previous item's rows overwrite this wave's Q rows
+            load_q(mb);  // before the previous item's rows overwrite this wave's Q rows
             put_lds();
         } else {
-            load_q();
+            load_q(mb);
         }
         start_item(mb);
         bool at_top = true;  // top(u) already done for the current step
@@ -670,6 +879,19 @@ hipError_t launch_fwd16_fast(const FwdArgs& a, hipStream_t st) {
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     const dim3 grid(npair < 512u ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<E, DP, MODE>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+// Born forward with the Q/K prologue fused into the loads (bf16, D == 64,
+// dense or causal, no window / documents); same grid as launch_fwd16_fast.
+template <int MODE>
+hipError_t launch_fwd16_fast_prologue(const FwdProArgs& a, hipStream_t st) {
+    using C = FastFwdCfg<64>;
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
+    const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
+    const dim3 grid(npair < 512u ? nsingle : npair);
+    hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, false, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -19,6 +19,9 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s);
 hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s);
 hipError_t fwd_launch_f32(const FwdArgs& a, hipStream_t s);
 hipError_t bwd_launch_bf16(const BwdArgs& a, hipStream_t s);
+// The forward with the Q/K prologue fused into its loads (bf16, D == 64, dense
+// or causal); hipErrorInvalidValue for anything else.
+hipError_t fwd_prologue_launch_bf16(const FwdProArgs& a, hipStream_t s);
 hipError_t bwd_launch_f16(const BwdArgs& a, hipStream_t s);
 hipError_t bwd_launch_f32(const BwdArgs& a, hipStream_t s);
 

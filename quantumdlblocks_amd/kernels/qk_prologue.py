@@ -34,6 +34,7 @@ from .flash_born import _DTYPE_CODE, _stream_ptr
 
 __all__ = [
     "apply_unitary_rope",
+    "flash_born_attention_qk_prologue",
     "fused_qk_rope_l2_normalize",
     "qk_prologue_backward",
     "qk_prologue_forward",
@@ -280,3 +281,140 @@ def fused_qk_rope_l2_normalize(
         if t.dtype not in _DTYPE_CODE:
             raise TypeError(f"fused_qk_rope_l2_normalize: unsupported dtype {t.dtype}")
     return _QKPrologueFn.apply(q, k, cos, sin, float(eps))
+
+
+# ---------------------------------------------------------------------------
+# Prologue folded into the attention kernel's loads
+# ---------------------------------------------------------------------------
+
+class _BornQKPrologueFn(torch.autograd.Function):
+    """Forward: Born attention of (q', k', v) with q' = l2_normalize(rope(q)),
+    k' likewise, in one call of ``qdl_flash_born_fwd_qk_prologue`` (one
+    kernel for bf16, D = 64, no documents or window: Q normalised as each
+    query block is loaded, K as each key tile lands in LDS).  Saves q', k' and
+    1/norm.  Backward: the attention backward on (q', k', v), then the
+    prologue backward into q and k (their dtypes and strides)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, cos, sin, is_causal, eps, window_size, doc_ids, norm_eps):
+        from .flash_born import _aligned, _autocast_dtype, _check_inputs
+
+        lib = _native.load()
+        target = _autocast_dtype(q) or v.dtype
+        if target not in _DTYPE_CODE:
+            raise TypeError(f"flash_born_attention_qk_prologue: unsupported dtype {target}")
+        scale_flat = scale.detach().contiguous().view(-1).to(dtype=torch.float32, device=q.device)
+        _check_inputs(q, k, v, scale_flat, doc_ids)
+        B, H, T, D = q.shape
+        q_in = _rows_ok(q.detach().to(target))
+        k_in = _rows_ok(k.detach().to(target))
+        v_c = _aligned(v.detach().to(target))
+        cos2, sin2 = _prep_tables(cos, sin, D // 2, T, q.device)
+        doc_c = None if doc_ids is None else _aligned(doc_ids.to(device=q.device, dtype=torch.int32))
+        out = torch.empty((B, H, T, D), dtype=target, device=q.device)
+        z = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+        q_out = torch.empty_like(out)
+        k_out = torch.empty_like(out)
+        q_r = torch.empty_like(z)
+        k_r = torch.empty_like(z)
+        qs, ks = _strides(q_in), _strides(k_in)
+        window = max(int(window_size), 0)
+        with torch.cuda.device(q.device):
+            rc = lib.qdl_flash_born_fwd_qk_prologue(
+                _DTYPE_CODE[target], B, H, T, D,
+                q_in.data_ptr(), qs.data_ptr(), k_in.data_ptr(), ks.data_ptr(), v_c.data_ptr(),
+                cos2.data_ptr() if cos2 is not None else None,
+                sin2.data_ptr() if sin2 is not None else None,
+                cos2.shape[1] if cos2 is not None else 0,
+                cos2.stride(0) if cos2 is not None else 0,
+                float(norm_eps), scale_flat.data_ptr(), scale_flat.numel(),
+                doc_c.data_ptr() if doc_c is not None else None,
+                1 if is_causal else 0, window, float(eps),
+                out.data_ptr(), z.data_ptr(), q_out.data_ptr(), k_out.data_ptr(),
+                q_r.data_ptr(), k_r.data_ptr(), _stream_ptr(q.device),
+            )
+        _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
+        ctx.save_for_backward(q_out, k_out, v_c, out, z, scale_flat, q_r, k_r,
+                              doc_c if doc_c is not None else torch.empty(0, dtype=torch.int32, device=q.device))
+        ctx.tables = (cos.detach(), sin.detach()) if cos is not None else (None, None)
+        ctx.q_layout = (tuple(q.shape), tuple(q.stride()))
+        ctx.k_layout = (tuple(k.shape), tuple(k.stride()))
+        ctx.is_causal, ctx.eps, ctx.window_size = bool(is_causal), float(eps), window
+        ctx.has_doc_ids = doc_ids is not None
+        ctx.scale_shape, ctx.scale_dtype = scale.shape, scale.dtype
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        lib = _native.load()
+        q_out, k_out, v_c, out, z, scale_flat, q_r, k_r, doc_c = ctx.saved_tensors
+        B, H, T, D = q_out.shape
+        from .flash_born import _aligned
+
+        do_c = _aligned(do.to(v_c.dtype))
+        dqn = torch.empty_like(q_out)
+        dkn = torch.empty_like(k_out)
+        dv = torch.empty_like(v_c)
+        dscale = torch.empty(scale_flat.numel(), dtype=torch.float32, device=q_out.device)
+        code = _DTYPE_CODE[v_c.dtype]
+        ws_bytes = int(lib.qdl_flash_born_bwd_workspace_size(code, B, H, T, D, scale_flat.numel()))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q_out.device)
+        with torch.cuda.device(q_out.device):
+            rc = lib.qdl_flash_born_bwd(
+                code, B, H, T, D,
+                q_out.data_ptr(), k_out.data_ptr(), v_c.data_ptr(), out.data_ptr(), do_c.data_ptr(),
+                z.data_ptr(), scale_flat.data_ptr(), scale_flat.numel(),
+                doc_c.data_ptr() if ctx.has_doc_ids else None,
+                1 if ctx.is_causal else 0, ctx.window_size, ctx.eps,
+                dqn.data_ptr(), dkn.data_ptr(), dv.data_ptr(), dscale.data_ptr(),
+                ws.data_ptr(), ws.numel(), _stream_ptr(q_out.device),
+            )
+        _native.check(rc, "qdl_flash_born_bwd")
+        cos, sin = ctx.tables
+        dq, dk = qk_prologue_backward(dqn, dkn, q_out, k_out, q_r, k_r, cos, sin, ctx.q_layout, ctx.k_layout)
+        qd, kd, vd = ctx.dtypes
+        return (dq.to(qd), dk.to(kd), dv.to(vd), dscale.view(ctx.scale_shape).to(ctx.scale_dtype),
+                None, None, None, None, None, None, None)
+
+
+def flash_born_attention_qk_prologue(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float | torch.Tensor,
+    cos: torch.Tensor | None = None,
+    sin: torch.Tensor | None = None,
+    is_causal: bool = True,
+    eps: float = 1e-12,
+    window_size: int = 0,
+    doc_ids: torch.Tensor | None = None,
+    norm_eps: float = 1e-12,
+) -> torch.Tensor:
+    """The Born layer's attention data flow with the Q/K prologue folded into
+    the attention kernel (attention.py:573-589 then 704-713):
+
+        flash_born_attention(l2_normalize(rope(q)), l2_normalize(rope(k)), v, scale, ...)
+
+    q, k: ``(B, H, T, D)`` raw projections with unit stride along D (e.g. the
+    ``(B, T, H, D)`` projection output viewed as ``(B, H, T, D)``); v: any
+    ``(B, H, T, D)``; cos, sin as for ``fused_qk_rope_l2_normalize`` (or None:
+    normalisation only); the other arguments as for ``flash_born_attention``.
+    On the GPU, bf16 with D = 64 and no documents or window runs as one
+    kernel; other cases run the prologue kernel and then the attention
+    kernels.  CPU tensors take the reference's eager formulation of both.
+    """
+    from .flash_born import MAX_HEAD_DIM, flash_born_attention
+
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, v must share one (B, H, T, D) shape")
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin must be given together")
+    if not isinstance(scale, torch.Tensor):
+        scale = torch.tensor(float(scale), dtype=torch.float32, device=q.device)
+    D = q.shape[-1]
+    if not q.is_cuda or D % 8 or D > MAX_HEAD_DIM:
+        qn, kn = fused_qk_rope_l2_normalize(q, k, cos, sin, norm_eps)
+        return flash_born_attention(qn, kn, v, scale, is_causal, eps, window_size, doc_ids)
+    return _BornQKPrologueFn.apply(q, k, v, scale, cos, sin, bool(is_causal), float(eps), int(window_size),
+                                   doc_ids, float(norm_eps))

@@ -1,0 +1,204 @@
+"""The Q/K prologue folded into the attention kernel
+(``qdl_flash_born_fwd_qk_prologue`` / ``flash_born_attention_qk_prologue``).
+
+Bars:
+  * bit for bit: the fused kernel (bf16, D = 64, dense or causal) gives the
+    same O, Z, normalised Q and K and 1/norm as the standalone prologue kernel
+    followed by the attention kernel (the same arithmetic, in one pass), on
+    contiguous and projection-layout inputs, full, partial and no rotary
+    tables, both scale signs, per-head scales, ragged T and the C3 shape;
+  * against the oracles: the normalised rows equal the prologue oracle's
+    rounding model given the kernel's 1/norm, 1/norm within 4 ulps, and O
+    within 2e-2 (normwise) of ``born_oracle.forward`` applied to the
+    oracle's normalised rows, Z within its rounding bound;
+  * gradients: the autograd entry gives bit-identical gradients to the
+    composition ``flash_born_attention(fused_qk_rope_l2_normalize(...))``
+    (the backward is the attention backward then the prologue backward);
+  * other shapes (fp16, D = 32, documents, window) take the two-launch path
+    through the same entry and equal the composition.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import born_oracle as orc
+from oracle import qk_prologue_oracle as po
+from util import f64, rel_err, z_row_bound
+
+pytestmark = pytest.mark.gpu
+
+
+def _tables(T, n, base=1024.0):
+    freqs = 1.0 / base ** (torch.arange(n, dtype=torch.float32) / max(n, 1))
+    ang = torch.outer(torch.arange(T, dtype=torch.float32), freqs)
+    return torch.cos(ang).view(1, 1, T, n), torch.sin(ang).view(1, 1, T, n)
+
+
+def _inputs(B, H, T, D, dtype, strided, seed, dev, std=1.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    if strided:  # (B, T, H, D) projection output viewed as (B, H, T, D)
+        q = (torch.randn(B, T, H, D, generator=g) * std).to(dtype).to(dev).transpose(1, 2)
+        k = (torch.randn(B, T, H, D, generator=g) * std).to(dtype).to(dev).transpose(1, 2)
+    else:
+        q = (torch.randn(B, H, T, D, generator=g) * std).to(dtype).to(dev)
+        k = (torch.randn(B, H, T, D, generator=g) * std).to(dtype).to(dev)
+    v = torch.randn(B, H, T, D, generator=g).to(dtype).to(dev)
+    do = torch.randn(B, H, T, D, generator=g).to(dtype).to(dev)
+    return q, k, v, do
+
+
+def _abi(fused, q, k, v, scale, cos, sin, causal=True, eps=1e-12, doc=None, window=0):
+    """Through the C ABI: the fused entry (fused=True) or the prologue entry
+    followed by the forward entry.  Returns out, z, q', k', q_rinv, k_rinv."""
+    from quantumdlblocks_amd import _native
+    from quantumdlblocks_amd.kernels.flash_born import _DTYPE_CODE
+    from quantumdlblocks_amd.kernels.qk_prologue import _prep_tables, _strides
+
+    lib = _native.load()
+    B, H, T, D = q.shape
+    dev = q.device
+    code = _DTYPE_CODE[q.dtype]
+    cos2, sin2 = _prep_tables(cos, sin, D // 2, T, dev)
+    tabs = (cos2.data_ptr() if cos2 is not None else None, sin2.data_ptr() if sin2 is not None else None,
+            cos2.shape[1] if cos2 is not None else 0, cos2.stride(0) if cos2 is not None else 0)
+    sc = torch.as_tensor(np.asarray(scale, np.float32).reshape(-1), device=dev)
+    doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
+    out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+    z = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    qo, ko = torch.empty_like(out), torch.empty_like(out)
+    qr, kr = torch.empty_like(z), torch.empty_like(z)
+    qs, ks = _strides(q), _strides(k)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    docp = None if doc_t is None else doc_t.data_ptr()
+    if fused:
+        rc = lib.qdl_flash_born_fwd_qk_prologue(code, B, H, T, D, q.data_ptr(), qs.data_ptr(), k.data_ptr(),
+                                                ks.data_ptr(), v.data_ptr(), *tabs, 1e-12, sc.data_ptr(),
+                                                sc.numel(), docp, int(causal), window, eps, out.data_ptr(),
+                                                z.data_ptr(), qo.data_ptr(), ko.data_ptr(), qr.data_ptr(),
+                                                kr.data_ptr(), stream)
+        _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
+    else:
+        rc = lib.qdl_flash_born_qk_prologue_fwd(code, B, H, T, D, q.data_ptr(), qs.data_ptr(), k.data_ptr(),
+                                                ks.data_ptr(), *tabs, 1e-12, qo.data_ptr(), ko.data_ptr(),
+                                                qr.data_ptr(), kr.data_ptr(), stream)
+        _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
+        rc = lib.qdl_flash_born_fwd(code, B, H, T, D, qo.data_ptr(), ko.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                    z.data_ptr(), sc.data_ptr(), sc.numel(), docp, int(causal), window, eps, stream)
+        _native.check(rc, "qdl_flash_born_fwd")
+    torch.cuda.synchronize(dev)
+    return out, z, qo, ko, qr, kr
+
+
+def _same(a, b):
+    iv = torch.int32 if a.dtype == torch.float32 else torch.int16
+    return torch.equal(a.view(iv), b.view(iv))
+
+
+CASES = [
+    # (B, H, T, nfreq or None, strided, causal, scale)
+    (2, 3, 300, 32, True, True, 8.0),
+    (2, 3, 300, 32, False, True, 8.0),
+    (1, 2, 1024, 20, True, True, -3.0),
+    (1, 4, 777, None, True, False, 8.0),
+    (2, 2, 65, 32, True, True, np.array([1.5, 9.0])),
+    (1, 1, 1, 32, False, True, 8.0),
+    (1, 2, 2500, 32, True, True, 8.0),
+    (3, 2, 513, 7, False, False, 2.0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-n{c[3]}-{'strided' if c[4] else 'dense'}-{'causal' if c[5] else 'full'}")
+def test_fused_equals_prologue_then_attention_bitwise(cuda_device, case):
+    B, H, T, nf, strided, causal, scale = case
+    q, k, v, _ = _inputs(B, H, T, 64, torch.bfloat16, strided, seed=T + 3, dev=cuda_device, std=0.7)
+    cos = sin = None
+    if nf is not None:
+        cos, sin = (x.to(cuda_device) for x in _tables(T, nf))
+    print(f"fused case B{B} H{H} T{T} n={nf} strided={strided} causal={causal}", flush=True)
+    a = _abi(True, q, k, v, scale, cos, sin, causal)
+    b = _abi(False, q, k, v, scale, cos, sin, causal)
+    for name, x, y in zip(("out", "z", "q'", "k'", "q_rinv", "k_rinv"), a, b):
+        assert _same(x, y), name
+
+
+def test_fused_c3_shape_bitwise_and_oracle(cuda_device):
+    """C3's shape in the projection layout: bit for bit against the two
+    launches; sampled heads against the composition of the oracles."""
+    B, H, T, D = 16, 16, 1024, 64
+    q, k, v, _ = _inputs(B, H, T, D, torch.bfloat16, True, seed=11, dev=cuda_device)
+    cos, sin = _tables(T, D // 2, base=10000.0)
+    cos_np, sin_np = cos[0, 0].numpy(), sin[0, 0].numpy()
+    cos, sin = cos.to(cuda_device), sin.to(cuda_device)
+    a = _abi(True, q, k, v, 8.0, cos, sin)
+    b = _abi(False, q, k, v, 8.0, cos, sin)
+    for name, x, y in zip(("out", "z", "q'", "k'", "q_rinv", "k_rinv"), a, b):
+        assert _same(x, y), name
+    out, z, qo, ko, qr, kr = a
+    for bb, hh in ((0, 0), (15, 15), (7, 3), (9, 12)):
+        for x, xo, xr in ((q, qo, qr), (k, ko, kr)):
+            xn = x[bb, hh].float().cpu().numpy()
+            want, want_r = po.prologue_forward(xn, cos_np, sin_np, 1e-12, "bf16")
+            got_r = xr[bb, hh].cpu().numpy()
+            np.testing.assert_allclose(got_r, want_r, rtol=4 * 2.0 ** -23, atol=0)
+            y = po.rope(xn, cos_np, sin_np, "bf16")
+            np.testing.assert_array_equal(xo[bb, hh].float().cpu().numpy(),
+                                          po.round_to((y * got_r[:, None]).astype(np.float32), "bf16"))
+        # attention of the oracle's normalised rows
+        qn = po.prologue_forward(q[bb, hh].float().cpu().numpy(), cos_np, sin_np, 1e-12, "bf16")[0]
+        kn = po.prologue_forward(k[bb, hh].float().cpu().numpy(), cos_np, sin_np, 1e-12, "bf16")[0]
+        vn = v[bb, hh].float().cpu().numpy()
+        ref, zref = orc.forward(qn[None, None], kn[None, None], vn[None, None], 8.0)
+        err = rel_err(f64(out[bb, hh]), ref[0, 0])
+        print(f"C3 fused head ({bb},{hh}): O rel {err:.3e}", flush=True)
+        assert err <= 2e-2
+        bound = z_row_bound(qn[None, None], kn[None, None], 8.0, zref, 1e-12, torch.bfloat16,
+                            orc.visible_mask(T, True, 0))
+        assert np.all(np.abs(f64(z[bb, hh]) - zref[0, 0]) <= bound[0, 0])
+
+
+@pytest.mark.parametrize("strided", [True, False])
+def test_fused_autograd_equals_composition(cuda_device, strided):
+    from quantumdlblocks_amd import flash_born_attention, flash_born_attention_qk_prologue, fused_qk_rope_l2_normalize
+
+    B, H, T, D = 2, 4, 333, 64
+    q, k, v, do = _inputs(B, H, T, D, torch.bfloat16, strided, seed=5, dev=cuda_device)
+    cos, sin = (x.to(cuda_device) for x in _tables(T, 32))
+    sc = torch.tensor([2.0, -3.0, 8.0, 0.5], device=cuda_device)
+
+    def run(fused):
+        qa, ka, va = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+        s = sc.detach().clone().requires_grad_(True)
+        if fused:
+            out = flash_born_attention_qk_prologue(qa, ka, va, s, cos, sin)
+        else:
+            qn, kn = fused_qk_rope_l2_normalize(qa, ka, cos, sin)
+            out = flash_born_attention(qn, kn, va, s)
+        out.backward(do)
+        torch.cuda.synchronize()
+        return out, qa.grad, ka.grad, va.grad, s.grad
+
+    a, b = run(True), run(False)
+    for name, x, y in zip(("out", "dq", "dk", "dv", "dscale"), a, b):
+        assert x.shape == y.shape and x.dtype == y.dtype, name
+        assert _same(x, y), name
+    assert a[1].stride() == q.stride()
+
+
+@pytest.mark.parametrize("dtype, D, doc, window", [
+    (torch.float16, 64, False, 0), (torch.bfloat16, 32, False, 0), (torch.bfloat16, 64, True, 0),
+    (torch.bfloat16, 64, False, 50), (torch.float32, 128, False, 0)])
+def test_other_shapes_take_the_two_launch_path(cuda_device, dtype, D, doc, window):
+    from quantumdlblocks_amd import flash_born_attention, flash_born_attention_qk_prologue, fused_qk_rope_l2_normalize
+
+    B, H, T = 2, 2, 200
+    q, k, v, do = _inputs(B, H, T, D, dtype, True, seed=D, dev=cuda_device)
+    cos, sin = (x.to(cuda_device) for x in _tables(T, D // 2))
+    doc_t = torch.as_tensor(orc.geometric_doc_ids(B, T, 40.0, seed=1), device=cuda_device) if doc else None
+    a = flash_born_attention_qk_prologue(q, k, v, 4.0, cos, sin, window_size=window, doc_ids=doc_t)
+    qn, kn = fused_qk_rope_l2_normalize(q, k, cos, sin)
+    b = flash_born_attention(qn, kn, v, 4.0, window_size=window, doc_ids=doc_t)
+    torch.cuda.synchronize()
+    assert _same(a, b)
