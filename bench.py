@@ -64,6 +64,9 @@ PURIFIED = {"p3", "p5", "p4b"}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
+# The prologue folded into the attention forward (one kernel), C3 / C5 shapes,
+# Q and K read raw from the (B, T, H, D) projection layout.
+FUSED = {"qkc3": (16, 16, 1024, 64), "qkc5": (16, 16, 2048, 64)}
 
 
 def parse_args():
@@ -73,7 +76,7 @@ def parse_args():
     # ~15% slower over the first ~20 steps than after ~2000 (~0.1 s of load).
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=2000)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(PROLOGUE))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + sorted(PROLOGUE) + sorted(FUSED))
     ap.add_argument("--sets", type=int, default=4, help="input sets rotated over the timed steps")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg")
@@ -300,6 +303,9 @@ def main():
 
     if args.config in PROLOGUE:
         prologue_main(args)
+        return
+    if args.config in FUSED:
+        fused_main(args)
         return
 
     import torch
@@ -644,6 +650,120 @@ def prologue_main(args):
             "hot_gbs": round(nbytes / hot_wall / 1e9, 1),
             "untimed_clock_ramp_steps": ramp,
             "algorithmic_bytes": nbytes,
+            "device": torch.cuda.get_device_name(dev),
+            "torch": torch.__version__,
+            "host": platform.node(),
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
+def fused_main(args):
+    """qkc3 / qkc5: qdl_flash_born_fwd_qk_prologue, RoPE + L2 normalisation of
+    Q and K folded into the Born attention forward (C3 / C5 shapes, bf16,
+    causal, scale 8; Q, K the (B, T, H, D) projection output, rotary tables of
+    the reference's UnitaryRoPE defaults).  value: the attention's
+    algorithmic TFLOP/s of the whole fused step; detail also times the same
+    work as two launches (prologue kernel, then attention kernel)."""
+    import torch
+
+    from quantumdlblocks_amd import _native
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    B, H, T, D = FUSED[args.config]
+    steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
+    code = _native.DTYPE_BF16
+    cos, sin = prologue_tables(T, D // 2, dev)
+    nf, ld = cos.shape[1], cos.stride(0)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    st = (ctypes.c_int64 * 3)(T * H * D, D, H * D)
+    scale = torch.tensor(8.0, dtype=torch.float32, device=dev)
+    g = torch.Generator("cpu").manual_seed(args.seed)
+    sets = []
+    for _ in range(max(1, args.sets)):
+        q = (torch.randn(B, T, H, D, generator=g) * 0.125).to(torch.bfloat16).to(dev)
+        k = (torch.randn(B, T, H, D, generator=g) * 0.125).to(torch.bfloat16).to(dev)
+        v = (torch.randn(B, H, T, D, generator=g) * 0.125).to(torch.bfloat16).to(dev)
+        out = torch.empty(B, H, T, D, dtype=torch.bfloat16, device=dev)
+        z = torch.empty(B, H, T, device=dev)
+        qo, ko = torch.empty_like(out), torch.empty_like(out)
+        qr, kr = torch.empty_like(z), torch.empty_like(z)
+        sets.append((q, k, v, out, z, qo, ko, qr, kr))
+
+    def fused(i, rotate=True):
+        q, k, v, out, z, qo, ko, qr, kr = sets[i % len(sets)] if rotate else sets[0]
+        rc = lib.qdl_flash_born_fwd_qk_prologue(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st, v.data_ptr(),
+                                                cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12, scale.data_ptr(), 1,
+                                                None, 1, 0, 1e-12, out.data_ptr(), z.data_ptr(), qo.data_ptr(),
+                                                ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), stream)
+        _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
+
+    def separate(i):
+        q, k, v, out, z, qo, ko, qr, kr = sets[i % len(sets)]
+        rc = lib.qdl_flash_born_qk_prologue_fwd(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st,
+                                                cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12,
+                                                qo.data_ptr(), ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), stream)
+        _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
+        rc = lib.qdl_flash_born_fwd(code, B, H, T, D, qo.data_ptr(), ko.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                    z.data_ptr(), scale.data_ptr(), 1, None, 1, 0, 1e-12, stream)
+        _native.check(rc, "qdl_flash_born_fwd")
+
+    for i in range(warmup):
+        fused(i)
+    torch.cuda.synchronize()
+    ramp = clock_ramp(fused, warmup)
+
+    def timed(fn, n_steps):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for i in range(n_steps):
+            fn(i)
+        ev1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_steps, ev0.elapsed_time(ev1) / 1e3 / n_steps
+
+    wall_step, ev_step = timed(fused, steps)
+    for i in range(max(steps, 50)):
+        separate(i)
+    sep_wall, sep_ev = timed(separate, steps)
+    for s_ in sets:
+        assert torch.isfinite(s_[3].float()).all(), "non-finite output"
+
+    flops = 4.0 * D * (T * (T + 1) // 2) * B * H
+    rows = B * H * T
+    nbytes = rows * D * 2 * 3 + rows * D * 2 + rows * 4 + 2 * (rows * D * 2 + rows * 4) + 2 * T * nf * 4
+    value = flops / wall_step / 1e12
+    roof = {"bound": "hbm", "achieved": round(nbytes / ev_step / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(nbytes / ev_step / 1e9 / PEAK_HBM_GBS, 4), "traffic": None}
+    line = {
+        "metric": f"Born-attn fwd with fused Q/K prologue TFLOP/s, B{B} H{H} T{T} hd{D}",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.015625) Q, K, V; %d rotated input sets)" % len(sets),
+        "config": {"workload": args.config, "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
+                   "rope_pairs": nf, "qk_layout": "(B, T, H, D) viewed as (B, H, T, D)", "scale": 8.0},
+        "pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": roof,
+        "cpu_baseline": None,
+        "detail": {
+            "fused_kernel_us_per_step_events": round(ev_step * 1e6, 3),
+            "separate_two_launches_us_per_step_events": round(sep_ev * 1e6, 3),
+            "separate_two_launches_us_per_step_wall": round(sep_wall * 1e6, 3),
+            "algorithmic_flops": flops,
+            "algorithmic_bytes": nbytes,
+            "untimed_clock_ramp_steps": ramp,
             "device": torch.cuda.get_device_name(dev),
             "torch": torch.__version__,
             "host": platform.node(),

@@ -249,10 +249,12 @@ int qdl_flash_born_qk_prologue_bwd(int dtype, int64_t B, int64_t H, int64_t T,
  * prologue; scale, doc_ids, is_causal, window_size, eps as for the forward.
  * Also writes q_out, k_out (contiguous (B, H, T, D), the normalised rows) and
  * q_rinv, k_rinv (1/norm per row), which the backward needs.  For bf16 with
- * D == 64, no documents and no window, one kernel normalises each query
- * block as it is loaded and each key tile in LDS before its use, so the
- * normalised Q and K are never read back from memory; other cases run the
- * prologue kernel and then the attention kernels (same results).
+ * D == 64, no documents and no window, the keys are normalised by the
+ * prologue kernel (keys only) and the attention kernel normalises each query
+ * block in registers as it loads it, so the normalised queries are never read
+ * back from memory; other cases run the prologue kernel on both and then the
+ * attention kernels.  The results are those of the two separate calls, bit
+ * for bit.
  * Replaces the apply_unitary_rope + l2_normalize calls on Q and K
  * (attention.py:583-589) together with the flash_born_attention call that
  * consumes them (attention.py:704-713, flash_born.py:475-513).

@@ -171,17 +171,21 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
         return QDL_BORN_E_NULL;
     if (!aligned16(v) || !aligned16(out) || !aligned16(q_out) || !aligned16(k_out)) return QDL_BORN_E_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // The fused kernel: bf16, D = 64, dense or causal, raw rows 16-byte
-    // aligned with (T + 256) rows of their time stride within 32-bit offsets.
-    auto rows_ok = [&](const void* p, const int64_t* st) {
-        return aligned16(p) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[2] >= D &&
-               (T + 256) * st[2] * 2 < ((int64_t)1 << 31);
-    };
-    if (dtype == QDL_BORN_DTYPE_BF16 && D == 64 && !doc_ids && window_size == 0 && rows_ok(q, q_strides) &&
-        rows_ok(k, k_strides) && (!cos_table || n_freq >= 1) && (T + 256) * D * 2 < ((int64_t)1 << 31)) {
+    // bf16, D = 64, dense or causal: K is normalised by the prologue kernel
+    // (K alone), then one attention kernel normalises each query block as it
+    // loads it (raw rows 16-byte aligned, (T + 256) rows of their time stride
+    // within 32-bit offsets) and writes the normalised rows for the backward.
+    const bool q_rows_ok = aligned16(q) && q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 &&
+                           q_strides[2] % 8 == 0 && q_strides[2] >= D &&
+                           (T + 256) * q_strides[2] * 2 < ((int64_t)1 << 31);
+    if (dtype == QDL_BORN_DTYPE_BF16 && D == 64 && !doc_ids && window_size == 0 && q_rows_ok &&
+        (!cos_table || n_freq >= 1) && (T + 256) * D * 2 < ((int64_t)1 << 31)) {
+        rc = qdl_flash_born_qk_prologue_fwd(dtype, B, H, T, D, nullptr, nullptr, k, k_strides, cos_table, sin_table,
+                                            n_freq, table_ld, norm_eps, nullptr, k_out, nullptr, k_rinv, stream);
+        if (rc != QDL_BORN_OK) return rc;
         qdl::FwdProArgs a;
         a.q = q;
-        a.k = k;
+        a.k = k_out;
         a.v = v;
         a.o = out;
         a.z = z;
@@ -198,18 +202,13 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
         a.q_sb = q_strides[0];
         a.q_sh = q_strides[1];
         a.q_st = q_strides[2];
-        a.k_sb = k_strides[0];
-        a.k_sh = k_strides[1];
-        a.k_st = k_strides[2];
         a.cos = cos_table;
         a.sin = cos_table ? sin_table : nullptr;
         a.ld = (int)table_ld;
         a.nfreq = (int)n_freq;
         a.norm_eps = (float)norm_eps;
         a.q_out = q_out;
-        a.k_out = k_out;
         a.q_rinv = q_rinv;
-        a.k_rinv = k_rinv;
         return hip_status(qdl::fwd_prologue_launch_bf16(a, s));
     }
     // Every other case: the prologue kernel, then the attention kernels on

@@ -155,21 +155,19 @@ struct FwdArgs {
     float eps;
 };
 
-// Forward with the Q/K prologue folded into the loads (bf16, D = 64): the
-// FwdArgs fields, with q and k holding the raw rows (unit stride along D,
-// element strides q_sb / q_sh / q_st for b, h, t), the rotary tables, and the
-// outputs the backward needs: the normalised rows and 1/norm per row.
+// Forward with the Q prologue folded into the query-block load (bf16,
+// D = 64): the FwdArgs fields, with q holding the raw query rows (unit stride
+// along D, element strides q_sb / q_sh / q_st for b, h, t) and k the keys
+// already normalised (contiguous), plus the rotary tables and the outputs
+// the backward needs: the normalised query rows and 1/norm per row.
 struct FwdProArgs : FwdArgs {
     int64_t q_sb, q_sh, q_st;
-    int64_t k_sb, k_sh, k_st;
     const float* cos;  // (T, ld) fp32, or nullptr: no rotation
     const float* sin;
     int ld, nfreq;
     float norm_eps;
     void* q_out;       // (B, H, T, D) contiguous
-    void* k_out;
     float* q_rinv;     // (B, H, T)
-    float* k_rinv;
 };
 
 // Kernel argument block shared by the backward kernels.

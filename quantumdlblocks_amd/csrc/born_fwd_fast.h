@@ -205,17 +205,14 @@ void born_fwd16_fast_kernel(
     // Bytes between consecutive Q / K rows: RB, or the raw rows' time stride
     // when the prologue is fused (the host keeps (T + 256) rows of it within
     // 32-bit offsets).
-    uint32_t qrow_b = RB, krow_b = RB;
-    size_t qbase = base, kbase_el = base;
+    uint32_t qrow_b = RB;
+    size_t qbase = base;
     if constexpr (PRO) {
-        const int b = bh / p.H;
         qrow_b = (uint32_t)p.q_st * 2u;
-        krow_b = (uint32_t)p.k_st * 2u;
-        qbase = (size_t)b * p.q_sb + (size_t)h * p.q_sh;
-        kbase_el = (size_t)b * p.k_sb + (size_t)h * p.k_sh;
+        qbase = (size_t)(bh / p.H) * p.q_sb + (size_t)h * p.q_sh;
     }
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + qbase, (uint32_t)T * qrow_b);
-    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + kbase_el, (uint32_t)T * krow_b);
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
 
     // Tile u of the block's sequence -> stage st: wave-instruction i writes
@@ -229,8 +226,7 @@ void born_fwd16_fast_kernel(
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
             const int off = (key0 + row) * RB;
-            const int koff = PRO ? (key0 + row) * (int)krow_b : off;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), koff + ((pc ^ lds_swz(row)) << 4));
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ lds_swz(row)) << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
         }
     };
@@ -443,13 +439,20 @@ void born_fwd16_fast_kernel(
     // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
     // of the scale is folded into Q; the asm pins the result in registers so
     // it is not recomputed inside the tile loop.
-    // Fused Q/K prologue (PRO): x' = l2_normalize(rope(x)) with the rounding
-    // of the standalone prologue kernel (qk_prologue.hip), so the rows are
-    // bit-identical to its output: each table entry, product, sum and
+    // Q prologue folded into the query-block load (PRO): the raw query rows
+    // come in through the Q block's LDS staging as usual, and each lane turns
+    // its rows' operands into q' = l2_normalize(rope(q)) in registers, with
+    // the rounding of the standalone prologue kernel (qk_prologue.hip), so the
+    // rows are bit-identical to its output: each table entry, product, sum and
     // difference rounded to bf16, the fp32 sum of squares accumulated pair by
     // pair and then across the row's four 8-pair chunks as ((c0 + c1) +
     // (c2 + c3)), 1/norm = 1/sqrt(sum + eps) correctly rounded from double.
-    // Chunk c of a row (columns 8c .. 8c+7) rotates against chunk c + 4.
+    // Chunk c of a row (columns 8c .. 8c+7) rotates against chunk c + 4; a
+    // lane's operands hold chunks g, 2 + g and their partners.  The keys
+    // arrive normalised (the prologue kernel runs on K alone first):
+    // normalising each K tile in LDS here measured slower than the two
+    // separate launches (every key tile is staged by ~2.5 workgroups, and the
+    // tile loop is bound by instruction issue).
     // The prologue's parameters are re-read from the kernel argument segment
     // where they are used (scalar loads), rather than held in registers
     // through the tile loop, whose scalar and vector registers are all taken.
@@ -544,45 +547,6 @@ void born_fwd16_fast_kernel(
 #pragma unroll
         for (int w = 0; w < 4; ++w) y[w] = BF16::pack(BF16::lo(y[w]) * rinv, BF16::hi(y[w]) * rinv);
     };
-    // Normalise K tile uu (landed and visible) in place in its LDS stage: four
-    // threads per key row, thread j holding chunks j and j + 4.  The
-    // workgroup whose first item spans every key writes the rows and their
-    // 1/norm out for the backward.
-    auto norm_k = [&](int uu) __attribute__((always_inline)) {
-        if constexpr (PRO) {
-            int soff = (uu % NST) * TB;
-            asm volatile("" : "+s"(soff));
-            uint8_t* kb = k_lds + soff;
-            const int key0 = (uu < nt_a ? uu : uu - nt_a) * BN;
-            // Per-lane values formed here, not hoisted out of the tile loop
-            // (the loop has no registers to spare for them).
-            int tl = tid;
-            asm volatile("" : "+v"(tl));
-            const int r = tl >> 2, j = tl & 3;
-            const int sw = lds_swz(r);
-            u32x4* pa = reinterpret_cast<u32x4*>(kb + r * RB + ((j ^ sw) << 4));
-            u32x4* pb = reinterpret_cast<u32x4*>(kb + r * RB + (((j + 4) ^ sw) << 4));
-            const u32x4 a = *pa, b = *pb;
-            u32x4 ya, yb;
-            const int t = key0 + r;
-            float ss = rope8(a, b, t, 8 * j, ya, yb);
-            ss += __shfl_xor(ss, 1);
-            ss += __shfl_xor(ss, 2);
-            const float rinv = rinv_of(ss);
-            scale_row(ya, rinv);
-            scale_row(yb, rinv);
-            *pa = ya;
-            *pb = yb;
-            if (mb_a == nmb - 1 && uu < nt_a && t < T) {
-                KargPtr ka = pro_args();
-                uint16_t* ko = reinterpret_cast<uint16_t*>(ka->k_out) + ((size_t)bh * T + t) * DP;
-                *reinterpret_cast<u32x4*>(ko + 8 * j) = ya;
-                *reinterpret_cast<u32x4*>(ko + 32 + 8 * j) = yb;
-                if (j == 0) ka->k_rinv[(size_t)bh * T + t] = rinv;
-            }
-        }
-    };
-
     auto load_q = [&](int mb) __attribute__((always_inline)) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
@@ -751,29 +715,7 @@ void born_fwd16_fast_kernel(
     constexpr int kTileLoads = 2 * LPW, kQLoads = LQW;
     const bool early_q = (nitems == 2);
     const int uq = max(1, nt_a - 4);
-    // Fused prologue: K tile u + 1 is normalised in place during step u, so
-    // at the top of step u everything issued so far (tiles u and u + 1) has
-    // to have landed; tile u + 2 then has one step to land.  Tile 0 is
-    // normalised at the top of step 0, behind one more barrier.
-    auto top_pro = [&](int u) __attribute__((always_inline)) {
-        wait_vmcnt<0>();
-        __syncthreads();
-        if (u == uq && early_q) issue_q(mb_b);
-        if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
-        if (u == 0) {
-            norm_k(0);
-            if (ntot > 1) norm_k(1);
-            __syncthreads();
-        } else if (u + 1 < ntot) {
-            norm_k(u + 1);
-        }
-        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
-    };
     auto top = [&](int u) __attribute__((always_inline)) {
-        if constexpr (PRO) {
-            top_pro(u);
-            return;
-        }
         // The first item's rows are stored at step nt_a + 1 (Born, from LDS)
         // or nt_a (purified, from registers); the next step drains them.
         const bool stores_out = (nitems == 2) && (u == nt_a + (PUR ? 1 : 2));

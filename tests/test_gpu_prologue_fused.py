@@ -1,10 +1,12 @@
-"""The Q/K prologue folded into the attention kernel
-(``qdl_flash_born_fwd_qk_prologue`` / ``flash_born_attention_qk_prologue``).
+"""The Q/K prologue folded into the attention forward
+(``qdl_flash_born_fwd_qk_prologue`` / ``flash_born_attention_qk_prologue``:
+K through the prologue kernel, Q normalised by the attention kernel as it
+loads each query block).
 
 Bars:
-  * bit for bit: the fused kernel (bf16, D = 64, dense or causal) gives the
+  * bit for bit: the fused path (bf16, D = 64, dense or causal) gives the
     same O, Z, normalised Q and K and 1/norm as the standalone prologue kernel
-    followed by the attention kernel (the same arithmetic, in one pass), on
+    on Q and K followed by the attention kernel, on
     contiguous and projection-layout inputs, full, partial and no rotary
     tables, both scale signs, per-head scales, ragged T and the C3 shape;
   * against the oracles: the normalised rows equal the prologue oracle's
