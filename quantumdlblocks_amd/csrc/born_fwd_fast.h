@@ -436,9 +436,6 @@ void born_fwd16_fast_kernel(
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
-    // of the scale is folded into Q; the asm pins the result in registers so
-    // it is not recomputed inside the tile loop.
     // Q prologue folded into the query-block load (PRO): the raw query rows
     // come in through the Q block's LDS staging as usual, and each lane turns
     // its rows' operands into q' = l2_normalize(rope(q)) in registers, with
@@ -547,6 +544,9 @@ void born_fwd16_fast_kernel(
 #pragma unroll
         for (int w = 0; w < 4; ++w) y[w] = BF16::pack(BF16::lo(y[w]) * rinv, BF16::hi(y[w]) * rinv);
     };
+    // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
+    // of the scale is folded into Q; the asm pins the result in registers so
+    // it is not recomputed inside the tile loop.
     auto load_q = [&](int mb) __attribute__((always_inline)) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
