@@ -128,7 +128,7 @@ def clock_ramp(step, done):
 
 
 def load_traffic(config):
-    """HBM bytes per forward launch measured by rocprofv3 --pmc for `config`,
+    """HBM bytes per step (every kernel of the step) measured by rocprofv3 --pmc for `config`,
     from profiles/traffic_<config>.txt (line `traffic_bytes_per_launch = N`),
     or None when no such measurement is committed."""
     path = os.path.join(ROOT, "profiles", f"traffic_{config}.txt")
@@ -428,7 +428,8 @@ def main():
     else:
         roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": mfma_peak,
                 "unit": "TFLOP/s", "frac": round(achieved_tflops / mfma_peak, 4)}
-    roof["traffic"] = None if backward else load_traffic(args.config)
+    # HBM bytes per step measured by rocprofv3 (all of the step's kernels).
+    roof["traffic"] = load_traffic(args.config)
 
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
