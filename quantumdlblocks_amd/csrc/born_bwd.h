@@ -1092,7 +1092,24 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     // offsets: the fast dQ kernel (which also forms delta and fills the
     // workspace, so no pre-pass) and then the fast dK/dV kernel
     // (born_bwd_fast.h).
-    const bool fast = DP == 64 && a.D == 64 && MODE != kGeneral && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    const bool addr32 = ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    const bool fast = DP == 64 && a.D == 64 && MODE != kGeneral && addr32;
+    // Documents without a window: the same two fast kernels' document
+    // variants (tile lists screened by document range).
+    if constexpr (DP == 64 && MODE == kGeneral) {
+        if (a.D == 64 && a.doc != nullptr && a.window == 0 && addr32) {
+            e = a.is_causal ? launch_bwd16_dq_fast<E, 64, kCausal, true>(a, st)
+                            : launch_bwd16_dq_fast<E, 64, kDense, true>(a, st);
+            if (e != hipSuccess) return e;
+            e = a.is_causal ? launch_bwd16_dkdv_fast<E, 64, kCausal, true>(a, st)
+                            : launch_bwd16_dkdv_fast<E, 64, kDense, true>(a, st);
+            if (e != hipSuccess) return e;
+            const int nwg = ((a.T + 255) / 256) * a.B * a.H;
+            hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),
+                               0, st, a, nwg);
+            return hipGetLastError();
+        }
+    }
     if constexpr (DP == 64 && MODE != kGeneral) {
         if (fast) {
             if ((e = launch_bwd16_dq_fast<E, 64, MODE>(a, st)) != hipSuccess) return e;

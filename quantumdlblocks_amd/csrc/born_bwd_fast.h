@@ -1,5 +1,5 @@
-// Flash-Born backward for head dim D == 64, dense or causal (no window, no
-// document ids): the C5 hot path.  Same arithmetic as born_bwd_dq16_kernel
+// Flash-Born backward for head dim D == 64, dense or causal, with or without
+// document ids (no window): the C5 and document-masked training hot paths.  Same arithmetic as born_bwd_dq16_kernel
 // (born_bwd.h); the tiles move and the instruction stream is laid out the way
 // born_fwd_fast.h does it.
 //
@@ -24,11 +24,86 @@
 //     (column block 0 in all four, block 1 in the last two).
 //   * The finished dQ rows are scaled, packed, staged in the idle ring and
 //     written back 16 bytes per lane (8 whole rows per store instruction).
+//
+// DOC (document ids, no window; flash_born.py:145-147, 175-177 and the
+// backward's HAS_DOC_IDS branches): the same kernels visit only the tiles
+// whose document-id range meets the block's (screened in chunks of candidate
+// tiles into a list in LDS, as the document forward does), and a tile's
+// column block is masked per element when it is on the causal diagonal or its
+// tile spans several documents, per lane when the tile is one document that
+// not all of the column block's rows (keys) belong to.
 #pragma once
+
+#include <climits>
 
 #include "born_fwd_fast.h"
 
 namespace qdl {
+
+// Tile-list entries: tile index, plus this bit when all of the tile's rows
+// belong to one document.
+constexpr int kDocOne = 1 << 30;
+
+// Document-id range of rows r0 .. r1-1 of one batch row's ids.
+__device__ __forceinline__ void doc_rows_range(const int32_t* __restrict__ docb, int r0, int r1, int n, bool vec,
+                                               int& lo, int& hi) {
+    lo = INT_MAX;
+    hi = INT_MIN;
+    if (vec && r1 - r0 == n) {
+#pragma unroll 2
+        for (int j = 0; j < n / 4; ++j) {
+            const int4 x = *reinterpret_cast<const int4*>(docb + r0 + 4 * j);
+            lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
+            hi = max(hi, max(max(x.x, x.y), max(x.z, x.w)));
+        }
+    } else {
+        for (int r = r0; r < r1; ++r) {
+            const int d = docb[r];
+            lo = min(lo, d);
+            hi = max(hi, d);
+        }
+    }
+}
+
+// Screens candidate tiles c0 .. c0+nc-1 (nc <= 256; tile t holds rows
+// row0 + TS t .. row0 + TS t + TS - 1, clipped to T) of one batch row's ids:
+// a tile is kept when its [min, max] id range meets [lo, hi] (exact for
+// sorted ids, a superset for any others, whose tiles keep the per-element
+// test).  Writes the kept tiles in ascending order to list (index | kDocOne
+// when the tile is one document) and that document to ldoc; returns how many.
+// Every thread of the 256-thread block calls it; keep / tdoc are nc-entry
+// scratch arrays, list / ldoc nc entries, count one int, all in LDS.
+template <int TS>
+__device__ int screen_doc_tiles(const int32_t* __restrict__ docb, int T, int row0, int c0, int nc, int lo, int hi,
+                                int32_t* keep, int32_t* tdoc, int32_t* list, int32_t* ldoc, int32_t* count) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const bool vec = ((reinterpret_cast<uintptr_t>(docb) | (uintptr_t)(row0 * 4)) & 15) == 0;
+    if (tid < nc) {
+        const int r0 = row0 + (c0 + tid) * TS;
+        int a, z;
+        doc_rows_range(docb, r0, min(r0 + TS, T), TS, vec, a, z);
+        keep[tid] = (z >= lo && a <= hi) ? (a == z ? 3 : 1) : 0;
+        tdoc[tid] = a;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        int n = 0;
+        for (int b0 = 0; b0 < nc; b0 += 64) {
+            const int i = b0 + lane;
+            const int kf = i < nc ? keep[i] : 0;
+            const uint64_t m = __ballot(kf != 0);
+            const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (kf != 0) {
+                list[pos] = (c0 + i) | ((kf & 2) ? kDocOne : 0);
+                ldoc[pos] = tdoc[i];
+            }
+            n += __popcll(m);
+        }
+        if (lane == 0) *count = n;
+    }
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*count);
+}
 
 // PUR: purified-Born gradients (flash_born.py:950-1061): with r the raw
 // overlap, u = relu(gamma (r - tau)), b = relu(r) (zero where masked),
@@ -36,12 +111,13 @@ namespace qdl {
 // `.to(k.dtype)` rounds it; O is the forward's fp32 output.  The dscale
 // closed form is Born's only: the purified dgamma / dtau come from the dK/dV
 // kernel.
-template <class E, int DP, int MODE, bool PUR = false>
+template <class E, int DP, int MODE, bool PUR = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    static_assert(MODE == kDense || MODE == kCausal, "no window masks here");
+    static_assert(!(PUR && DOC), "documents: Born gradients");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -49,7 +125,9 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
-    constexpr int kTileLoads = 2 * LPW;
+    constexpr int CAP = 256;               // documents: candidate tiles screened per pass
+    // Loads per wave per tile: K, V (and a 16-key slice of the key document ids).
+    constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB, "tile split / staging fits the ring");
     static_assert(BM == 4 * BN, "four 64-row slices per block");
     constexpr bool kCaus = (MODE == kCausal);
@@ -57,6 +135,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // One buffer: the K/V ring during the tile loop, the output staging
     // (256 rows x 128 bytes) once the loop is done.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+    // Documents: key document ids per stage, the kept-tile list and screening scratch.
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[2 * NW + 1];
     uint8_t* const k_lds = smem;
     uint8_t* const v_lds = smem + NST * TB;
 
@@ -100,6 +182,13 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     int qrow[NQB];
     u32x4 qr[NQB][KS], dr[NQB][KS];
     float zinv[NQB], nd[NQB];
+    // Documents: each row's document id (INT_MIN past T; such rows are not
+    // stored), kept in LDS (r_doc, by row of the block) for the tile loop,
+    // whose registers are all taken.
+    int qdoc[NQB];
+    __shared__ int32_t r_doc[DOC ? BM : 1];
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
     {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
         const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
@@ -114,6 +203,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             qrow[qb] = R + 128 * qb + lrow;
             const int qi = qrow[qb];
             const bool ok = qi < T;
+            if constexpr (DOC) {
+                qdoc[qb] = ok ? docb[qi] : INT_MIN;
+                if (g == 0) r_doc[128 * qb + lrow] = qdoc[qb];
+            }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
@@ -181,19 +274,24 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         }
     }
 
+    // Key tiles: 0 .. ntiles-1 (documents: the candidates, screened below).
     const int ntiles = kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN;
     const int t0 = kCaus ? min(R / BN, ntiles) : ntiles;  // first diagonal tile
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
     auto kswz = [](int r) __attribute__((always_inline)) { return ((r & 3) << 1) | ((r >> 2) & 1); };
 
-    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
-    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    // Tile u (documents: kept tile u of the list) -> stage u % NST:
+    // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane,
+    // slot = row * CPR + chunk'; documents: also this wave's 16 key document
+    // ids (lanes 0-3, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
-        const int key0 = u * BN;
+        int key0 = u * BN;
+        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -204,6 +302,8 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ kswz(row)) << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
         }
+        if constexpr (DOC)
+            if (lane < 4) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 16), (key0 + wave * 16 + lane * 4) * 4);
     };
 
     // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, dP^T);
@@ -247,6 +347,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // canonicalisation).  One instantiation for every tile (a second one
     // costs more registers than the wave has): the causal mask of column
     // block qb is applied under the uniform flag mk[qb].
+    // Documents, per tile: column block qb is tested per element (dm) or not
+    // at all; kdp: this stage's key document ids.
+    bool dm[NQB] = {false, false};
+    const int32_t* kdp = kd_lds;
     auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const bool (&mk)[NQB])
         __attribute__((always_inline)) {
         f32x16 s[NQB], t[NQB];
@@ -290,7 +394,22 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         } else {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
-            if (mk[qb]) {
+            if constexpr (DOC) {
+                // Key kbase + 8 (r / 4) + r % 4 of register r is masked past
+                // the lane's row (causal) or in another document.
+                if (dm[qb]) {
+                    const int lim = kCaus ? qrow[qb] - kbase : INT_MAX;
+                    const int rd = r_doc[128 * qb + 64 * (c >> 4) + 16 * wave + (c & 15)];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > lim || dk[k] != rd) s[qb][4 * i + k] = 0.f;
+                    }
+                }
+            } else if (mk[qb]) {
                 const int lim = qrow[qb] - kbase;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
@@ -332,6 +451,77 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // for tile 1), tile u+2 right after the barrier that starts step u; at
     // that barrier each wave has waited for its share of tile u (loads return
     // in order: only tile u+1's may still be in flight).
+    if constexpr (DOC) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[qb][ks]), "+v"(dr[qb][ks]));
+            asm volatile("" : "+v"(zinv[qb]), "+v"(nd[qb]));
+        }
+        // Document range of each column block's valid rows (uniform per
+        // wave; qone: all of them in document qsd) and of the whole block.
+        int qsd[NQB];
+        bool qone[NQB];
+        int wlo = INT_MAX, whi = INT_MIN;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            int lo = qrow[qb] < T ? qdoc[qb] : INT_MAX, hi = qrow[qb] < T ? qdoc[qb] : INT_MIN;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                lo = min(lo, __shfl_xor(lo, off));
+                hi = max(hi, __shfl_xor(hi, off));
+            }
+            lo = __builtin_amdgcn_readfirstlane(lo);
+            hi = __builtin_amdgcn_readfirstlane(hi);
+            qsd[qb] = lo;
+            qone[qb] = lo == hi;
+            wlo = min(wlo, lo);
+            whi = max(whi, hi);
+        }
+        if (lane == 0) {
+            s_rng[2 * wave] = wlo;
+            s_rng[2 * wave + 1] = whi;
+        }
+        __syncthreads();
+        int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_rng[2 * w]);
+            bq_hi = max(bq_hi, s_rng[2 * w + 1]);
+        }
+        // The kept tiles of each chunk of candidates through the same pipeline.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            if (n > 1) issue(1);
+            for (int u = 0; u < n; ++u) {
+                if (u + 1 < n)
+                    wait_vmcnt<kTileLoads>();
+                else
+                    wait_vmcnt<0>();
+                __syncthreads();
+                if (u + 2 < n) issue(u + 2);
+                int soff = (u % NST) * TB;
+                asm volatile("" : "+s"(soff));
+                const uint8_t* kb = k_lds + soff;
+                const uint8_t* vb = v_lds + soff;
+                kdp = kd_lds + (soff / TB) * BN;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int ti = e & ~kDocOne;
+                const bool one = (e & kDocOne) != 0;
+                // A column block is tested per element on the causal diagonal
+                // (as in the plain loop below) and unless the tile's keys and
+                // all of its rows are one and the same document.
+                const bool mk[NQB] = {ti >= t0, ti >= t0 + 2};
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) dm[qb] = mk[qb] || !(one && qone[qb] && td == qsd[qb]);
+                tile(kb, vb, ti * BN, mk);
+            }
+            __syncthreads();  // the list and the ring are reused by the next chunk
+        }
+    } else {
     if (ntiles > 0) issue(0);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
@@ -356,6 +546,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         // by the mask), block 1 cut.
         const bool mk[NQB] = {u >= t0, u >= t0 + 2};
         tile(kb, vb, u * BN, mk);
+    }
     }
 
     // Epilogue: scale, pack, stage this wave's rows in the idle ring (row r at
@@ -427,11 +618,11 @@ __global__ __launch_bounds__(256) void born_bwd_dscale_groups_kernel(BwdArgs p, 
     }
 }
 
-template <class E, int DP, int MODE>
+template <class E, int DP, int MODE, bool DOC = false>
 hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
     constexpr int BM = 256;
     const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, DP, MODE>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, DP, MODE, false, DOC>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -460,24 +651,32 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 // past T are left out of those sums (their zero K row still weighs
 // relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
 // workspace read, so they add nothing.
-template <class E, int DP, int MODE, bool PUR = false>
+template <class E, int DP, int MODE, bool PUR = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    static_assert(MODE == kDense || MODE == kCausal, "no window masks here");
+    static_assert(!(PUR && DOC), "documents: Born gradients");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BQ * RB;            // bytes per Q or dO tile
-    constexpr int SB = 2 * TB + 2 * BQ * 4;  // bytes per stage: Q, dO, -delta, 1/Z
+    // Bytes per stage: Q, dO, -delta, 1/Z (documents: and the query document ids).
+    constexpr int NROWV = DOC ? 3 : 2;
+    constexpr int SB = 2 * TB + NROWV * BQ * 4;
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
+    // Documents: candidate tiles screened per pass (three workgroups per CU
+    // leave room for 128-entry lists).
+    constexpr int CAP = 128;
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && 2 * BK * RB <= NST * SB, "tile split / staging");
     constexpr bool kCaus = (MODE == kCausal);
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[2 * NW + 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -527,7 +726,16 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             vr[ks] = y;
         }
     }
+    // Documents: this lane's key's document id (INT_MIN past T; such keys
+    // have zero K and V rows and are not stored).
+    const int32_t* __restrict__ docb = nullptr;
+    int kdoc = INT_MIN;
+    if constexpr (DOC) {
+        docb = p.doc + (size_t)(bh / p.H) * T;
+        if (key < T) kdoc = docb[key];
+    }
 
+    // Query tiles q_lo + BQ u (documents: the candidates, screened below).
     const int q_lo = kCaus ? K0 : 0;
     const int ntiles = (K0 < T) ? (T - q_lo + BQ - 1) / BQ : 0;
 
@@ -536,14 +744,20 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
     const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
     auto swz = [](int r) __attribute__((always_inline)) { return ((r & 3) << 1) | ((r >> 2) & 1); };
 
-    // Tile u -> stage u % NST.  Waves 0 and 1 also bring the tile's -delta
-    // and 1/Z (lanes 0-15, 16 bytes each): one more load per tile.
-    const int kTileLoadsW = 2 * LPW + (wave < 2 ? 1 : 0);
+    // Tile u (documents: kept tile u of the list) -> stage u % NST.  Waves 0
+    // and 1 (documents: and 2) also bring the tile's -delta, 1/Z (and query
+    // document ids), lanes 0-15, 16 bytes each: one more load per tile.
+    const int kTileLoadsW = 2 * LPW + (wave < NROWV ? 1 : 0);
+    auto tile_row0 = [&](int u) __attribute__((always_inline)) -> int {
+        if constexpr (DOC) return q_lo + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BQ;
+        return q_lo + u * BQ;
+    };
     auto issue = [&](int u) __attribute__((always_inline)) {
         uint8_t* sb = smem + (u % NST) * SB;
-        const int i0 = q_lo + u * BQ;
+        const int i0 = tile_row0(u);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
@@ -552,8 +766,15 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             dma_load16(rq, lds_addr(sb + (wave * LPW + i) * 1024), off);
             dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
         }
-        if (wave < 2 && lane < 16)
-            dma_load16(wave == 0 ? rdl : rzi, lds_addr(sb + 2 * TB + wave * BQ * 4), (i0 + 4 * lane) * 4);
+        if (lane < 16) {
+            const uint32_t la = lds_addr(sb + 2 * TB + wave * BQ * 4);
+            if (wave == 0)
+                dma_load16(rdl, la, (i0 + 4 * lane) * 4);
+            else if (wave == 1)
+                dma_load16(rzi, la, (i0 + 4 * lane) * 4);
+            else if (DOC && wave == 2)
+                dma_load16(rdoc, la, (i0 + 4 * lane) * 4);
+        }
     };
 
     const int trow_l = 4 * g + ((lane & 15) >> 2);
@@ -579,6 +800,9 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
 
+    // Documents, per tile: the wave's keys are tested per element (xm) or
+    // not at all.
+    bool xm = false;
     // One 32-query half nb of a tile (rows i0 + nb * 32 + 8 (r / 4) + 4 g +
     // r % 4 for register r).  One instantiation for every tile; the causal
     // mask (key past the query) applies under the uniform flag mk.
@@ -631,7 +855,22 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 }
             }
         } else {
-        if (mk) {
+        if constexpr (DOC) {
+            // Query qbase + 8 (r / 4) + r % 4 of register r is masked before
+            // the lane's key (causal) or in another document.
+            if (xm) {
+                const int lim = kCaus ? qbase - key : INT_MAX / 2;
+                const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int4 d4 = *reinterpret_cast<const int4*>(qd + nb * 32 + 8 * i + 4 * g);
+                    const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (8 * i + k + lim < 0 || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                }
+            }
+        } else if (mk) {
             const int lim = qbase - key;  // register r is masked when 8 (r / 4) + r % 4 < -lim
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -670,6 +909,66 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 
     // Pipeline as in the dQ kernel: tiles 0 and 1 issued up front, tile u+2
     // right after the barrier that starts step u.
+    if constexpr (DOC) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
+        // Document range of the wave's valid keys (uniform; kone: all of them
+        // in document ksd) and of the whole block.
+        int lo = key < T ? kdoc : INT_MAX, hi = key < T ? kdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            lo = min(lo, __shfl_xor(lo, off));
+            hi = max(hi, __shfl_xor(hi, off));
+        }
+        lo = __builtin_amdgcn_readfirstlane(lo);
+        hi = __builtin_amdgcn_readfirstlane(hi);
+        const int ksd = lo;
+        const bool kone = lo == hi;
+        if (lane == 0) {
+            s_rng[2 * wave] = lo;
+            s_rng[2 * wave + 1] = hi;
+        }
+        __syncthreads();
+        int bk_lo = INT_MAX, bk_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bk_lo = min(bk_lo, s_rng[2 * w]);
+            bk_hi = max(bk_hi, s_rng[2 * w + 1]);
+        }
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BQ>(docb, T, q_lo, c0, min(CAP, ntiles - c0), bk_lo, bk_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            if (n > 1) issue(1);
+            for (int u = 0; u < n; ++u) {
+                if (u + 1 < n) {
+                    if (wave < NROWV)
+                        wait_vmcnt<2 * LPW + 1>();
+                    else
+                        wait_vmcnt<2 * LPW>();
+                } else {
+                    wait_vmcnt<0>();
+                }
+                __syncthreads();
+                if (u + 2 < n) issue(u + 2);
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int i0 = q_lo + (e & ~kDocOne) * BQ;
+                if (kCaus && i0 + BQ - 1 < kw0) continue;  // every query before every key
+                int soff = (u % NST) * SB;
+                asm volatile("" : "+s"(soff));
+                const uint8_t* sb = smem + soff;
+                const bool mk = kCaus && i0 < kw0 + 31;
+                // Tested per element on the causal diagonal and unless the
+                // tile's queries and all of the wave's keys are one and the
+                // same document.
+                xm = mk || !((e & kDocOne) != 0 && kone && td == ksd);
+                half(sb, 0, i0 + 4 * g, mk);
+                half(sb, 1, i0 + 32 + 4 * g, mk);
+            }
+            __syncthreads();  // the list and the ring are reused by the next chunk
+        }
+    } else {
     if (ntiles > 0) issue(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
@@ -694,6 +993,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         const bool mk = kCaus && i0 < kw0 + 31;
         half(sb, 0, i0 + 4 * g, mk);
         half(sb, 1, i0 + 32 + 4 * g, mk);
+    }
     }
     (void)kTileLoadsW;
 
@@ -759,11 +1059,11 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         }
 }
 
-template <class E, int DP, int MODE>
+template <class E, int DP, int MODE, bool DOC = false>
 hipError_t launch_bwd16_dkdv_fast(const BwdArgs& a, hipStream_t st) {
     constexpr int BK = 128;
     const dim3 grid((unsigned)((a.T + BK - 1) / BK) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<E, DP, MODE>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<E, DP, MODE, false, DOC>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -201,6 +201,39 @@ def test_bwd_documents_many_tiles(cuda_device):
     _check_bwd(1, 1, 4500, 256, torch.float32, cuda_device, doc=doc, std=0.5)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_documents_fast_kernels(cuda_device, dtype, is_causal):
+    """D = 64 with documents and no window runs the document variants of the
+    DMA-ring dQ and dK/dV kernels: T not a multiple of the 64-row tile or of
+    the 128- / 256-row blocks, per-head scales (one negative) and dscale."""
+    doc = orc.geometric_doc_ids(2, 1100, 90.0, seed=3)
+    _check_bwd(2, 3, 1100, 64, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=[8.0, -0.5, 2.0],
+               check_dscale=True)
+
+
+def test_bwd_documents_fast_many_chunks_causal(cuda_device):
+    """More candidate tiles than one screening pass holds (256 key tiles in
+    dQ, 128 query tiles in dK/dV): a 17000-token row of sorted documents, one
+    of them longer than a pass."""
+    T = 17000
+    doc = np.zeros((1, T), dtype=np.int32)
+    doc[0, 3000:12000] = 1
+    doc[0, 12000:] = 2 + orc.geometric_doc_ids(1, T - 12000, 700.0, seed=11)[0]
+    _check_bwd(1, 2, T, 64, torch.bfloat16, cuda_device, doc=doc, seed=11)
+
+
+def test_bwd_documents_fast_many_chunks_unsorted(cuda_device):
+    """Unsorted, repeating ids over more query tiles than one dK/dV screening
+    pass holds, without causality: every tile is mixed and takes the
+    per-element test."""
+    T = 8300
+    rng = np.random.default_rng(12)
+    doc = rng.integers(0, 3, size=(1, T)).astype(np.int32)
+    doc[0, 5000:] = rng.integers(7, 9, size=T - 5000)
+    _check_bwd(1, 1, T, 64, torch.bfloat16, cuda_device, is_causal=False, doc=doc, seed=12)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_bwd_scales_and_dscale(cuda_device, dtype):
     for scale in (np.array([2.5, 3.2, -0.5, 7.0]), np.array([1.0, 0.0, -8.0, 2.0])):
