@@ -664,8 +664,10 @@ def fused_main(args):
     Q and K folded into the Born attention forward (C3 / C5 shapes, bf16,
     causal, scale 8; Q, K the (B, T, H, D) projection output, rotary tables of
     the reference's UnitaryRoPE defaults).  value: the attention's
-    algorithmic TFLOP/s of the whole fused step; detail also times the same
-    work as two launches (prologue kernel, then attention kernel)."""
+    algorithmic TFLOP/s of the whole fused step when no backward follows
+    (1/norm and q' are not written); detail also times the fused step that
+    writes them for a backward, and the same work as two launches (prologue
+    kernel, then attention kernel), with and without 1/norm."""
     import torch
 
     from quantumdlblocks_amd import _native
@@ -692,19 +694,24 @@ def fused_main(args):
         qr, kr = torch.empty_like(z), torch.empty_like(z)
         sets.append((q, k, v, out, z, qo, ko, qr, kr))
 
-    def fused(i, rotate=True):
+    def fused(i, rotate=True, bwd_outputs=False):
         q, k, v, out, z, qo, ko, qr, kr = sets[i % len(sets)] if rotate else sets[0]
         rc = lib.qdl_flash_born_fwd_qk_prologue(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st, v.data_ptr(),
                                                 cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12, scale.data_ptr(), 1,
                                                 None, 1, 0, 1e-12, out.data_ptr(), z.data_ptr(), qo.data_ptr(),
-                                                ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), stream)
+                                                ko.data_ptr(), qr.data_ptr() if bwd_outputs else None,
+                                                kr.data_ptr() if bwd_outputs else None, stream)
         _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
 
-    def separate(i):
+    def fused_train(i):
+        fused(i, bwd_outputs=True)
+
+    def separate(i, bwd_outputs=False):
         q, k, v, out, z, qo, ko, qr, kr = sets[i % len(sets)]
         rc = lib.qdl_flash_born_qk_prologue_fwd(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st,
                                                 cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12,
-                                                qo.data_ptr(), ko.data_ptr(), qr.data_ptr(), kr.data_ptr(), stream)
+                                                qo.data_ptr(), ko.data_ptr(), qr.data_ptr() if bwd_outputs else None,
+                                                kr.data_ptr() if bwd_outputs else None, stream)
         _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
         rc = lib.qdl_flash_born_fwd(code, B, H, T, D, qo.data_ptr(), ko.data_ptr(), v.data_ptr(), out.data_ptr(),
                                     z.data_ptr(), scale.data_ptr(), 1, None, 1, 0, 1e-12, stream)
@@ -729,14 +736,20 @@ def fused_main(args):
 
     wall_step, ev_step = timed(fused, steps)
     for i in range(max(steps, 50)):
+        fused_train(i)
+    _, train_ev = timed(fused_train, steps)
+    for i in range(max(steps, 50)):
         separate(i)
     sep_wall, sep_ev = timed(separate, steps)
+    _, sep_train_ev = timed(lambda i: separate(i, bwd_outputs=True), steps)
     for s_ in sets:
         assert torch.isfinite(s_[3].float()).all(), "non-finite output"
 
     flops = 4.0 * D * (T * (T + 1) // 2) * B * H
     rows = B * H * T
-    nbytes = rows * D * 2 * 3 + rows * D * 2 + rows * 4 + 2 * (rows * D * 2 + rows * 4) + 2 * T * nf * 4
+    # Algorithmic bytes of the step without a backward: read Q, K, V and the
+    # tables, write O and Z.
+    nbytes = rows * D * 2 * 3 + rows * D * 2 + rows * 4 + 2 * T * nf * 4
     value = flops / wall_step / 1e12
     roof = {"bound": "hbm", "achieved": round(nbytes / ev_step / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(nbytes / ev_step / 1e9 / PEAK_HBM_GBS, 4), "traffic": None}
@@ -762,6 +775,8 @@ def fused_main(args):
             "fused_kernel_us_per_step_events": round(ev_step * 1e6, 3),
             "separate_two_launches_us_per_step_events": round(sep_ev * 1e6, 3),
             "separate_two_launches_us_per_step_wall": round(sep_wall * 1e6, 3),
+            "with_backward_outputs_fused_us_per_step_events": round(train_ev * 1e6, 3),
+            "with_backward_outputs_separate_us_per_step_events": round(sep_train_ev * 1e6, 3),
             "algorithmic_flops": flops,
             "algorithmic_bytes": nbytes,
             "untimed_clock_ramp_steps": ramp,

@@ -202,8 +202,9 @@ int qdl_flash_purified_born_bwd(int dtype, int64_t B, int64_t H, int64_t T,
  * i < n_freq holds the angle table for pair i; pairs i >= n_freq are rotated
  * by angle 0 (cos 1, sin 0), the reference's padding of short tables
  * (attention.py:574-582).  cos_table == NULL skips the rotation.
- * Either tensor may be left out by passing NULL for all of its pointers.
- * D must be even, 2 <= D <= 256.
+ * Either tensor may be left out by passing NULL for all of its pointers;
+ * q_rinv, k_rinv may be NULL on their own (1/norm is then not written: no
+ * backward follows).  D must be even, 2 <= D <= 256.
  */
 
 /* Forward.  Replaces the apply_unitary_rope and l2_normalize calls on Q and K
@@ -254,7 +255,9 @@ int qdl_flash_born_qk_prologue_bwd(int dtype, int64_t B, int64_t H, int64_t T,
  * block in registers as it loads it, so the normalised queries are never read
  * back from memory; other cases run the prologue kernel on both and then the
  * attention kernels.  The results are those of the two separate calls, bit
- * for bit.
+ * for bit.  q_rinv and k_rinv may be NULL when no backward follows: then
+ * neither 1/norm is written, and q_out is scratch (the one-kernel path does
+ * not write it).
  * Replaces the apply_unitary_rope + l2_normalize calls on Q and K
  * (attention.py:583-589) together with the flash_born_attention call that
  * consumes them (attention.py:704-713, flash_born.py:475-513).

@@ -166,15 +166,15 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
     if (cos_table && (!sin_table || n_freq < 0 || n_freq > D / 2 || table_ld < n_freq)) return QDL_BORN_E_TABLE;
     if (!(norm_eps >= 0.0)) return QDL_BORN_E_SHAPE;
     if (B * H * T == 0) return QDL_BORN_OK;
-    if (!q || !k || !v || !q_strides || !k_strides || !out || !z || !scale || !q_out || !k_out || !q_rinv ||
-        !k_rinv)
+    if (!q || !k || !v || !q_strides || !k_strides || !out || !z || !scale || !q_out || !k_out)
         return QDL_BORN_E_NULL;
     if (!aligned16(v) || !aligned16(out) || !aligned16(q_out) || !aligned16(k_out)) return QDL_BORN_E_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     // bf16, D = 64, dense or causal: K is normalised by the prologue kernel
     // (K alone), then one attention kernel normalises each query block as it
     // loads it (raw rows 16-byte aligned, (T + 256) rows of their time stride
-    // within 32-bit offsets) and writes the normalised rows for the backward.
+    // within 32-bit offsets) and, when q_rinv is given (a backward follows),
+    // writes the normalised rows and their 1/norm.
     const bool q_rows_ok = aligned16(q) && q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 &&
                            q_strides[2] % 8 == 0 && q_strides[2] >= D &&
                            (T + 256) * q_strides[2] * 2 < ((int64_t)1 << 31);

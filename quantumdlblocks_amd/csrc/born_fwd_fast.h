@@ -459,52 +459,61 @@ void born_fwd16_fast_kernel(
         asm volatile("" : "+s"(ka));
         return ka;
     };
-    // Rotate the 8 pairs (a[v], b[v]) of columns i0 .. i0+7 of row t; returns
-    // the pairs' sum of squares.  ya, yb: the rotated (bf16-exact) values.
-    // Rows past T hold zeros (any table row gives zeros); pairs past nfreq
-    // rotate by angle 0.
-    auto rope8 = [&](const u32x4& a, const u32x4& b, int t, int i0, u32x4& ya, u32x4& yb)
+    // Table entries of row t (clamped to T - 1; rows past T hold zeros, so
+    // any table row gives zeros) for pairs i0 .. i0+7, rounded to bf16 as
+    // the prologue kernel rounds them; pairs past nfreq rotate by angle 0.
+    // Loaded for all of a lane's rows before any is used, so one memory
+    // round trip covers the whole Q block.
+    struct RotRow {
+        float c[8], s[8];
+    };
+    // vec: 16-byte loads (tables aligned, ld a multiple of 4, and all 32
+    // pairs of the head dim inside the table), the same for every lane.
+    auto load_rot = [&](int t, int i0, bool vec, RotRow& r) __attribute__((always_inline)) {
+        if constexpr (PRO) {
+            KargPtr ka = pro_args();
+            const int nf = ka->nfreq, ld = ka->ld;
+            const int tt = min(t, T - 1);
+            const float* cr = ka->cos + (size_t)tt * ld;
+            const float* sr = ka->sin + (size_t)tt * ld;
+            if (vec) {
+#pragma unroll
+                for (int v = 0; v < 8; v += 4) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(cr + i0 + v);
+                    const f32x4 y = *reinterpret_cast<const f32x4*>(sr + i0 + v);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        r.c[v + e] = x[e];
+                        r.s[v + e] = y[e];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const int idx = min(i0 + v, nf - 1);
+                    const float x = cr[idx], y = sr[idx];
+                    r.c[v] = (i0 + v < nf) ? x : 1.f;
+                    r.s[v] = (i0 + v < nf) ? y : 0.f;
+                }
+            }
+        }
+    };
+    // Rotate the 8 pairs (a[v], b[v]) of columns i0 .. i0+7 of a row by the
+    // table entries r (rot: a table was given); returns the pairs' sum of
+    // squares.  ya, yb: the rotated (bf16-exact) values.
+    auto rope8 = [&](const u32x4& a, const u32x4& b, RotRow& r, bool rot, u32x4& ya, u32x4& yb)
         __attribute__((always_inline)) -> float {
 #pragma clang fp contract(off)
         float ss = 0.f;
         if constexpr (PRO) {
-            KargPtr ka = pro_args();
-            float cs[8], sn[8];
-            const bool rot = ka->cos != nullptr;
             if (rot) {
-                const int nf = ka->nfreq, ld = ka->ld;
-                const int tt = min(t, T - 1);
-                const float* cr = ka->cos + (size_t)tt * ld;
-                const float* sr = ka->sin + (size_t)tt * ld;
-                const bool vec = ((reinterpret_cast<uintptr_t>(ka->cos) | reinterpret_cast<uintptr_t>(ka->sin)) & 15) == 0 &&
-                                 (ld & 3) == 0 && i0 + 8 <= nf;
-                if (vec) {
-#pragma unroll
-                    for (int v = 0; v < 8; v += 4) {
-                        const f32x4 x = *reinterpret_cast<const f32x4*>(cr + i0 + v);
-                        const f32x4 y = *reinterpret_cast<const f32x4*>(sr + i0 + v);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            cs[v + e] = x[e];
-                            sn[v + e] = y[e];
-                        }
-                    }
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 8; ++v) {
-                        const int idx = min(i0 + v, nf - 1);
-                        const float x = cr[idx], y = sr[idx];
-                        cs[v] = (i0 + v < nf) ? x : 1.f;
-                        sn[v] = (i0 + v < nf) ? y : 0.f;
-                    }
-                }
 #pragma unroll
                 for (int v = 0; v < 8; v += 2) {
-                    const uint32_t uc = BF16::pack(cs[v], cs[v + 1]), us = BF16::pack(sn[v], sn[v + 1]);
-                    cs[v] = BF16::lo(uc);
-                    cs[v + 1] = BF16::hi(uc);
-                    sn[v] = BF16::lo(us);
-                    sn[v + 1] = BF16::hi(us);
+                    const uint32_t uc = BF16::pack(r.c[v], r.c[v + 1]), us = BF16::pack(r.s[v], r.s[v + 1]);
+                    r.c[v] = BF16::lo(uc);
+                    r.c[v + 1] = BF16::hi(uc);
+                    r.s[v] = BF16::lo(us);
+                    r.s[v + 1] = BF16::hi(us);
                 }
             }
 #pragma unroll
@@ -516,10 +525,10 @@ void born_fwd16_fast_kernel(
                     const float x2 = e ? BF16::hi(b[w]) : BF16::lo(b[w]);
                     if (rot) {
                         const int v = 2 * w + e;
-                        const float r0 = BF16::lo(BF16::pack(x1 * cs[v], 0.f));
-                        const float r1 = BF16::lo(BF16::pack(x2 * sn[v], 0.f));
-                        const float r2 = BF16::lo(BF16::pack(x1 * sn[v], 0.f));
-                        const float r3 = BF16::lo(BF16::pack(x2 * cs[v], 0.f));
+                        const float r0 = BF16::lo(BF16::pack(x1 * r.c[v], 0.f));
+                        const float r1 = BF16::lo(BF16::pack(x2 * r.s[v], 0.f));
+                        const float r2 = BF16::lo(BF16::pack(x1 * r.s[v], 0.f));
+                        const float r3 = BF16::lo(BF16::pack(x2 * r.c[v], 0.f));
                         y1[e] = BF16::lo(BF16::pack(r0 - r1, 0.f));
                         y2[e] = BF16::lo(BF16::pack(r2 + r3, 0.f));
                     } else {
@@ -551,6 +560,31 @@ void born_fwd16_fast_kernel(
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+        // The Q prologue: every table entry this lane needs, for both of its
+        // rows, before any is used.
+        RotRow rtab[PRO ? NQB : 1][2];
+        bool rot = false;
+        if constexpr (PRO) {
+            KargPtr ka = pro_args();
+            rot = ka->cos != nullptr;
+            // One branch around all four row loads, so they form one batch.
+            auto load_all = [&](bool vec) __attribute__((always_inline)) {
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) {
+                    const int t = mb * BM + 128 * qb + lr;
+                    load_rot(t, 8 * (ln >> 5), vec, rtab[qb][0]);
+                    load_rot(t, 8 * (2 + (ln >> 5)), vec, rtab[qb][1]);
+                }
+            };
+            if (rot) {
+                const bool vec = ((reinterpret_cast<uintptr_t>(ka->cos) | reinterpret_cast<uintptr_t>(ka->sin)) & 15) == 0 &&
+                                 (ka->ld & 3) == 0 && ka->nfreq >= DP / 2;
+                if (vec)
+                    load_all(true);
+                else
+                    load_all(false);
+            }
+        }
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
@@ -565,8 +599,8 @@ void born_fwd16_fast_kernel(
                 const int gg = ln >> 5;
                 const int t = mb * BM + 128 * qb + lr;
                 u32x4 y0, y1, y2, y3;
-                const float pa = rope8(qr[qb][0], qr[qb][2], t, 8 * gg, y0, y2);
-                const float pb = rope8(qr[qb][1], qr[qb][3], t, 8 * (2 + gg), y1, y3);
+                const float pa = rope8(qr[qb][0], qr[qb][2], rtab[qb][0], rot, y0, y2);
+                const float pb = rope8(qr[qb][1], qr[qb][3], rtab[qb][1], rot, y1, y3);
                 const float s01 = pa + __shfl_xor(pa, 32);
                 const float s23 = pb + __shfl_xor(pb, 32);
                 const float rinv = rinv_of(s01 + s23);
@@ -578,12 +612,15 @@ void born_fwd16_fast_kernel(
                 qr[qb][1] = y1;
                 qr[qb][2] = y2;
                 qr[qb][3] = y3;
-                if (t < T) {
+                // The normalised rows and their 1/norm, for the backward
+                // (not written when no backward follows: q_rinv null).
+                if (t < T && pro_args()->q_rinv != nullptr) {
                     KargPtr ka = pro_args();
                     uint16_t* qo = reinterpret_cast<uint16_t*>(ka->q_out) + ((size_t)bh * T + t) * DP;
 #pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) *reinterpret_cast<u32x4*>(qo + 8 * (2 * ks + gg)) = qr[qb][ks];
-                    if (gg == 0) ka->q_rinv[(size_t)bh * T + t] = rinv;
+                    for (int ks = 0; ks < KS; ++ks)
+                        __builtin_nontemporal_store(qr[qb][ks], reinterpret_cast<u32x4*>(qo + 8 * (2 * ks + gg)));
+                    if (gg == 0) __builtin_nontemporal_store(rinv, ka->q_rinv + (size_t)bh * T + t);
                 }
             }
 #pragma unroll

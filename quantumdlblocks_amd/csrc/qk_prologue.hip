@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(PrologueArgs p) {
             IO::store(dst + (int64_t)(half + j * VEC) * IO::kBytes, VEC, o2);
         }
     }
-    if (j0 == 0) p.rinv_out[which][pos.lin] = rinv;
+    if (j0 == 0 && p.rinv_out[which] != nullptr) p.rinv_out[which][pos.lin] = rinv;
 }
 
 // Backward.  Same grid and lane mapping as the forward.
@@ -486,8 +486,8 @@ int qdl_flash_born_qk_prologue_fwd(int dtype, int64_t B, int64_t H, int64_t T, i
     if (rc != QDL_BORN_OK) return rc;
     if (!(eps >= 0.0)) return QDL_BORN_E_SHAPE;
     if (B * H * T == 0 || (!q && !k)) return QDL_BORN_OK;
-    if (q && (!q_strides || !q_out || !q_rinv)) return QDL_BORN_E_NULL;
-    if (k && (!k_strides || !k_out || !k_rinv)) return QDL_BORN_E_NULL;
+    if (q && (!q_strides || !q_out)) return QDL_BORN_E_NULL;
+    if (k && (!k_strides || !k_out)) return QDL_BORN_E_NULL;
     PrologueArgs a = {};
     a.src[0] = ref(q, q_strides, H, T, D);
     a.src[1] = ref(k, k_strides, H, T, D);

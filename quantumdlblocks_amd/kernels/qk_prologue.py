@@ -289,10 +289,11 @@ def fused_qk_rope_l2_normalize(
 
 class _BornQKPrologueFn(torch.autograd.Function):
     """Forward: Born attention of (q', k', v) with q' = l2_normalize(rope(q)),
-    k' likewise, in one call of ``qdl_flash_born_fwd_qk_prologue`` (one
-    kernel for bf16, D = 64, no documents or window: Q normalised as each
-    query block is loaded, K as each key tile lands in LDS).  Saves q', k' and
-    1/norm.  Backward: the attention backward on (q', k', v), then the
+    k' likewise, in one call of ``qdl_flash_born_fwd_qk_prologue`` (for bf16,
+    D = 64, no documents or window: the prologue kernel on K alone, then one
+    attention kernel that normalises each query block as it loads it).  Saves
+    q', k' and 1/norm when a gradient is needed (otherwise 1/norm and q' are
+    not written).  Backward: the attention backward on (q', k', v), then the
     prologue backward into q and k (their dtypes and strides)."""
 
     @staticmethod
@@ -315,8 +316,9 @@ class _BornQKPrologueFn(torch.autograd.Function):
         z = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
         q_out = torch.empty_like(out)
         k_out = torch.empty_like(out)
-        q_r = torch.empty_like(z)
-        k_r = torch.empty_like(z)
+        grad = any(ctx.needs_input_grad[:4])
+        q_r = torch.empty_like(z) if grad else None
+        k_r = torch.empty_like(z) if grad else None
         qs, ks = _strides(q_in), _strides(k_in)
         window = max(int(window_size), 0)
         with torch.cuda.device(q.device):
@@ -331,9 +333,11 @@ class _BornQKPrologueFn(torch.autograd.Function):
                 doc_c.data_ptr() if doc_c is not None else None,
                 1 if is_causal else 0, window, float(eps),
                 out.data_ptr(), z.data_ptr(), q_out.data_ptr(), k_out.data_ptr(),
-                q_r.data_ptr(), k_r.data_ptr(), _stream_ptr(q.device),
+                q_r.data_ptr() if grad else None, k_r.data_ptr() if grad else None, _stream_ptr(q.device),
             )
         _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
+        if not grad:
+            return out
         ctx.save_for_backward(q_out, k_out, v_c, out, z, scale_flat, q_r, k_r,
                               doc_c if doc_c is not None else torch.empty(0, dtype=torch.int32, device=q.device))
         ctx.tables = (cos.detach(), sin.detach()) if cos is not None else (None, None)

@@ -52,9 +52,11 @@ def _inputs(B, H, T, D, dtype, strided, seed, dev, std=1.0):
     return q, k, v, do
 
 
-def _abi(fused, q, k, v, scale, cos, sin, causal=True, eps=1e-12, doc=None, window=0):
+def _abi(fused, q, k, v, scale, cos, sin, causal=True, eps=1e-12, doc=None, window=0, rinv=True):
     """Through the C ABI: the fused entry (fused=True) or the prologue entry
-    followed by the forward entry.  Returns out, z, q', k', q_rinv, k_rinv."""
+    followed by the forward entry.  Returns out, z, q', k', q_rinv, k_rinv
+    (rinv=False: 1/norm pointers NULL, as when no backward follows; the
+    returned 1/norm buffers then hold NaN, their fill)."""
     from quantumdlblocks_amd import _native
     from quantumdlblocks_amd.kernels.flash_born import _DTYPE_CODE
     from quantumdlblocks_amd.kernels.qk_prologue import _prep_tables, _strides
@@ -71,7 +73,8 @@ def _abi(fused, q, k, v, scale, cos, sin, causal=True, eps=1e-12, doc=None, wind
     out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
     z = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     qo, ko = torch.empty_like(out), torch.empty_like(out)
-    qr, kr = torch.empty_like(z), torch.empty_like(z)
+    qr, kr = torch.full_like(z, float("nan")), torch.full_like(z, float("nan"))
+    qrp, krp = (qr.data_ptr(), kr.data_ptr()) if rinv else (None, None)
     qs, ks = _strides(q), _strides(k)
     stream = torch.cuda.current_stream(dev).cuda_stream
     docp = None if doc_t is None else doc_t.data_ptr()
@@ -79,13 +82,12 @@ def _abi(fused, q, k, v, scale, cos, sin, causal=True, eps=1e-12, doc=None, wind
         rc = lib.qdl_flash_born_fwd_qk_prologue(code, B, H, T, D, q.data_ptr(), qs.data_ptr(), k.data_ptr(),
                                                 ks.data_ptr(), v.data_ptr(), *tabs, 1e-12, sc.data_ptr(),
                                                 sc.numel(), docp, int(causal), window, eps, out.data_ptr(),
-                                                z.data_ptr(), qo.data_ptr(), ko.data_ptr(), qr.data_ptr(),
-                                                kr.data_ptr(), stream)
+                                                z.data_ptr(), qo.data_ptr(), ko.data_ptr(), qrp, krp, stream)
         _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
     else:
         rc = lib.qdl_flash_born_qk_prologue_fwd(code, B, H, T, D, q.data_ptr(), qs.data_ptr(), k.data_ptr(),
                                                 ks.data_ptr(), *tabs, 1e-12, qo.data_ptr(), ko.data_ptr(),
-                                                qr.data_ptr(), kr.data_ptr(), stream)
+                                                qrp, krp, stream)
         _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
         rc = lib.qdl_flash_born_fwd(code, B, H, T, D, qo.data_ptr(), ko.data_ptr(), v.data_ptr(), out.data_ptr(),
                                     z.data_ptr(), sc.data_ptr(), sc.numel(), docp, int(causal), window, eps, stream)
@@ -124,6 +126,26 @@ def test_fused_equals_prologue_then_attention_bitwise(cuda_device, case):
     b = _abi(False, q, k, v, scale, cos, sin, causal)
     for name, x, y in zip(("out", "z", "q'", "k'", "q_rinv", "k_rinv"), a, b):
         assert _same(x, y), name
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_fused_without_backward_outputs(cuda_device, causal):
+    """1/norm pointers NULL (no backward follows): O and Z bit for bit as
+    with them, k' still written (the attention reads it), 1/norm buffers
+    untouched; the same through the two launches."""
+    q, k, v, _ = _inputs(2, 3, 700, 64, torch.bfloat16, True, seed=41, dev=cuda_device, std=0.7)
+    cos, sin = (x.to(cuda_device) for x in _tables(700, 32))
+    full = _abi(True, q, k, v, 8.0, cos, sin, causal)
+    for fused in (True, False):
+        part = _abi(fused, q, k, v, 8.0, cos, sin, causal, rinv=False)
+        for name, i in (("out", 0), ("z", 1), ("k'", 3)):
+            assert _same(part[i], full[i]), (fused, name)
+        assert torch.isnan(part[4]).all() and torch.isnan(part[5]).all(), fused
+    from quantumdlblocks_amd import flash_born_attention_qk_prologue
+
+    with torch.no_grad():
+        o_ng = flash_born_attention_qk_prologue(q, k, v, 8.0, cos, sin, is_causal=causal)
+    assert _same(o_ng, full[0])
 
 
 def test_fused_c3_shape_bitwise_and_oracle(cuda_device):

@@ -156,7 +156,8 @@ def test_qk_prologue_argument_validation(lib):
         assert call(B=0) == 0  # empty: nothing to launch
     assert fwd(eps=-1.0) == m["QDL_BORN_E_SHAPE"]
     assert fwd(qo=None) == m["QDL_BORN_E_NULL"]
-    assert fwd(kr=None) == m["QDL_BORN_E_NULL"]
+    # (q_rinv / k_rinv may be NULL: 1/norm not written; exercised on the GPU.)
+    assert fwd(ko=None) == m["QDL_BORN_E_NULL"]
     assert fwd(qs=None) == m["QDL_BORN_E_NULL"]
     assert fwd(q=None, k=None) == 0  # neither tensor given
     assert bwd(qo=None) == m["QDL_BORN_E_NULL"]
