@@ -61,6 +61,16 @@ CONFIGS = {
     "p4b": (4, 16, 8192, 64, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
 }
 PURIFIED = {"p3", "p5", "p4b"}
+# Outside the D = 64 / no-window fast kernels, on the C3 work: head dim 128
+# (half the heads, same flops and bytes) and sliding windows (causal, the
+# reference's window_size; runtime-changed windows, born_gpt.py:594).
+CONFIGS.update({
+    "d3": (16, 8, 1024, 128, 0.125, False, None, False),
+    "d5": (16, 8, 2048, 128, 1.0, False, None, True),
+    "w3": (16, 16, 1024, 64, 0.125, False, None, False),
+    "w5": (16, 16, 2048, 64, 1.0, False, None, True),
+})
+WINDOW = {"w3": 256, "w5": 512}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
@@ -168,9 +178,13 @@ def make_inputs(cfg, seed, device, dtype):
     return [x.to(device, dtype).contiguous() for x in (q, k, v, do)], doc
 
 
-def visible_pairs(cfg, doc):
-    """Visible (b, i, j) pairs summed over the batch, per head (causal)."""
+def visible_pairs(cfg, doc, window=0):
+    """Visible (b, i, j) pairs summed over the batch, per head (causal; with a
+    sliding window row i sees min(i + 1, window) keys)."""
     B, H, T = cfg[0], cfg[1], cfg[2]
+    if window > 0:
+        w = min(window, T)
+        return B * (w * (w + 1) // 2 + (T - w) * w)
     if doc is None:
         return B * T * (T + 1) // 2
     import numpy as np
@@ -182,7 +196,7 @@ def visible_pairs(cfg, doc):
     return total
 
 
-def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None):
+def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None, window=0):
     """Time the reference's eager CPU path (fp32, full T x T) on a bounded sample
     of the same workload: n heads of batch row 0, its document mask when the
     config has documents, and the autograd backward when the config has one.
@@ -199,7 +213,7 @@ def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None):
     def eager(q, k, v, sc):
         if purified:
             return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS, doc_ids=doc_row)
-        return eager_fp32_torch(q, k, v, sc, doc_ids=doc_row)
+        return eager_fp32_torch(q, k, v, sc, window_size=window, doc_ids=doc_row)
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -236,7 +250,9 @@ def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    if doc_row is None:
+    if window > 0:
+        pairs = visible_pairs((1, 1, T), None, window)
+    elif doc_row is None:
         pairs = T * (T + 1) // 2
     else:
         _, counts = np.unique(doc_row.numpy()[0], return_counts=True)  # documents are contiguous runs
@@ -320,6 +336,7 @@ def main():
     B, H, T, D = cfg[:4]
     backward = cfg[7]
     purified = args.config in PURIFIED
+    window = WINDOW.get(args.config, 0)
     steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
 
     sets = []
@@ -365,14 +382,14 @@ def main():
         q, k, v, _, out, z, _ = s
         rc = lib.qdl_flash_born_fwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                     out.data_ptr(), z.data_ptr(), scale.data_ptr(), 1, doc_ptr,
-                                    1, 0, 1e-12, stream)
+                                    1, window, 1e-12, stream)
         _native.check(rc, "qdl_flash_born_fwd")
 
     def bwd(s):
         q, k, v, do, out, z, (dq, dk, dv) = s
         rc = lib.qdl_flash_born_bwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                     out.data_ptr(), do.data_ptr(), z.data_ptr(), scale.data_ptr(), 1,
-                                    doc_ptr, 1, 0, 1e-12, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    doc_ptr, 1, window, 1e-12, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                     dscale.data_ptr(), ws.data_ptr(), ws.numel(), stream)
         _native.check(rc, "qdl_flash_born_bwd")
 
@@ -405,7 +422,7 @@ def main():
     for s in sets:
         assert torch.isfinite(s[4]).all(), "non-finite output"
 
-    pairs = visible_pairs(cfg, doc)
+    pairs = visible_pairs(cfg, doc, window)
     fwd_flops = 4.0 * D * pairs * H
     flops = fwd_flops * (3.5 if backward else 1.0)
     el = 2  # bf16 bytes
@@ -434,7 +451,7 @@ def main():
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
         cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed, purified,
-                           None if doc is None else doc.cpu().numpy())
+                           None if doc is None else doc.cpu().numpy(), window)
         cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
 
     name = "fwd" if not backward else "fwd+bwd"
@@ -455,7 +472,7 @@ def main():
         "config": {
             "workload": args.config + (" (headline)" if args.config == "c3" else ""),
             "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
-            "doc_mask": doc is not None, "backward": backward, "scale": 8.0,
+            "doc_mask": doc is not None, "window": window, "backward": backward, "scale": 8.0,
             "eps": PUR_EPS if purified else 1e-12,
             **({"tau": PUR_TAU, "eps_base": PUR_EPS_BASE} if purified else {}),
         },

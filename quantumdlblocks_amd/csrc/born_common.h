@@ -203,6 +203,7 @@ enum MaskMode : int {
     kDense = 0,    // non-causal, no window, no documents
     kCausal = 1,   // causal only
     kGeneral = 2,  // runtime causal flag + window + document ids
+    kWindow = 3,   // causal with a sliding window (the D = 64 fast kernels only)
 };
 
 // Document ids: the span of candidate tiles a block has to visit.  The

@@ -14,6 +14,9 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
     const bool addr32 = ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
     // Documents (no window): the document-aware fast kernel.
     if (a.D == 64 && a.doc != nullptr && a.window == 0 && addr32) return launch_fwd16_doc<BF16, 64>(a, s);
+    // Causal sliding window (no documents): the fast kernel's window mode.
+    if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32)
+        return launch_fwd16_fast<BF16, 64, kWindow>(a, s);
     if (a.D == 64 && mode != kGeneral && addr32)
         return mode == kCausal ? launch_fwd16_fast<BF16, 64, kCausal>(a, s) : launch_fwd16_fast<BF16, 64, kDense>(a, s);
 #define QDL_MODE_BODY(M) return launch_fwd16<BF16, DPV, M>(a, s);

@@ -130,9 +130,10 @@ template <class E, int DP, int MODE, bool PUR = false, bool PRO = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_fast_kernel(
     typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal, "no window / document masks here");
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
+    static_assert(MODE != kWindow || (!PUR && !PRO), "sliding windows: Born forward");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
     constexpr int KS = DP / 16;
@@ -146,7 +147,12 @@ void born_fwd16_fast_kernel(
     constexpr int LQW = QB / (1024 * NW);  // 1-KiB loads per wave per Q block
     static_assert(TB % (1024 * NW) == 0 && QB % (1024 * NW) == 0, "tile split");
     static_assert(NST == 3, "vmcnt bookkeeping below assumes a three-stage ring");
-    constexpr bool kCaus = (MODE == kCausal);
+    // kWindow: causal, and row i sees keys i - window + 1 .. i
+    // (flash_born.py:152, 173-174).  Launched unpaired (one block per
+    // workgroup: blocks carry about equal work); each block visits the key
+    // tiles from its window's first key on.
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
 
     // The DMA loads are issued as inline asm, so the compiler never waits on
     // them; their completion is tracked by the pipeline's own vmcnt waits and
@@ -175,12 +181,16 @@ void born_fwd16_fast_kernel(
     const int h = bh % p.H;
     const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
+    const int W = kWin ? p.window : 0;
+    // First key tile of a block (its window's first key), and its tile count.
+    auto item_t0 = [&](int mb) -> int { return kWin ? max(0, mb * BM - W + 1) / BN : 0; };
     auto item_tiles = [&](int mb) -> int {
         const int kv_hi = kCaus ? min(T, (mb + 1) * BM) : T;
-        return (kv_hi + BN - 1) / BN;
+        return (kv_hi + BN - 1) / BN - item_t0(mb);
     };
     const int nt_a = item_tiles(mb_a);
     const int ntot = nt_a + (nitems == 2 ? item_tiles(mb_b) : 0);
+    const int tb_a = item_t0(mb_a), tb_b = item_t0(mb_b);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -218,7 +228,7 @@ void born_fwd16_fast_kernel(
     // Tile u of the block's sequence -> stage st: wave-instruction i writes
     // LDS slots (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
     auto issue = [&](int u, int st) __attribute__((always_inline)) {
-        const int key0 = (u < nt_a ? u : u - nt_a) * BN;
+        const int key0 = (u < nt_a ? tb_a + u : tb_b + (u - nt_a)) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -321,10 +331,15 @@ void born_fwd16_fast_kernel(
         for (int qb = 0; qb < NQB; ++qb) {
             if (M[qb] == kSkip) continue;
             if (M[qb] == kMasked) {
+                // Key kbase + 8 (r / 4) + r % 4 of register r: masked past the
+                // lane's row, and (window) before the row's first key.
                 const int lim = qrow[qb] - kbase;
+                const int wlo = kWin ? lim - W + 1 : 0;
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = 0.f;
+                for (int r = 0; r < 16; ++r) {
+                    const int off = 8 * (r >> 2) + (r & 3);
+                    if (off > lim || (kWin && off < wlo)) s[qb][r] = 0.f;
+                }
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -777,9 +792,15 @@ void born_fwd16_fast_kernel(
     for (int it = 0; it < nitems; ++it) {
         const int mb = it ? mb_b : mb_a;
         const int nt = it ? ntot - nt_a : nt_a;
-        // Purified, non-causal, T not a multiple of the tile: the last tile
-        // masks the keys past T.
-        const int t0 = kCaus ? min(mb * (BM / BN), nt) : ((PUR && T % BN) ? nt - 1 : nt);
+        // Tiles are counted from the item's first key tile tb (0 but for
+        // windows).  Purified, non-causal, T not a multiple of the tile: the
+        // last tile masks the keys past T.
+        const int tb = it ? tb_b : tb_a;
+        const int t0 = kCaus ? min(mb * (BM / BN) - tb, nt) : ((PUR && T % BN) ? nt - 1 : nt);
+        // Window: tiles before te hold keys older than some row's window (the
+        // block's last row R + 255 sees keys from R + 256 - W on): both
+        // column blocks tested per element there.
+        const int te = kWin ? min(max((mb * BM + BM - W + BN - 1) / BN - tb, 0), t0) : 0;
         // The item's first step: the previous item's rows go out right
         // after this barrier, a full step before the next wait.
         top(u);
@@ -805,27 +826,42 @@ void born_fwd16_fast_kernel(
             vb = v_lds + soff;
         };
         int t = 0;
+        if constexpr (kWin) {
+            for (; t < te; ++t, ++u) {
+                if (!at_top) top(u);
+                at_top = false;
+                const uint8_t *kb, *vb;
+                stage(u, kb, vb);
+                read_k(kop, kb, 0);
+                tile(kb, vb, (tb + t) * BN, Masked{}, Masked{});
+            }
+        }
         for (; t < t0; ++t, ++u) {
             if (!at_top) top(u);
             at_top = false;
             const uint8_t *kb, *vb;
             stage(u, kb, vb);
             read_k(kop, kb, 0);
-            tile(kb, vb, t * BN, Full{}, Full{});
+            tile(kb, vb, (tb + t) * BN, Full{}, Full{});
         }
         if constexpr (kCaus) {
             // Diagonal tiles 0 and 1: block 0 cut by the mask, block 1 fully
-            // visible; tiles 2 and 3: block 0 fully masked, block 1 cut.
+            // visible (window: tested too, it may start inside the tile);
+            // tiles 2 and 3: block 0 fully masked, block 1 cut.
             for (; t < nt; ++t, ++u) {
                 if (!at_top) top(u);
                 at_top = false;
                 const uint8_t *kb, *vb;
                 stage(u, kb, vb);
                 read_k(kop, kb, 0);
-                if (t - t0 < 2)
-                    tile(kb, vb, t * BN, Masked{}, Full{});
-                else
-                    tile(kb, vb, t * BN, Skip{}, Masked{});
+                if (t - t0 < 2) {
+                    if constexpr (kWin)
+                        tile(kb, vb, (tb + t) * BN, Masked{}, Masked{});
+                    else
+                        tile(kb, vb, (tb + t) * BN, Masked{}, Full{});
+                } else {
+                    tile(kb, vb, (tb + t) * BN, Skip{}, Masked{});
+                }
             }
         } else if constexpr (PUR) {
             for (; t < nt; ++t, ++u) {
@@ -852,11 +888,11 @@ template <class E, int DP, int MODE>
 hipError_t launch_fwd16_fast(const FwdArgs& a, hipStream_t st) {
     using C = FastFwdCfg<DP>;
     // Pair query blocks unless that leaves fewer than two workgroups per CU
-    // (256 CUs): then one block per workgroup.
+    // (256 CUs): then one block per workgroup.  Windows: never paired.
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid(npair < 512u ? nsingle : npair);
+    const dim3 grid((npair < 512u || MODE == kWindow) ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<E, DP, MODE>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }

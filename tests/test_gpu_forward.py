@@ -134,6 +134,22 @@ def test_fwd_sliding_window(cuda_device, dtype, window, is_causal):
     _check_fwd(2, 2, 200, 64, dtype, cuda_device, is_causal=is_causal, window_size=window, seed=window)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 63, 64, 65, 100, 255, 256, 257, 320, 512, 900])
+def test_fwd_sliding_window_fast_kernel(cuda_device, dtype, window):
+    """Causal windows at D = 64 run the fast kernel's window mode: windows
+    that start inside, on and beside the 64-key tile and 256-row block
+    edges, longer than T, over several blocks and a partial last block."""
+    _check_fwd(2, 2, 1100, 64, dtype, cuda_device, window_size=window, seed=window + 7)
+
+
+def test_fwd_sliding_window_c3_shape(cuda_device):
+    """C3's shape with a 256-key window, 16 heads covering every block
+    residue of the launch."""
+    sel = [(b, b) for b in range(16)]
+    _check_fwd(16, 16, 1024, 64, torch.bfloat16, cuda_device, window_size=256, std=0.125, heads=sel)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_fwd_document_mask(cuda_device, dtype, is_causal):
