@@ -116,8 +116,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal, "no window masks here");
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!(PUR && DOC), "documents: Born gradients");
+    static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -130,7 +131,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB, "tile split / staging fits the ring");
     static_assert(BM == 4 * BN, "four 64-row slices per block");
-    constexpr bool kCaus = (MODE == kCausal);
+    // kWindow: causal, row i sees keys i - window + 1 .. i (flash_born.py:394,
+    // 415-416): the block visits the key tiles from its window's first key on.
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
 
     // One buffer: the K/V ring during the tile loop, the output staging
     // (256 rows x 128 bytes) once the loop is done.
@@ -274,9 +278,15 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         }
     }
 
-    // Key tiles: 0 .. ntiles-1 (documents: the candidates, screened below).
-    const int ntiles = kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN;
-    const int t0 = kCaus ? min(R / BN, ntiles) : ntiles;  // first diagonal tile
+    // Key tiles tb .. tb+ntiles-1 (tb: the window's first key tile, else 0;
+    // documents: the candidates, screened below), counted from tb.
+    const int W = kWin ? p.window : 0;
+    const int tb = kWin ? max(0, R - W + 1) / BN : 0;
+    const int ntiles = (kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN) - tb;
+    const int t0 = kCaus ? min(R / BN - tb, ntiles) : ntiles;  // first diagonal tile
+    // Window: tiles before te hold keys older than the window of some row (the
+    // block's last row sees keys from R + BM - W on).
+    const int te = kWin ? min(max((R + BM - W + BN - 1) / BN - tb, 0), t0) : 0;
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
@@ -290,7 +300,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // ids (lanes 0-3, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
-        int key0 = u * BN;
+        int key0 = (tb + u) * BN;
         if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
@@ -410,10 +420,14 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     }
                 }
             } else if (mk[qb]) {
+                // Masked past the lane's row, and (window) before its first key.
                 const int lim = qrow[qb] - kbase;
+                const int wlo = kWin ? lim - W + 1 : 0;
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = 0.f;
+                for (int r = 0; r < 16; ++r) {
+                    const int off = 8 * (r >> 2) + (r & 3);
+                    if (off > lim || (kWin && off < wlo)) s[qb][r] = 0.f;
+                }
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -543,9 +557,11 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         const uint8_t* vb = v_lds + soff;
         // Diagonal tiles t0, t0+1: block 0 cut by the mask, block 1 fully
         // visible; t0+2, t0+3: block 0 fully masked (computed, then zeroed
-        // by the mask), block 1 cut.
-        const bool mk[NQB] = {u >= t0, u >= t0 + 2};
-        tile(kb, vb, u * BN, mk);
+        // by the mask), block 1 cut.  Window: both blocks tested on the
+        // window's edge tiles and on all four diagonal tiles.
+        const bool medge = kWin && (u < te || u >= t0);
+        const bool mk[NQB] = {u >= t0 || medge, u >= t0 + 2 || medge};
+        tile(kb, vb, (tb + u) * BN, mk);
     }
     }
 
@@ -656,8 +672,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal, "no window masks here");
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!(PUR && DOC), "documents: Born gradients");
+    static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -672,7 +689,10 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     // leave room for 128-entry lists).
     constexpr int CAP = 128;
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && 2 * BK * RB <= NST * SB, "tile split / staging");
-    constexpr bool kCaus = (MODE == kCausal);
+    // kWindow: causal, key j is seen by queries j .. j + window - 1: the
+    // block visits the query tiles up to its last key's window.
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
     __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
@@ -735,9 +755,12 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         if (key < T) kdoc = docb[key];
     }
 
-    // Query tiles q_lo + BQ u (documents: the candidates, screened below).
+    // Query tiles q_lo + BQ u (documents: the candidates, screened below;
+    // window: up to the last query that sees the block's last key).
+    const int W = kWin ? p.window : 0;
     const int q_lo = kCaus ? K0 : 0;
-    const int ntiles = (K0 < T) ? (T - q_lo + BQ - 1) / BQ : 0;
+    const int q_hi = kWin ? (int)min((int64_t)T, (int64_t)K0 + BK - 1 + W) : T;
+    const int ntiles = (K0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
@@ -871,10 +894,14 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 }
             }
         } else if (mk) {
-            const int lim = qbase - key;  // register r is masked when 8 (r / 4) + r % 4 < -lim
+            // Register r (query qbase + off) is masked before the lane's key
+            // (off + lim < 0) and (window) past its window (off + lim >= W).
+            const int lim = qbase - key;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + (r & 3) + lim < 0) s[r] = 0.f;
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off + lim < 0 || (kWin && off + lim >= W)) s[r] = 0.f;
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -987,10 +1014,11 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         const int i0 = q_lo + u * BQ;
         // This wave's keys kw0 .. kw0+31 against queries i0 .. i0+63.
         if (kCaus && i0 + BQ - 1 < kw0) continue;  // every query before every key
+        if (kWin && i0 > kw0 + 31 + W - 1) continue;  // every query past every key's window
         int soff = (u % NST) * SB;
         asm volatile("" : "+s"(soff));
         const uint8_t* sb = smem + soff;
-        const bool mk = kCaus && i0 < kw0 + 31;
+        const bool mk = (kCaus && i0 < kw0 + 31) || (kWin && i0 + BQ - 1 > kw0 + W - 1);
         half(sb, 0, i0 + 4 * g, mk);
         half(sb, 1, i0 + 32 + 4 * g, mk);
     }

@@ -158,6 +158,21 @@ def test_bwd_sliding_window(cuda_device, dtype, window, is_causal):
     _check_bwd(2, 2, 200, 64, dtype, cuda_device, is_causal=is_causal, window_size=window, seed=window)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 63, 64, 65, 127, 128, 129, 255, 256, 300, 700, 2000])
+def test_bwd_sliding_window_fast_kernels(cuda_device, dtype, window):
+    """Causal windows at D = 64 run the fast dQ and dK/dV kernels' window
+    mode: windows on and beside the 64-row tile, 128-key and 256-row block
+    edges, longer than T, a partial last block; per-head scales and dscale."""
+    _check_bwd(2, 2, 1100, 64, dtype, cuda_device, window_size=window, seed=window + 3, scale=[8.0, -0.7],
+               check_dscale=True)
+
+
+def test_bwd_sliding_window_c5_shape(cuda_device):
+    """C5's shape with a 512-key window, 16 heads covering every block residue."""
+    _check_bwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, window_size=512, heads=[(b, b) for b in range(16)])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_bwd_document_mask(cuda_device, dtype, is_causal):
