@@ -117,7 +117,6 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(!(PUR && DOC), "documents: Born gradients");
     static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
@@ -384,18 +383,29 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
                 const int lim = qrow[qb] - kbase;
+                // Documents: the row's id (read only where the tile is tested).
+                int rd = 0;
+                if constexpr (DOC)
+                    if (dm[qb]) rd = r_doc[128 * qb + 64 * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float w[2];
 #pragma unroll
                     for (int e = 0; e < 2; ++e) {
                         const int r = 2 * j + e;
+                        const int off = 8 * (r >> 2) + (r & 3);
                         const float x = s[qb][r];
                         const float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
                         const float bb = __int_as_float(max(__float_as_int(x), 0));
                         const float f = fmaf(p4g, u * u * u, p2e * bb);
                         float dr_ = f * fmaf(t[qb][r], zinv[qb], nd[qb]);
-                        if (mk[qb] && 8 * (r >> 2) + (r & 3) > lim) dr_ = 0.f;
+                        // A masked pair weighs zero even where its overlap is
+                        // zero (u = relu(-gamma tau) > 0 for tau < 0).
+                        if constexpr (DOC) {
+                            if (dm[qb] && ((kCaus && off > lim) || kdp[nb * 32 + 4 * g + off] != rd)) dr_ = 0.f;
+                        } else {
+                            if (mk[qb] && off > lim) dr_ = 0.f;
+                        }
                         w[e] = dr_;
                     }
                     pk[qb][j] = E::pack(w[0], w[1]);
@@ -668,12 +678,11 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 // relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
 // workspace read, so they add nothing.
 template <class E, int DP, int MODE, bool PUR = false, bool DOC = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && DOC) ? 2 : 3, (PUR && DOC) ? 2 : 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(!(PUR && DOC), "documents: Born gradients");
     static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
@@ -864,7 +873,13 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const float x = s[r];
                         float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
                         float bb = __int_as_float(max(__float_as_int(x), 0));
-                        if (mk && 8 * (r >> 2) + (r & 3) + lim < 0) u = bb = 0.f;
+                        const int off = 8 * (r >> 2) + (r & 3);
+                        if constexpr (DOC) {
+                            const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
+                            if (xm && ((kCaus && off + lim < 0) || qd[nb * 32 + 4 * g + off] != kdoc)) u = bb = 0.f;
+                        } else {
+                            if (mk && off + lim < 0) u = bb = 0.f;
+                        }
                         const float u2_ = u * u;
                         const float dpz = dp[r] * z4[k + e];
                         const float a = u2_ * u * dpz;

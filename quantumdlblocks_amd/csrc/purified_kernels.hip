@@ -30,15 +30,16 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
 // bf16, D = 64, dense or causal: the bf16-MFMA dQ kernel (which also writes
 // -delta and 1/Z) before the dK/dV kernel (which writes the dgamma / dtau
 // partials), then the fixed-order reduction.
-template <int MODE>
+template <int MODE, bool DOC = false>
 static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     const unsigned BH = (unsigned)(a.B * a.H);
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true>), dim3((unsigned)((a.T + 255) / 256) * BH),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC>),
+                       dim3((unsigned)((a.T + 255) / 256) * BH), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 64);
-    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<BF16, 64, MODE, true>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<BF16, 64, MODE, true, DOC>), dim3((unsigned)nwg), dim3(256), 0, s,
+                       a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
     hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
@@ -49,6 +50,12 @@ template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
+    // bf16, D = 64, document ids without a window: the same kernels' document
+    // variants (the forward stays on the fp32-MFMA kernel; its fp32 output and
+    // Z are what the backward reads either way).
+    if (std::is_same<IN, BF16>::value && a.D == 64 && a.window == 0 && a.doc != nullptr &&
+        ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31))
+        return a.is_causal ? purified_bwd_fast<kCausal, true>(a, s) : purified_bwd_fast<kDense, true>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);
         case 64: return launch_purified_bwd<IN, 64>(a, s);
