@@ -34,10 +34,16 @@
 
 namespace qdl {
 
-template <class E, int DP>
+// PUR: purified-Born weights (flash_born.py:696-811) as in the fast forward:
+// p = relu(gamma (r - tau))^4 + eps_base relu(r)^2 in fp32, each weight split
+// into two bf16 terms for the P V contraction, Z summed in fp32, the output
+// in fp32.  A masked pair (or a key past T) weighs zero even where its
+// overlap is zero, so the masks zero the weights, not the overlaps.
+template <class E, int DP, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_fwd16_doc_kernel(FwdArgs p) {
+void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = 256;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -82,8 +88,15 @@ void born_fwd16_doc_kernel(FwdArgs p) {
     const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
     const int32_t* __restrict__ docb = p.doc + (size_t)b * T;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
+    float pg = 0.f, pgt = 0.f, pse = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        pse = sqrtf(p.eps_base);
+    }
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
@@ -314,7 +327,9 @@ void born_fwd16_doc_kernel(FwdArgs p) {
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) s[qb] = E::mfma(ops[ks], qr[qb][ks], s[qb]);
     };
-    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8]) __attribute__((always_inline)) {
+    constexpr int PW = PUR ? 8 : 1;  // packed low parts of the purified weights
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[NQB][8], const uint32_t (&pl)[NQB][PW])
+        __attribute__((always_inline)) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -323,7 +338,55 @@ void born_fwd16_doc_kernel(FwdArgs p) {
                 for (int qb = 0; qb < NQB; ++qb) {
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
                     oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
+                    if constexpr (PUR) {
+                        const u32x4 bl = {pl[qb][4 * hh % PW], pl[qb][(4 * hh + 1) % PW], pl[qb][(4 * hh + 2) % PW],
+                                          pl[qb][(4 * hh + 3) % PW]};
+                        oacc[db][qb] = E::mfma(ops[hh][db], bl, oacc[db][qb]);
+                    }
                 }
+    };
+    // Purified weights of one 32-key half (keys key0h + 4 g + 8 (r / 4) +
+    // r % 4), the masked ones zeroed: per element where the column block is
+    // tested (mm: causal bound, or T - 1 without causality, and the key id;
+    // a tile of one document tests only the bound, all of it when the lane's
+    // row is in another document), per lane (ll: rows outside the tile's one
+    // document), or not at all.  Z in fp32, each weight split hi + lo.
+    auto elementwise_pur = [&](f32x16 (&s)[NQB], uint32_t (&pk)[NQB][8], uint32_t (&pl)[NQB][PW], int key0h,
+                               const int32_t* kd, bool mm0, bool mm1, bool ll0, bool ll1, bool vv0, bool vv1,
+                               bool single) __attribute__((always_inline)) {
+        const bool mm[NQB] = {mm0, mm1}, ll[NQB] = {ll0, ll1}, vv[NQB] = {vv0, vv1};
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            int lim = (causal ? qrow[qb] : T - 1) - (key0h + 4 * g);
+            if (single && !vv[qb]) lim = -1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float w[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int r = 2 * j + e;
+                    const int off = 8 * (r >> 2) + (r & 3);
+                    const float x = s[qb][r];
+                    const float t = fmaf(x, pg, pgt);
+                    const float u = __int_as_float(max(__float_as_int(t), 0));
+                    const float bq = __int_as_float(max(__float_as_int(x * pse), 0));
+                    const float u2 = u * u;
+                    float pw = fmaf(u2, u2, bq * bq);
+                    bool masked = false;
+                    if (mm[qb]) {
+                        masked = off > lim;
+                        if (!single) masked = masked || kd[4 * g + off] != qdoc[qb];
+                    } else if (ll[qb]) {
+                        masked = !vv[qb];
+                    }
+                    w[e] = masked ? 0.f : pw;
+                }
+                zacc[qb][0] += w[0] + w[1];
+                const uint32_t hi = E::pack(w[0], w[1]);
+                pk[qb][j] = hi;
+                pl[qb][j % PW] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+            }
+        }
     };
     // The fast kernel's four phases (see born_fwd_fast.h), MFMA-only phases at
     // raised wave priority.  One instantiation for every tile (a second one in
@@ -334,6 +397,43 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         f32x16 s0[NQB], s1[NQB];
         uint32_t pk0[NQB][8], pk1[NQB][8];
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
+        if constexpr (PUR) {
+            // Purified: masks applied to the weights; PV issues twice the
+            // MFMAs (hi and lo parts); V of keys 32-63 is read at the start
+            // of the last phase (keeps the tile within the register budget).
+            uint32_t pl0[NQB][PW], pl1[NQB][PW];
+            __builtin_amdgcn_s_setprio(1);
+            read_k(kop1, kb, 1);
+            qk_op(kop, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            read_v(vop0, vb, 0);
+            qk_op(kop1, s1);
+            elementwise_pur(s0, pk0, pl0, key0, kd, m0, m1, l0, l1, v0, v1, single);
+#pragma unroll
+            for (int i = 0; i < KS * NQB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 40, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            pv_op(vop0, pk0, pl0);
+            elementwise_pur(s1, pk1, pl1, key0 + 32, kd + 32, m0, m1, l0, l1, v0, v1, single);
+#pragma unroll
+            for (int i = 0; i < 4 * DB * NQB; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x002, 20, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+            read_v(vop1, vb, 1);
+            pv_op(vop1, pk1, pl1);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            return;
+        }
+        const uint32_t plx[NQB][PW] = {};  // (Born: no low parts)
         __builtin_amdgcn_s_setprio(1);
         read_k(kop1, kb, 1);
         qk_op(kop, s0);
@@ -360,7 +460,7 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         else if (l1) apply_lane(s1[1], v1);
         __builtin_amdgcn_sched_barrier(0);
         read_v(vop1, vb, 1);
-        pv_op(vop0, pk0);
+        pv_op(vop0, pk0, plx);
         elementwise(s1, pk1);
 #pragma unroll
         for (int i = 0; i < 2 * DB * NQB; ++i) {
@@ -370,7 +470,7 @@ void born_fwd16_doc_kernel(FwdArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        pv_op(vop1, pk1);
+        pv_op(vop1, pk1, plx);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -407,18 +507,43 @@ void born_fwd16_doc_kernel(FwdArgs p) {
             // per-lane select clears the other rows' columns.
             const int rel = ti - t0;  // t0 is INT_MAX without causality
             const bool mixed = td == INT_MIN;
-            const bool m0 = rel >= 0 || mixed;
-            const bool m1 = rel >= 2 || mixed;
+            // Purified: a tile holding keys past T is tested per element (the
+            // zero rows of those keys still weigh relu(-gamma tau)).
+            const bool tail = PUR && (ti + 1) * BN > T;
+            const bool m0 = rel >= 0 || mixed || tail;
+            const bool m1 = rel >= 2 || mixed || tail;
             tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td, !mixed);
         }
         __syncthreads();  // the list and the ring are reused by the next chunk
     }
 
+    float* __restrict__ Zp = p.z + (size_t)bh * T;
+    if constexpr (PUR) {
+        // Purified: O = acc / (Z + eps) in fp32, stored from the accumulators.
+        float* __restrict__ O32 = p.o + base;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float zl = zacc[qb][0] + zacc[qb][1];
+            const float zd = zl + __shfl_xor(zl, 32) + p.eps;
+            const int qi = R + 128 * qb + lrow;
+            if (qi < T) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x16& o = oacc[db][qb];
+                        const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
+                        __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                    }
+                if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
+            }
+        }
+        return;
+    }
     // Epilogue: normalise, stage this wave's rows in the idle ring (row r at
     // smem + 128 r, chunks XOR-swizzled by r & 7), read them back 16 bytes
     // per lane and store 8 whole rows per instruction (non-temporal).
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
-    float* __restrict__ Zp = p.z + (size_t)bh * T;
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
     // (The lane index goes through an empty asm so these addresses are formed
@@ -461,6 +586,13 @@ template <class E, int DP>
 hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
     hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// Purified-Born forward with document ids (bf16, D = 64, no window).
+inline hipError_t launch_purified_fwd_doc(const PurArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

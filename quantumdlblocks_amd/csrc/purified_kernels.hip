@@ -2,6 +2,7 @@
 // (32, 64, 128, 256; the host zero-pads D to a multiple of 8 and the kernels
 // bound-check columns past D).
 #include "born_bwd_fast.h"
+#include "born_fwd_doc.h"
 #include "purified.h"
 
 namespace qdl {
@@ -15,11 +16,18 @@ inline bool purified_fast_ok(const PurArgs& a) {
     return a.D == 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
+inline bool purified_doc_fast_ok(const PurArgs& a) {
+    return a.D == 64 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+}
+
 template <class IN>
 static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
+    // bf16, D = 64, document ids without a window: the document kernel's
+    // purified mode.
+    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) return launch_purified_fwd_doc(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);
@@ -51,10 +59,8 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
     // bf16, D = 64, document ids without a window: the same kernels' document
-    // variants (the forward stays on the fp32-MFMA kernel; its fp32 output and
-    // Z are what the backward reads either way).
-    if (std::is_same<IN, BF16>::value && a.D == 64 && a.window == 0 && a.doc != nullptr &&
-        ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31))
+    // variants.
+    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal, true>(a, s) : purified_bwd_fast<kDense, true>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);

@@ -169,7 +169,7 @@ FAST_CASES = [
 ]
 
 
-def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None):
+def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None, window=0):
     from quantumdlblocks_amd import _native
 
     lib = _native.load()
@@ -181,7 +181,7 @@ def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None):
     rc = lib.qdl_flash_purified_born_fwd(
         _native.DTYPE_BF16, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), z.data_ptr(),
         sc.data_ptr(), sc.numel(), ta.data_ptr(), ta.numel(), float(eps_base),
-        doc.data_ptr() if doc is not None else None, int(causal), 0, float(eps),
+        doc.data_ptr() if doc is not None else None, int(causal), int(window), float(eps),
         torch.cuda.current_stream(q.device).cuda_stream)
     _native.check(rc, "qdl_flash_purified_born_fwd")
     torch.cuda.synchronize()
@@ -294,12 +294,13 @@ def test_purified_fast_backward_full_size(cuda_device):
         assert abs(got - gen) <= 5e-3 * abs(gen) + 1e-6, (i, got, gen)
 
 
-def test_purified_fast_backward_documents_c4_shape(cuda_device):
-    """C4's shape and documents (p4b): the document variants of the bf16-MFMA
-    backward kernels, on two heads against the oracle document by document
-    (a masked pair contributes nothing, so each causal document is exact on
-    its own), and on all heads (gradients, dgamma, dtau) against the
-    fp32-MFMA kernels reached through a window longer than T."""
+def test_purified_fast_documents_c4_shape(cuda_device):
+    """C4's shape and documents (p4b): the document kernel's purified forward
+    and the document variants of the bf16-MFMA backward kernels, on two heads
+    against the oracle document by document (a masked pair contributes
+    nothing, so each causal document is exact on its own), and on all heads
+    (output, gradients, dgamma, dtau) against the fp32-MFMA kernels reached
+    through a window longer than T."""
     from util import doc_spans
 
     B, H, T = 4, 16, 8192
@@ -311,9 +312,21 @@ def test_purified_fast_backward_documents_c4_shape(cuda_device):
     ta = torch.tensor(-0.03, device=cuda_device)  # tau < 0: masked pairs must be zeroed explicitly
     fast = _run(q, k, v, do, sc, ta, is_causal=True, doc_ids=doc_t)
     generic = _run(q, k, v, do, sc, ta, is_causal=True, doc_ids=doc_t, window_size=T + 1)
+    # The forward (the document kernel's purified mode), through the C ABI's
+    # fp32 output: fp32 accumulation of split weights, held to 1e-4 against
+    # the fp32-MFMA kernel and the oracle (the autograd entry's output is
+    # rounded to bf16, which alone moves it by up to 2^-9).
+    o32, z32 = _pur_fwd_abi(q, k, v, 8.0, -0.03, 0.05, True, 1e-8, doc=doc_t)
+    o32g, z32g = _pur_fwd_abi(q, k, v, 8.0, -0.03, 0.05, True, 1e-8, doc=doc_t, window=T + 1)
+    eo = rel_err(f64(o32), f64(o32g))
+    print(f"p4b out: rel {eo:.3e} vs the fp32-MFMA kernel", flush=True)
+    assert eo <= 1e-4, eo
+    assert np.max(np.abs(f64(z32) - f64(z32g)) / f64(z32g)) <= 1e-4
     for b, h in ((0, 3), (3, 14)):
         for a, e in doc_spans(docs[b])[:6]:
             sl = (slice(b, b + 1), slice(h, h + 1), slice(a, e))
+            o_ref, _ = orc.purified_forward(f64(q[sl]), f64(k[sl]), f64(v[sl]), 8.0, -0.03, 0.05, True, 1e-8)
+            assert rel_err(f64(o32[sl]), o_ref) <= 1e-4, (b, h, a, e)
             ref = orc.purified_backward(f64(q[sl]), f64(k[sl]), f64(v[sl]), 8.0, -0.03, f64(do[sl]))
             mag = orc.purified_backward_magnitudes(f64(q[sl]), f64(k[sl]), f64(v[sl]), 8.0, -0.03, f64(do[sl]))
             for i, name in enumerate(("dq", "dk", "dv")):
