@@ -360,19 +360,22 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // at all; kdp: this stage's key document ids.
     bool dm[NQB] = {false, false};
     const int32_t* kdp = kd_lds;
-    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const bool (&mk)[NQB])
+    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const bool (&mk)[NQB], auto skip0)
         __attribute__((always_inline)) {
+        // skip0: column block 0 sees none of the tile (diagonal tiles 2 and
+        // 3 under causality): its MFMAs and elementwise pass are left out.
+        constexpr int Q0 = decltype(skip0)::value ? 1 : 0;
         f32x16 s[NQB], t[NQB];
         uint32_t pk[NQB][8];
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16(), t[qb] = zero16();
+        for (int qb = Q0; qb < NQB; ++qb) s[qb] = zero16(), t[qb] = zero16();
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const u32x4 ko = k_row(kb, nb, ks);
             const u32x4 vo = v_row(vb, nb, ks);
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
+            for (int qb = Q0; qb < NQB; ++qb) {
                 s[qb] = E::mfma(ko, qr[qb][ks], s[qb]);
                 t[qb] = E::mfma(vo, dr[qb][ks], t[qb]);
             }
@@ -381,7 +384,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         __builtin_amdgcn_s_setprio(0);
         if constexpr (PUR) {
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
+            for (int qb = Q0; qb < NQB; ++qb) {
                 const int lim = qrow[qb] - kbase;
                 // Documents: the row's id (read only where the tile is tested).
                 int rd = 0;
@@ -413,7 +416,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             }
         } else {
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
+        for (int qb = Q0; qb < NQB; ++qb) {
             if constexpr (DOC) {
                 // Key kbase + 8 (r / 4) + r % 4 of register r is masked past
                 // the lane's row (causal) or in another document.
@@ -456,7 +459,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             for (int db = 0; db < DB; ++db) {
                 const u32x4 a = k_tr(kb, nb, hh, db);
 #pragma unroll
-                for (int qb = 0; qb < NQB; ++qb) {
+                for (int qb = Q0; qb < NQB; ++qb) {
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
                     acc[db][qb] = E::mfma(a, bq, acc[db][qb]);
                 }
@@ -464,11 +467,13 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
-    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, const bool (&mk)[NQB])
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, const bool (&mk)[NQB], auto skip0)
         __attribute__((always_inline)) {
-        half(kb, vb, 0, key0 + 4 * g, mk);
-        half(kb, vb, 1, key0 + 32 + 4 * g, mk);
+        half(kb, vb, 0, key0 + 4 * g, mk, skip0);
+        half(kb, vb, 1, key0 + 32 + 4 * g, mk, skip0);
     };
+    using NoSkip = std::integral_constant<bool, false>;
+    using Skip0 = std::integral_constant<bool, true>;
 
     // Pipeline: tiles 0 and 1 issued up front (tile 1 after the stationary
     // loads have landed, so the compiler's wait for them does not also wait
@@ -541,7 +546,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 const bool mk[NQB] = {ti >= t0, ti >= t0 + 2};
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) dm[qb] = mk[qb] || !(one && qone[qb] && td == qsd[qb]);
-                tile(kb, vb, ti * BN, mk);
+                tile(kb, vb, ti * BN, mk, NoSkip{});
             }
             __syncthreads();  // the list and the ring are reused by the next chunk
         }
@@ -566,12 +571,15 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         const uint8_t* kb = k_lds + soff;
         const uint8_t* vb = v_lds + soff;
         // Diagonal tiles t0, t0+1: block 0 cut by the mask, block 1 fully
-        // visible; t0+2, t0+3: block 0 fully masked (computed, then zeroed
-        // by the mask), block 1 cut.  Window: both blocks tested on the
-        // window's edge tiles and on all four diagonal tiles.
+        // visible; t0+2, t0+3: block 0 sees none of the tile (left out),
+        // block 1 cut.  Window: both blocks tested on the window's edge
+        // tiles and on the diagonal tiles.
         const bool medge = kWin && (u < te || u >= t0);
         const bool mk[NQB] = {u >= t0 || medge, u >= t0 + 2 || medge};
-        tile(kb, vb, (tb + u) * BN, mk);
+        if (kCaus && u >= t0 + 2)
+            tile(kb, vb, (tb + u) * BN, mk, Skip0{});
+        else
+            tile(kb, vb, (tb + u) * BN, mk, NoSkip{});
     }
     }
 
