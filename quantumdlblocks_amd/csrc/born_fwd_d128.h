@@ -1,0 +1,457 @@
+// Flash-Born forward specialised for head dim D == 128 (no padding): dense,
+// causal, or causal with a sliding window.
+//
+// Same arithmetic and load pipeline as the D == 64 kernel (born_fwd_fast.h):
+// LDS-DMA K/V ring of three 64-key stages, one barrier per tile, two 256-row
+// query blocks per workgroup under causality (mb and nmb-1-mb), Q block and
+// output rows staged through LDS.  What changes with the wider rows:
+//   * Registers: a wave holds one 32-row MFMA column block (its Q operands
+//     are 32 VGPRs and its O accumulators 64 at D == 128; two column blocks
+//     would not fit two waves per SIMD).  The workgroup is 8 waves (two per
+//     SIMD) over a 256-row block, wave w owning rows 32w .. 32w+31, so every
+//     K/V tile in LDS feeds 256 query rows.
+//   * LDS: 3 x (16 + 16) KiB ring + 64 KiB Q block = 160 KiB, one workgroup
+//     per CU.  Rows are 256 bytes, so every row starts on bank 0 and the
+//     16-byte chunks are XOR-swizzled per row:
+//       K, Q: chunk' = chunk ^ (row & 15)       -> 16 consecutive rows of one
+//             chunk (a ds_read_b128 quarter-wave) hit 16 distinct chunks;
+//       V:    chunk' = chunk ^ 4 (row & 3)      -> the 4 rows x 64 bytes of a
+//             ds_read_b64_tr_b16 half-wave hit 4 distinct 64-byte groups.
+//   * Masks per wave: with contiguous rows, each wave's tiles split into
+//     runs that are fully visible to all of its rows (no mask), cut by its
+//     diagonal or its window edge (both bounds tested per element), or
+//     invisible to it (no work; it only joins the barrier).  Under causality
+//     the four diagonal tiles of a block then cost the busier SIMD 2, 2, 1
+//     and 1 wave-tiles instead of 2 each.
+// Per tile the wave runs the D == 64 kernel's four fenced phases: QK(keys
+// 0-31); QK(keys 32-63) | elementwise(0-31); PV(0-31) | elementwise(32-63);
+// PV(32-63), each phase's LDS operands read one phase ahead.
+#pragma once
+
+#include <type_traits>
+
+#include "born_common.h"
+#include "born_fwd_fast.h"
+
+namespace qdl {
+
+struct FwdD128Cfg {
+    static constexpr int DP = 128;
+    static constexpr int NW = 8;    // waves per workgroup, two per SIMD
+    static constexpr int BM = 256;  // query rows per block, 32 per wave
+    static constexpr int BN = 64;   // keys per tile
+    static constexpr int NST = 3;   // K/V ring stages
+};
+
+template <class E, int MODE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void born_fwd16_d128_kernel(FwdArgs p) {
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
+    using C = FwdD128Cfg;
+    constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
+    constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
+    constexpr int DB = DP / 32;            // 32-column blocks of O
+    constexpr int RB = DP * 2;             // bytes per row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int QB = BM * RB;            // bytes per Q block
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
+    constexpr int LQW = QB / (1024 * NW);  // 1-KiB loads per wave per Q block
+    static_assert(TB % (1024 * NW) == 0 && QB % (1024 * NW) == 0, "tile split");
+    static_assert(LQW * 1024 == 32 * RB, "each wave's Q loads land on its own 32 rows");
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t k_lds[NST * TB];
+    __shared__ __attribute__((aligned(1024))) uint8_t v_lds[NST * TB];
+    __shared__ __attribute__((aligned(1024))) uint8_t q_lds[QB];
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int nmb = fast_fwd_nmb(T, BM);
+    const int bid = blockIdx.x;
+    // Paired launch: item 0 is query block nmb-1-pr, item 1 block pr when
+    // that is a different block.  Unpaired: one block per workgroup, the
+    // longest key ranges first.
+    const bool paired = gridDim.x < (unsigned)(nmb * BH);
+    const int bh = bid % BH;
+    const int pr = bid / BH;
+    const int h = bh % p.H;
+    const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
+    const int nitems = (mb_a != mb_b) ? 2 : 1;
+    const int W = kWin ? p.window : 0;
+    // First key tile of a block (its first row's window start) and its tile count.
+    auto item_t0 = [&](int mb) -> int { return kWin ? max(0, mb * BM - W + 1) / BN : 0; };
+    auto item_tiles = [&](int mb) -> int {
+        const int kv_hi = kCaus ? min(T, (mb + 1) * BM) : T;
+        return (kv_hi + BN - 1) / BN - item_t0(mb);
+    };
+    const int nt_a = item_tiles(mb_a);
+    const int ntot = nt_a + (nitems == 2 ? item_tiles(mb_b) : 0);
+    const int tb_a = item_t0(mb_a), tb_b = item_t0(mb_b);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+    const int c = lane & 31, g = lane >> 5;
+
+    const size_t base = (size_t)bh * T * DP;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+
+    // Tile u of the workgroup's sequence -> stage st: wave-instruction i
+    // writes LDS slots (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    auto issue = [&](int u, int st) __attribute__((always_inline)) {
+        const int key0 = (u < nt_a ? tb_a + u : tb_b + (u - nt_a)) * BN;
+        uint8_t* kb = k_lds + st * TB;
+        uint8_t* vb = v_lds + st * TB;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (key0 + row) * RB;
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 15)) << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 2)) << 4));
+        }
+    };
+    auto issue_q = [&](int mb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < LQW; ++i) {
+            const int slot = (wave * LQW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            dma_load16<true>(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
+                             (mb * BM + row) * RB + ((pc ^ (row & 15)) << 4));
+        }
+    };
+
+    int qrow = 0;  // this lane's query row (current item)
+    u32x4 qr[KS];
+    f32x16 oacc[DB];
+    float zacc[2];
+
+    // Per-lane V offsets (transposed read): row kc + 4 g + (lane & 15) / 4
+    // (+8), column db*32 + 16 ((lane >> 4) & 1) + 4 (lane & 3).
+    const int vrow_l = 4 * g + ((lane & 15) >> 2);
+    const int vcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+    // K (A operand of S^T = K Q^T): key row nb*32 + c, chunk 2 ks + g.
+    auto k_operand = [&](const uint8_t* kb, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        const int pc = (2 * ks + g) ^ (row & 15);
+        return *reinterpret_cast<const u32x4*>(kb + row * RB + pc * 16);
+    };
+    auto v_operand = [&](const uint8_t* vb, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + vrow_l;
+        const int col = db * 32 + vcol_l;
+        const int pc = (col >> 3) ^ ((row & 3) << 2);  // rows r and r + 8 share the swizzle
+        const uint8_t* b0 = vb + row * RB + pc * 16 + (col & 7) * 2;
+        const uint8_t* b1 = b0 + 8 * RB;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b1));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    // Tile forms, passed as integral constants: kFull (no mask) or kMasked
+    // (key past the row, or before its window, zeroed per element).
+    constexpr int kFull = 1, kMasked = 2;
+    using Full = std::integral_constant<int, kFull>;
+    using Masked = std::integral_constant<int, kMasked>;
+
+    // Elementwise pass over one 32-key half of S^T (lane: query c, keys
+    // kbase + 8 (r / 4) + r % 4): p' = relu(x|x|) packed, z += p'.  Masked
+    // keys (past the row, or before its window) are zeroed first.
+    auto elementwise = [&](f32x16& s, uint32_t (&pk)[8], auto m, int kbase) __attribute__((always_inline)) {
+        if constexpr (decltype(m)::value == kMasked) {
+            const int lim = qrow - kbase;
+            const int wlo = kWin ? lim - W + 1 : 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float x0 = s[2 * j], x1 = s[2 * j + 1];
+            if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+            const uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
+            zacc[j & 1] = E::sum2(u, zacc[j & 1]);
+            pk[j] = u;
+        }
+    };
+
+    u32x4 kop[KS];
+    auto read_k = [&](u32x4 (&dst)[KS], const uint8_t* kb, int nb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) dst[ks] = k_operand(kb, nb, ks);
+    };
+    auto read_v = [&](u32x4 (&dst)[2][DB], const uint8_t* vb, int nb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) dst[hh][db] = v_operand(vb, nb, hh, db);
+    };
+    auto qk_op = [&](const u32x4 (&ops)[KS], f32x16& s) __attribute__((always_inline)) {
+        s = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s = E::mfma(ops[ks], qr[ks], s);
+    };
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
+                oacc[db] = E::mfma(ops[hh][db], bq, oacc[db]);
+            }
+    };
+    // One tile, four fenced phases (kop: K of keys 0-31, read after the
+    // tile's barrier):
+    //   1: S0 = QK(kop)                           reads K(keys 32-63) -> kop1
+    //   2: S1 = QK(kop1) | elementwise(S0) -> P0  reads V(keys 0-31)  -> vop0
+    //   3: O += PV(vop0, P0) | elementwise(S1)    reads V(keys 32-63) -> vop1
+    //   4: O += PV(vop1, P1)
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, auto m) __attribute__((always_inline)) {
+        f32x16 s0, s1;
+        uint32_t pk0[8], pk1[8];
+        u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
+        // 1
+        __builtin_amdgcn_s_setprio(1);
+        read_k(kop1, kb, 1);
+        qk_op(kop, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        // 2
+        __builtin_amdgcn_s_setprio(0);
+        read_v(vop0, vb, 0);
+        qk_op(kop1, s1);
+        elementwise(s0, pk0, m, key0 + 4 * g);
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 3
+        read_v(vop1, vb, 1);
+        pv_op(vop0, pk0);
+        elementwise(s1, pk1, m, key0 + 32 + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 2 * DB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 4
+        __builtin_amdgcn_s_setprio(1);
+        pv_op(vop1, pk1);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // This wave's 32 rows of the Q block in LDS -> B operands of S^T, the
+    // sign of the scale folded in; the asm pins them in registers.
+    auto load_q = [&]() __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int row = 32 * wave + (ln & 31);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int pc = (2 * ks + (ln >> 5)) ^ (row & 15);
+            qr[ks] = *reinterpret_cast<const u32x4*>(q_lds + row * RB + pc * 16);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            qr[ks] ^= flip;
+            asm volatile("" : "+v"(qr[ks]));
+        }
+    };
+
+    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    float* __restrict__ Zp = p.z + (size_t)bh * T;
+    const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
+    const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+
+    // Normalise and store a finished item's rows: pack() turns the
+    // accumulators into 16-bit pairs, put_lds() writes them into this wave's
+    // own rows of the Q block (their Q is in registers by then), flush()
+    // reads them back 16 bytes per lane (4 whole rows per store instruction)
+    // and stores them and the row sums, non-temporal.
+    u32x2 opk[DB][4];
+    float ztot = 0.f;
+    auto pack = [&]() __attribute__((always_inline)) {
+        const float zl = zacc[0] + zacc[1];
+        ztot = zl + __shfl_xor(zl, 32);
+        const float rcp = 1.0f / (ztot + eps_s);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x16& o = oacc[db];
+                opk[db][j][0] = E::pack(o[4 * j] * rcp, o[4 * j + 1] * rcp);
+                opk[db][j][1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
+            }
+    };
+    auto put_lds = [&]() __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int row = 32 * wave + (ln & 31);
+        const int gg = ln >> 5;
+        uint8_t* rb = q_lds + row * RB;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int chunk = 4 * db + j;  // columns 32 db + 8 j + 4 gg .. +3
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * gg) = opk[db][j];
+            }
+    };
+    auto flush = [&](int mb) __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int qz = mb * BM + 32 * wave + (ln & 31);
+        if ((ln >> 5) == 0 && qz < T) __builtin_nontemporal_store(s2 * ztot + p.eps, Zp + qz);
+        const int chunk = ln & 15;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = 32 * wave + 4 * i + (ln >> 4);
+            const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 15)) << 4));
+            const int qi = mb * BM + row;
+            if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
+        }
+    };
+    auto start_item = [&](int mb) __attribute__((always_inline)) {
+        qrow = mb * BM + 32 * wave + c;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+        zacc[0] = zacc[1] = 0.f;
+    };
+
+    // Load pipeline (as in the D == 64 kernel): Q of item 0 and tiles 0, 1
+    // up front; at the top of step u, after the barrier, tile u+2 (and at
+    // u == uq the second item's Q block, ahead of tile uq+2).  Each wave waits
+    // for its share of tile u (everything issued before tile u+1), then the
+    // barrier makes the whole tile visible and frees tile u-1's stage.  The
+    // first item's rows are staged in LDS in the second item's first step and
+    // stored at the top of its second step; the next step drains them.
+    constexpr int kTileLoads = 2 * LPW, kQLoads = LQW;
+    const bool early_q = (nitems == 2);
+    const int uq = max(1, nt_a - 4);
+    auto top = [&](int u) __attribute__((always_inline)) {
+        const bool stores_out = (nitems == 2) && (u == nt_a + 2);
+        const int after = stores_out ? 0 : ((u == uq + 1 && early_q) ? kQLoads : 0) + (u + 1 < ntot ? kTileLoads : 0);
+        if (after >= kQLoads + kTileLoads)
+            wait_vmcnt<kQLoads + kTileLoads>();
+        else if (after >= kTileLoads)
+            wait_vmcnt<kTileLoads>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        if (u == uq && early_q) issue_q(mb_b);
+        if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
+        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
+    };
+
+    issue_q(mb_a);
+    issue(0, 0);
+    if (ntot > 1) issue(1, 1);
+
+    int u = 0;
+    for (int it = 0; it < nitems; ++it) {
+        const int mb = it ? mb_b : mb_a;
+        const int nt = it ? ntot - nt_a : nt_a;
+        const int tb = it ? tb_b : tb_a;
+        top(u);
+        if (it > 0) {
+            pack();
+            load_q();  // before the previous item's rows overwrite this wave's Q rows
+            put_lds();
+        } else {
+            load_q();
+        }
+        start_item(mb);
+        // This wave's rows are rw .. rw + 31: the keys it may see are
+        // [kv0, kv1] and the keys all of its rows see [kf0, kf1].  Its tiles
+        // (counted from the item's first, tb) fall into five runs: [0, ta)
+        // nothing visible, [ta, tf) masked, [tf, tg) full, [tg, tv) masked,
+        // [tv, nt) nothing visible (causal: tg is the tile holding the
+        // wave's diagonal, tv the one after it).  One loop per run keeps the
+        // masked and full tile bodies out of a common branch (two tile bodies
+        // in one branch exceed the register budget).  The barriers and loads
+        // of every step run in every wave.
+        constexpr int kBig = 1 << 29;
+        const int rw = mb * BM + 32 * wave;
+        const int kv0 = kWin ? max(0, rw - W + 1) : 0;
+        const int kv1 = kCaus ? rw + 31 : kBig;
+        const int kf0 = kWin ? max(0, rw + 32 - W) : 0;
+        const int kf1 = kCaus ? rw : kBig;
+        auto rel = [&](int kt) -> int { return min(max(kt - tb, 0), nt); };
+        const int ta = rel(kv0 / BN);
+        const int tv = max(rel(kv1 / BN + 1), ta);
+        const int tf = min(max(rel((kf0 + BN - 1) / BN), ta), tv);
+        const int tg = min(max(rel((kf1 + 1) / BN), tf), tv);
+        auto stage = [&](int uu, const uint8_t*& kb, const uint8_t*& vb) __attribute__((always_inline)) {
+            int soff = (uu % NST) * TB;  // opaque: operand addresses formed per tile
+            asm volatile("" : "+s"(soff));
+            kb = k_lds + soff;
+            vb = v_lds + soff;
+        };
+        int t = 0;
+        bool at_top = true;  // top(u) already done for the current step
+        auto idle_run = [&](int tend) __attribute__((always_inline)) {
+            for (; t < tend; ++t, ++u) {
+                if (!at_top) top(u);
+                at_top = false;
+            }
+        };
+        auto masked_run = [&](int tend) __attribute__((always_inline)) {
+            for (; t < tend; ++t, ++u) {
+                if (!at_top) top(u);
+                at_top = false;
+                const uint8_t *kb, *vb;
+                stage(u, kb, vb);
+                read_k(kop, kb, 0);
+                tile(kb, vb, (tb + t) * BN, Masked{});
+            }
+        };
+        idle_run(ta);
+        masked_run(tf);
+        for (; t < tg; ++t, ++u) {
+            if (!at_top) top(u);
+            at_top = false;
+            const uint8_t *kb, *vb;
+            stage(u, kb, vb);
+            read_k(kop, kb, 0);
+            tile(kb, vb, (tb + t) * BN, Full{});
+        }
+        masked_run(tv);
+        idle_run(nt);
+    }
+    if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
+    pack();
+    put_lds();
+    flush(nitems == 2 ? mb_b : mb_a);
+}
+
+template <class E, int MODE>
+hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
+    using C = FwdD128Cfg;
+    // One workgroup per CU (160 KiB of LDS): pair query blocks unless that
+    // leaves fewer workgroups than CUs (256).  Windows: never paired.
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
+    const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
+    const dim3 grid((npair < 256u || MODE == kWindow) ? nsingle : npair);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace qdl

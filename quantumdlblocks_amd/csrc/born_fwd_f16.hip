@@ -1,5 +1,6 @@
 // Forward kernel instantiations for f16 inputs.
 #include "born_fwd.h"
+#include "born_fwd_d128.h"
 #include "born_fwd_doc.h"
 #include "born_fwd_fast.h"
 #include "born_launch.h"
@@ -17,6 +18,11 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
     // Causal sliding window (no documents): the fast kernel's window mode.
     if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32)
         return launch_fwd16_fast<F16, 64, kWindow>(a, s);
+    // D == 128: dense, causal or causal sliding window (no documents).
+    if (a.D == 128 && a.doc == nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+        if (a.window > 0) return launch_fwd16_d128<F16, kWindow>(a, s);
+        return a.is_causal ? launch_fwd16_d128<F16, kCausal>(a, s) : launch_fwd16_d128<F16, kDense>(a, s);
+    }
     if (a.D == 64 && mode != kGeneral && addr32)
         return mode == kCausal ? launch_fwd16_fast<F16, 64, kCausal>(a, s) : launch_fwd16_fast<F16, 64, kDense>(a, s);
 #define QDL_MODE_BODY(M) return launch_fwd16<F16, DPV, M>(a, s);

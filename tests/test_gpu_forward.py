@@ -143,6 +143,46 @@ def test_fwd_sliding_window_fast_kernel(cuda_device, dtype, window):
     _check_fwd(2, 2, 1100, 64, dtype, cuda_device, window_size=window, seed=window + 7)
 
 
+@pytest.mark.parametrize("T", [1, 37, 64, 255, 256, 300, 513, 777, 1100])
+@pytest.mark.parametrize("is_causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale", [0.09, -0.5])
+def test_fwd_d128_kernel(cuda_device, T, is_causal, dtype, scale):
+    """D = 128 without documents runs its own kernel (8 waves over 256-row
+    query blocks, 32 rows per wave): ragged lengths, one to five blocks,
+    both scale signs (unpaired launch: too few heads to pair)."""
+    _check_fwd(1, 2, T, 128, dtype, cuda_device, scale=scale, is_causal=is_causal, seed=T + 1)
+
+
+@pytest.mark.parametrize("T", [700, 1100])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_d128_block_pairs(cuda_device, T, is_causal):
+    """Enough heads for the paired launch (blocks mb and nmb-1-mb in one
+    workgroup, the odd block count's middle block alone); per-head scales of
+    both signs; heads covering every residue of the pair index."""
+    B, H = 4, 32
+    sc = np.linspace(-0.2, 0.2, H).astype(np.float32)
+    sc[H // 2] = 0.13
+    sel = [(b, (7 * b + 5 * j) % H) for b in range(B) for j in range(3)]
+    _check_fwd(B, H, T, 128, torch.bfloat16, cuda_device, scale=sc, is_causal=is_causal, std=0.5, seed=T,
+               heads=sel)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 31, 32, 33, 64, 100, 255, 256, 257, 512, 900])
+def test_fwd_d128_sliding_window(cuda_device, dtype, window):
+    """Causal windows at D = 128: windows starting inside, on and beside a
+    wave's 32 rows, a 64-key tile and a 256-row block, longer than T."""
+    _check_fwd(2, 2, 1100, 128, dtype, cuda_device, window_size=window, scale=0.09, seed=window + 11)
+
+
+def test_fwd_d128_config_d3(cuda_device):
+    """d3: bf16 B16 H8 T1024 D128 causal (the C3 work at head dim 128),
+    N(0, 1/128); 16 heads covering every batch row and workgroup residue."""
+    sel = [(b, (3 * b + 1) % 8) for b in range(16)]
+    _check_fwd(16, 8, 1024, 128, torch.bfloat16, cuda_device, scale=1.0, std=128 ** -0.5, heads=sel)
+
+
 def test_fwd_sliding_window_c3_shape(cuda_device):
     """C3's shape with a 256-key window, 16 heads covering every block
     residue of the launch."""
