@@ -25,6 +25,7 @@
 // both layouts, V row-major) -> dscale reduction.
 #pragma once
 
+#include "born_bwd_d128.h"
 #include "born_bwd_fast.h"
 #include "born_common.h"
 #include "born_stage.h"
@@ -1120,6 +1121,14 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
             hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),
                                0, st, a, nwg);
             return hipGetLastError();
+        }
+    }
+    // D == 128, dense, causal or causal sliding window (no documents): the
+    // D == 128 kernels (born_bwd_d128.h).
+    if constexpr (DP == 128) {
+        if (a.D == 128 && a.doc == nullptr && addr32) {
+            if (MODE == kGeneral && a.window > 0 && a.is_causal) return launch_bwd16_d128<E, kWindow>(a, st);
+            if (MODE == kDense || MODE == kCausal) return launch_bwd16_d128<E, MODE == kCausal ? kCausal : kDense>(a, st);
         }
     }
     if constexpr (DP == 64 && MODE != kGeneral) {

@@ -1,0 +1,613 @@
+// Flash-Born backward specialised for head dim D == 128 (no padding): dense,
+// causal, or causal with a sliding window; Born weights, no document ids.
+// Same arithmetic as the D == 64 kernels (born_bwd_fast.h), the same two
+// launches (dQ first: it also forms delta and fills the workspace), with the
+// register split the wider rows need:
+//   * dQ (queries stationary): 8 waves over a 256-row query block, wave w
+//     owning rows 32w .. 32w+31 (one MFMA column block: its Q and dO operands
+//     are 64 VGPRs and its dQ accumulators 64).
+//   * dK/dV (keys stationary): 8 waves over a 256-key block, wave w owning
+//     keys 32w .. 32w+31 (K and V operands 64 VGPRs, dK and dV accumulators
+//     128).
+//   * Tiles of 64 rows (K, V for dQ; Q, dO plus -delta and 1/Z for dK/dV) go
+//     global -> LDS with buffer_load ... lds through a ring of three stages,
+//     one workgroup per CU.  Rows are 256 bytes, so every row starts on bank
+//     0; 16-byte chunk c of row r sits at chunk c ^ swz256(r), conflict-free
+//     both for the row reads (ds_read_b128 quarter-waves: 16 consecutive
+//     rows of one chunk) and the transposed reads (ds_read_b64_tr_b16
+//     half-waves: rows r0 .. r0+3, r0 % 4 == 0, of an aligned group of four
+//     chunks).
+//   * Each wave's tiles split into runs as in the D == 128 forward: tiles
+//     none of its pairs see (no work, only the barrier), tiles its diagonal
+//     or window edge cuts (masked per element), and tiles all of its pairs
+//     see (no mask), each run in a loop of its own.
+#pragma once
+
+#include "born_bwd_fast.h"
+
+namespace qdl {
+
+__device__ __forceinline__ int swz256(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+struct BwdD128Cfg {
+    static constexpr int DP = 128;
+    static constexpr int NW = 8;    // waves per workgroup, two per SIMD
+    static constexpr int BM = 256;  // dQ: query rows per block (32 per wave)
+    static constexpr int NWK = 4;   // dK/dV: waves per workgroup, one per SIMD
+    static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
+};
+
+// Runs of a wave's tiles t = 0 .. n-1 (tile t holds rows lo + 64 t ..
+// lo + 64 t + 63 of the other side): [0, ta) invisible, [ta, tf) masked,
+// [tf, tg) full, [tg, tv) masked, [tv, n) invisible, for a wave that may see
+// rows [v0, v1] and sees all of them in full in rows [f0, f1].
+struct WaveRuns {
+    int ta, tf, tg, tv;
+    __device__ __forceinline__ WaveRuns(int lo, int n, int v0, int v1, int f0, int f1) {
+        auto rel = [&](int t) { return min(max(t, 0), n); };
+        ta = rel(v0 >= lo ? (v0 - lo) / 64 : 0);
+        tv = max(rel(v1 >= lo ? (v1 - lo) / 64 + 1 : 0), ta);
+        tf = min(max(rel(f0 > lo ? (f0 - lo + 63) / 64 : 0), ta), tv);
+        tg = min(max(rel(f1 + 1 >= lo ? (f1 - lo + 1) / 64 : 0), tf), tv);
+    }
+};
+
+constexpr int kD128Big = 1 << 29;
+
+template <class E, int MODE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void born_bwd16_dq_d128_kernel(BwdArgs p) {
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
+    constexpr int KS = DP / 16, DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per tile row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
+    constexpr int kTileLoads = 2 * LPW;
+    static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB && BM == 32 * NW, "tile split / staging");
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
+
+    // The K/V ring during the tile loop, the output staging afterwards.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+    __shared__ float s_dz[NW];
+    uint8_t* const k_lds = smem;
+    uint8_t* const v_lds = smem + NST * TB;
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    // Under causality the longest key ranges go first.
+    const int mb = kCaus ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int h = bh % p.H;
+    const int R = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+    const int qrow = R + 32 * wave + c;  // this lane's query row
+
+    const size_t base = (size_t)bh * T * DP;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    // Stationary operands (sign-flipped Q, dO: B operands of S^T and T^T),
+    // delta_i = dO_i . O_i from the stored O (each lane holds half a row, the
+    // other half is in lane ^ 32), and the workspace rows -delta, 1/Z,
+    // delta/Z for the dK/dV kernel and the dscale reduction.
+    u32x4 qr[KS], dr[KS];
+    float zinv, nd;
+    {
+        const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
+        const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
+        const uint16_t* __restrict__ Og = reinterpret_cast<const uint16_t*>(p.o) + base;
+        const bool ok = qrow < T;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+            if (ok) {
+                x = ldg16(Qg + (size_t)qrow * DP + (2 * ks + g) * 8);
+                y = ldg16(dOg + (size_t)qrow * DP + (2 * ks + g) * 8);
+            }
+            qr[ks] = x ^ flip;
+            dr[ks] = y;
+        }
+        float dl = 0.f;
+        if (ok) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4 o = ldg16(Og + (size_t)qrow * DP + (2 * ks + g) * 8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    dl += E::lo(o[j]) * E::lo(dr[ks][j]) + E::hi(o[j]) * E::hi(dr[ks][j]);
+            }
+        }
+        dl += __shfl_xor(dl, 32);
+        const size_t row = (size_t)bh * T + qrow;
+        const float zr = ok ? p.z[row] : 1.f;
+        zinv = ok ? 1.0f / zr : 0.f;
+        nd = ok ? -(dl / zr) : 0.f;
+        if (ok && g == 0) {
+            p.ndelta[row] = -dl;
+            p.zinv[row] = zinv;
+            p.delta_z[row] = dl / zr;
+        }
+    }
+    // This workgroup's part of dscale = (2/s) eps sum delta / Z (closed form):
+    // its rows' sum in a fixed order (lanes, then waves), one double.
+    {
+        float dz = (g == 0) ? -nd : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) dz += __shfl_xor(dz, off);
+        if (lane == 0) s_dz[wave] = dz;
+        __syncthreads();
+        if (tid == 0) {
+            double acc = 0.0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) acc += (double)s_dz[w];
+            p.dscale_part[bid] = acc;
+        }
+    }
+
+    // Key tiles tb .. tb+ntiles-1 (tb: the window's first key tile, else 0).
+    const int W = kWin ? p.window : 0;
+    const int tb = kWin ? max(0, R - W + 1) / BN : 0;
+    const int ntiles = (kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN) - tb;
+    // This wave's rows rw .. rw + 31 see keys [rw - W + 1, rw + 31] (causal,
+    // window) and all of them see keys [rw + 32 - W, rw].
+    const int rw = R + 32 * wave;
+    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kD128Big,
+                        kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kD128Big);
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+
+    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
+    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        const int st = u % NST;
+        const int key0 = (tb + u) * BN;
+        uint8_t* kb = k_lds + st * TB;
+        uint8_t* vb = v_lds + st * TB;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (key0 + row) * RB + ((pc ^ swz256(row)) << 4);
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
+        }
+    };
+
+    // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, T^T);
+    // K^T: keys nb * 32 + hh * 16 + 4 g + (lane & 15) / 4 (+8), d columns
+    // db * 32 + 16 ((lane >> 4) & 1) + 4 (lane & 3): the key order of the
+    // accumulator layout of U.
+    const int trow_l = 4 * g + ((lane & 15) >> 2);
+    const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto row_rd = [&](const uint8_t* tb_, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        return *reinterpret_cast<const u32x4*>(tb_ + row * RB + (((2 * ks + g) ^ swz256(row)) << 4));
+    };
+    auto tr_rd = [&](const uint8_t* tb_, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + trow_l;
+        const int col = db * 32 + tcol_l;
+        const uint8_t* b0 = tb_ + row * RB + (((col >> 3) ^ swz256(row)) << 4) + (col & 7) * 2;
+        const uint8_t* b1 = tb_ + (row + 8) * RB + (((col >> 3) ^ swz256(row + 8)) << 4) + (col & 7) * 2;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b1));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = zero16();
+
+    constexpr int kFull = 1, kMasked = 2;
+    using Full = std::integral_constant<int, kFull>;
+    using Masked = std::integral_constant<int, kMasked>;
+    // One 32-key half nb of a tile:
+    //   S^T = K Q^T, T^T = V dO^T      (A = K, V rows; B = Q^T, dO^T)
+    //   U = relu(S^T) (T^T / Z - delta / Z), masked keys zeroed
+    //   dQ^T += K^T U                    (A = K^T, B = U)
+    // MFMAs at raised wave priority, the elementwise pass at normal priority.
+    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, auto m) __attribute__((always_inline)) {
+        f32x16 s = zero16(), t = zero16();
+        uint32_t pk[8];
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            s = E::mfma(row_rd(kb, nb, ks), qr[ks], s);
+            t = E::mfma(row_rd(vb, nb, ks), dr[ks], t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        if constexpr (decltype(m)::value == kMasked) {
+            // Key kbase + 8 (r / 4) + r % 4 of register r: masked past the
+            // lane's row, and (window) before its first key.
+            const int lim = qrow - kbase;
+            const int wlo = kWin ? lim - W + 1 : 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float x0 = s[2 * j], x1 = s[2 * j + 1];
+            if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+            const float a0 = __int_as_float(max(__float_as_int(x0), 0));
+            const float a1 = __int_as_float(max(__float_as_int(x1), 0));
+            pk[j] = E::pack(a0 * fmaf(t[2 * j], zinv, nd), a1 * fmaf(t[2 * j + 1], zinv, nd));
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
+                acc[db] = E::mfma(tr_rd(kb, nb, hh, db), bq, acc[db]);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Pipeline: tiles 0 and 1 issued up front (tile 1 after the stationary
+    // loads have landed), tile u+2 right after the barrier that starts step
+    // u; at that barrier each wave has waited for its share of tile u.
+    if (ntiles > 0) issue(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]), "+v"(dr[ks]));
+    asm volatile("" : "+v"(zinv), "+v"(nd));
+    if (ntiles > 1) issue(1);
+    int u = 0;
+    auto step = [&]() __attribute__((always_inline)) {
+        if (u + 1 < ntiles)
+            wait_vmcnt<kTileLoads>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        if (u + 2 < ntiles) issue(u + 2);
+    };
+    auto run = [&](int tend, auto m) __attribute__((always_inline)) {
+        for (; u < tend; ++u) {
+            step();
+            int soff = (u % NST) * TB;
+            asm volatile("" : "+s"(soff));
+            const uint8_t* kb = k_lds + soff;
+            const uint8_t* vb = v_lds + soff;
+            const int key0 = (tb + u) * BN;
+            half(kb, vb, 0, key0 + 4 * g, m);
+            half(kb, vb, 1, key0 + 32 + 4 * g, m);
+        }
+    };
+    for (; u < runs.ta; ++u) step();
+    run(runs.tf, Masked{});
+    run(runs.tg, Full{});
+    run(runs.tv, Masked{});
+    for (; u < ntiles; ++u) step();
+
+    // Epilogue: scale, pack, stage this wave's rows in the idle ring (row r
+    // at smem + RB r, chunks XOR-swizzled by r & 15), read them back 16
+    // bytes per lane and store 4 whole rows per instruction.
+    __syncthreads();  // every wave is done with the ring
+    uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
+    const float f = 2.f * sc * fabsf(sc) / sq_pre;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    {
+        const int row = 32 * wave + (ln & 31);
+        uint8_t* rb = smem + row * RB;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                u32x2 w;
+                w[0] = E::pack(acc[db][4 * j] * f, acc[db][4 * j + 1] * f);
+                w[1] = E::pack(acc[db][4 * j + 2] * f, acc[db][4 * j + 3] * f);
+                const int chunk = 4 * db + j;
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * (ln >> 5)) = w;
+            }
+    }
+    const int chunk = ln & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 32 * wave + 4 * i + (ln >> 4);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 15)) << 4));
+        const int q = R + row;
+        if (q < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * DP + chunk * 8));
+    }
+}
+
+template <class E, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
+    constexpr int KS = DP / 16, DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per tile row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BQ * RB;            // bytes per Q or dO tile
+    constexpr int SB = 2 * TB + 2 * BQ * 4;  // bytes per stage: Q, dO, -delta, 1/Z
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
+    static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && BK * RB <= NST * SB && BK == 32 * NW,
+                  "tile split / staging");
+    constexpr bool kWin = (MODE == kWindow);
+    constexpr bool kCaus = (MODE == kCausal) || kWin;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    // Key blocks in ascending order: under causality the first sees the most queries.
+    const int kblk = bid / BH;
+    const int h = bh % p.H;
+    const int K0 = kblk * BK;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+    const int kw0 = K0 + 32 * wave;  // first key of this wave
+    const int key = kw0 + c;         // this lane's key
+
+    const size_t base = (size_t)bh * T * DP;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+
+    // Stationary operands: sign-flipped K and V rows of this lane's key.
+    u32x4 kr[KS], vr[KS];
+    {
+        const uint16_t* __restrict__ Kg = reinterpret_cast<const uint16_t*>(p.k) + base;
+        const uint16_t* __restrict__ Vg = reinterpret_cast<const uint16_t*>(p.v) + base;
+        const bool ok = key < T;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+            if (ok) {
+                x = ldg16(Kg + (size_t)key * DP + (2 * ks + g) * 8);
+                y = ldg16(Vg + (size_t)key * DP + (2 * ks + g) * 8);
+            }
+            kr[ks] = x ^ flip;
+            vr[ks] = y;
+        }
+    }
+
+    // Query tiles q_lo + BQ u up to q_hi (window: the last query that sees
+    // the block's last key).
+    const int W = kWin ? p.window : 0;
+    const int q_lo = kCaus ? K0 : 0;
+    const int q_hi = kWin ? (int)min((int64_t)T, (int64_t)K0 + BK - 1 + W) : T;
+    const int ntiles = (q_hi - q_lo + BQ - 1) / BQ;
+    // This wave's keys kw0 .. kw0 + 31 are seen by queries [kw0, kw0 + 31 +
+    // W - 1] (causal, window), all of them by queries [kw0 + 31, kw0 + W - 1].
+    const WaveRuns runs(q_lo, ntiles, kCaus ? kw0 : 0, kWin ? kw0 + 31 + W - 1 : kD128Big, kCaus ? kw0 + 31 : 0,
+                        kWin ? kw0 + W - 1 : kD128Big);
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
+    const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
+    const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
+    const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
+
+    // Tile u -> stage u % NST.  Waves 0 and 1 also bring the tile's -delta
+    // and 1/Z (lanes 0-15, 16 bytes each): one more load per tile.
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        uint8_t* sb = smem + (u % NST) * SB;
+        const int i0 = q_lo + u * BQ;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int off = (i0 + row) * RB + ((pc ^ swz256(row)) << 4);
+            dma_load16(rq, lds_addr(sb + (wave * LPW + i) * 1024), off);
+            dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
+        }
+        if (lane < 16) {
+            const uint32_t la = lds_addr(sb + 2 * TB + wave * BQ * 4);
+            if (wave == 0)
+                dma_load16(rdl, la, (i0 + 4 * lane) * 4);
+            else if (wave == 1)
+                dma_load16(rzi, la, (i0 + 4 * lane) * 4);
+        }
+    };
+
+    const int trow_l = 4 * g + ((lane & 15) >> 2);
+    const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // Row reads (A of S and dPz): query row nb * 32 + c, chunk 2 ks + g.
+    auto row_rd = [&](const uint8_t* tb_, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + c;
+        return *reinterpret_cast<const u32x4*>(tb_ + row * RB + (((2 * ks + g) ^ swz256(row)) << 4));
+    };
+    // Transposed reads (A of dV^T, dK^T): queries nb * 32 + hh * 16 + 4 g +
+    // (lane & 15) / 4 (+8), d columns db * 32 + 16 ((lane >> 4) & 1) + 4 (lane & 3).
+    auto tr_rd = [&](const uint8_t* tb_, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int row = nb * 32 + hh * 16 + trow_l;
+        const int col = db * 32 + tcol_l;
+        const uint8_t* b0 = tb_ + row * RB + (((col >> 3) ^ swz256(row)) << 4) + (col & 7) * 2;
+        const uint8_t* b1 = tb_ + (row + 8) * RB + (((col >> 3) ^ swz256(row + 8)) << 4) + (col & 7) * 2;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b1));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    };
+
+    f32x16 acc_v[DB], acc_k[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
+
+    constexpr int kFull = 1, kMasked = 2;
+    using Full = std::integral_constant<int, kFull>;
+    using Masked = std::integral_constant<int, kMasked>;
+    // One 32-query half nb of a tile (queries qbase + 8 (r / 4) + r % 4 for
+    // register r; one key per lane):
+    //   S   = Q K'^T                  (A = Q rows)
+    //   dPz = dO V^T - delta          (A = dO rows, accumulator initialised
+    //                                  with -delta from LDS)
+    //   t = relu(S) / Z_i, W = t relu(S), U = t dPz   (masked queries zeroed)
+    //   dV^T += dO^T W,  dK^T += Q^T U   (A = dO^T, Q^T transposed reads)
+    auto half = [&](const uint8_t* sb, int nb, int qbase, auto m) __attribute__((always_inline)) {
+        const uint8_t* qt = sb;
+        const uint8_t* dt = sb + TB;
+        const float* dl = reinterpret_cast<const float*>(sb + 2 * TB);
+        const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
+        f32x16 s = zero16(), dp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dp[4 * i + k] = d4[k];
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            s = E::mfma(row_rd(qt, nb, ks), kr[ks], s);
+            dp = E::mfma(row_rd(dt, nb, ks), vr[ks], dp);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        if constexpr (decltype(m)::value == kMasked) {
+            // Register r (query qbase + off) is masked before the lane's key
+            // (off + lim < 0) and (window) past its window (off + lim >= W).
+            const int lim = qbase - key;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off + lim < 0 || (kWin && off + lim >= W)) s[r] = 0.f;
+            }
+        }
+        uint32_t w2[8], u2[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+            for (int k = 0; k < 4; k += 2) {
+                const int r = 4 * i + k;
+                float x0 = s[r], x1 = s[r + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                const float a0 = __int_as_float(max(__float_as_int(x0), 0));
+                const float a1 = __int_as_float(max(__float_as_int(x1), 0));
+                const float t0 = a0 * z4[k], t1 = a1 * z4[k + 1];
+                w2[r >> 1] = E::pack(t0 * a0, t1 * a1);
+                u2[r >> 1] = E::pack(t0 * dp[r], t1 * dp[r + 1]);
+            }
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const u32x4 bw = {w2[4 * hh], w2[4 * hh + 1], w2[4 * hh + 2], w2[4 * hh + 3]};
+            const u32x4 bu = {u2[4 * hh], u2[4 * hh + 1], u2[4 * hh + 2], u2[4 * hh + 3]};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                acc_v[db] = E::mfma(tr_rd(dt, nb, hh, db), bw, acc_v[db]);
+                acc_k[db] = E::mfma(tr_rd(qt, nb, hh, db), bu, acc_k[db]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Pipeline as in the dQ kernel.
+    if (ntiles > 0) issue(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
+    if (ntiles > 1) issue(1);
+    int u = 0;
+    auto step = [&]() __attribute__((always_inline)) {
+        if (u + 1 < ntiles) {
+            if (wave < 2)
+                wait_vmcnt<2 * LPW + 1>();
+            else
+                wait_vmcnt<2 * LPW>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (u + 2 < ntiles) issue(u + 2);
+    };
+    auto run = [&](int tend, auto m) __attribute__((always_inline)) {
+        for (; u < tend; ++u) {
+            step();
+            int soff = (u % NST) * SB;
+            asm volatile("" : "+s"(soff));
+            const uint8_t* sb = smem + soff;
+            const int i0 = q_lo + u * BQ;
+            half(sb, 0, i0 + 4 * g, m);
+            half(sb, 1, i0 + 32 + 4 * g, m);
+        }
+    };
+    for (; u < runs.ta; ++u) step();
+    run(runs.tf, Masked{});
+    run(runs.tg, Full{});
+    run(runs.tv, Masked{});
+    for (; u < ntiles; ++u) step();
+
+    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre),
+    // packed and staged, one output at a time, in this wave's own 32 rows of
+    // the idle ring (row r at smem + RB r, chunks XOR-swizzled by r & 15),
+    // then read back 16 bytes per lane and stored 4 whole rows per
+    // instruction.
+    __syncthreads();  // every wave is done with the ring
+    const float fk = 2.f * sc * fabsf(sc) / sq_pre;
+    const float fv = (sc / sq_pre) * (sc / sq_pre);
+    uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
+    uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        const int row = 32 * wave + (ln & 31);
+        uint8_t* rb = smem + row * RB;
+        const float f = which ? fv : fk;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x16& o = which ? acc_v[db] : acc_k[db];
+                u32x2 w;
+                w[0] = E::pack(o[4 * j] * f, o[4 * j + 1] * f);
+                w[1] = E::pack(o[4 * j + 2] * f, o[4 * j + 3] * f);
+                const int chunk = 4 * db + j;
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * (ln >> 5)) = w;
+            }
+        const int chunk = ln & 15;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r2 = 32 * wave + 4 * i + (ln >> 4);
+            const u32x4 x = *reinterpret_cast<const u32x4*>(smem + r2 * RB + ((chunk ^ (r2 & 15)) << 4));
+            const int kk = K0 + r2;
+            if (kk < T)
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * DP + chunk * 8));
+        }
+    }
+}
+
+// The D == 128 backward: dQ (and the workspace), dK/dV, then dscale from the
+// dQ kernel's per-workgroup sums.
+template <class E, int MODE>
+hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
+    const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64), 0, st, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
+                       st, a, (int)(nq * BH));
+    return hipGetLastError();
+}
+
+}  // namespace qdl

@@ -168,6 +168,32 @@ def test_bwd_sliding_window_fast_kernels(cuda_device, dtype, window):
                check_dscale=True)
 
 
+@pytest.mark.parametrize("T", [1, 37, 64, 200, 256, 300, 513, 1100])
+@pytest.mark.parametrize("is_causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_bwd_d128_kernels(cuda_device, T, is_causal, dtype):
+    """D = 128 without documents runs its own dQ (8 waves over 256 query
+    rows) and dK/dV (4 waves over 128 keys) kernels: ragged lengths, partial
+    blocks and tiles, per-head scales of both signs, dscale."""
+    _check_bwd(1, 2, T, 128, dtype, cuda_device, is_causal=is_causal, scale=[0.09, -0.2], std=0.7, seed=T + 5,
+               check_dscale=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 31, 32, 33, 64, 100, 127, 128, 129, 256, 700, 2000])
+def test_bwd_d128_sliding_window(cuda_device, dtype, window):
+    """Causal windows at D = 128: windows on and beside a wave's 32 rows or
+    keys, the 64-row tiles, the 128-key and 256-row blocks, longer than T."""
+    _check_bwd(2, 2, 1100, 128, dtype, cuda_device, window_size=window, seed=window + 13, scale=[0.09, -0.3],
+               std=0.7, check_dscale=True)
+
+
+def test_bwd_d128_config_d5(cuda_device):
+    """d5: bf16 B16 H8 T2048 D128 forward + backward (the C5 work at head dim
+    128), N(0,1); 16 heads covering every batch row and block residue."""
+    _check_bwd(16, 8, 2048, 128, torch.bfloat16, cuda_device, scale=0.09, heads=[(b, (3 * b + 1) % 8) for b in range(16)])
+
+
 def test_bwd_sliding_window_c5_shape(cuda_device):
     """C5's shape with a 512-key window, 16 heads covering every block residue."""
     _check_bwd(16, 16, 2048, 64, torch.bfloat16, cuda_device, window_size=512, heads=[(b, b) for b in range(16)])
