@@ -423,22 +423,48 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
         }
     };
 
-    const int trow_l = 4 * g + ((lane & 15) >> 2);
-    const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    // Row reads (A of S and dPz): query row nb * 32 + c, chunk 2 ks + g.
-    auto row_rd = [&](const uint8_t* tb_, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
-        const int row = nb * 32 + c;
-        return *reinterpret_cast<const u32x4*>(tb_ + row * RB + (((2 * ks + g) ^ swz256(row)) << 4));
+    // Operand reads.  Rows (A of S and dPz): query row nb * 32 + c, chunk
+    // 2 ks + g.  Transposed (A of dV^T, dK^T): queries nb * 32 + hh * 16 +
+    // 4 g + (lane & 15) / 4 (+8), d columns db * 32 + 16 ((lane >> 4) & 1) +
+    // 4 (lane & 3).  swz256 is unchanged by the row steps of 8, 16 and 32, so
+    // a lane's byte offsets within a stage are the 8 + 8 below plus
+    // constants: each tile adds its stage base to them once and every read
+    // takes its constant part as the instruction's immediate offset.
+    int roff[KS], toff[DB][2];
+    {
+        const int trow_l = 4 * g + ((lane & 15) >> 2);
+        const int tcol_l = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) roff[ks] = c * RB + (((2 * ks + g) ^ swz256(c)) << 4);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int row = trow_l + 8 * e;
+                const int col = db * 32 + tcol_l;
+                toff[db][e] = row * RB + (((col >> 3) ^ swz256(row)) << 4) + (col & 7) * 2;
+            }
+    }
+    struct Bases {
+        const uint8_t* r[KS];
+        const uint8_t* t[DB][2];
     };
-    // Transposed reads (A of dV^T, dK^T): queries nb * 32 + hh * 16 + 4 g +
-    // (lane & 15) / 4 (+8), d columns db * 32 + 16 ((lane >> 4) & 1) + 4 (lane & 3).
-    auto tr_rd = [&](const uint8_t* tb_, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
-        const int row = nb * 32 + hh * 16 + trow_l;
-        const int col = db * 32 + tcol_l;
-        const uint8_t* b0 = tb_ + row * RB + (((col >> 3) ^ swz256(row)) << 4) + (col & 7) * 2;
-        const uint8_t* b1 = tb_ + (row + 8) * RB + (((col >> 3) ^ swz256(row + 8)) << 4) + (col & 7) * 2;
-        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b0));
-        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b1));
+    auto bases_of = [&](const uint8_t* sb) __attribute__((always_inline)) -> Bases {
+        Bases b;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) b.r[ks] = sb + roff[ks];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) b.t[db][0] = sb + toff[db][0], b.t[db][1] = sb + toff[db][1];
+        return b;
+    };
+    // which: 0 = Q, 1 = dO (the second tile of the stage).
+    auto row_rd = [&](const Bases& b, int which, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
+        return *reinterpret_cast<const u32x4*>(b.r[ks] + which * TB + nb * 32 * RB);
+    };
+    auto tr_rd = [&](const Bases& b, int which, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
+        const int k = which * TB + (nb * 32 + hh * 16) * RB;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(b.t[db][0] + k));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(b.t[db][1] + k));
         const u32x4 a = {x[0], x[1], y[0], y[1]};
         return a;
     };
@@ -450,33 +476,51 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
     constexpr int kFull = 1, kMasked = 2;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
-    // One 32-query half nb of a tile (queries qbase + 8 (r / 4) + r % 4 for
-    // register r; one key per lane):
+    // Per 32-query half nb of a tile (queries i0 + nb * 32 + 8 (r / 4) +
+    // 4 g + r % 4 for register r; one key per lane):
     //   S   = Q K'^T                  (A = Q rows)
     //   dPz = dO V^T - delta          (A = dO rows, accumulator initialised
     //                                  with -delta from LDS)
     //   t = relu(S) / Z_i, W = t relu(S), U = t dPz   (masked queries zeroed)
     //   dV^T += dO^T W,  dK^T += Q^T U   (A = dO^T, Q^T transposed reads)
-    auto half = [&](const uint8_t* sb, int nb, int qbase, auto m) __attribute__((always_inline)) {
-        const uint8_t* qt = sb;
-        const uint8_t* dt = sb + TB;
+    // One wave per SIMD leaves nothing to hide a wave's LDS latency behind
+    // but its own work, so a tile runs as four fenced phases with every
+    // phase's operands read one phase earlier (the first phase's right after
+    // the tile's barrier):
+    //   1: S, dPz of half 0                         reads rows of half 1
+    //   2: S, dPz of half 1 | elementwise(half 0)   reads Q^T, dO^T of half 0
+    //   3: dV, dK += half 0 | elementwise(half 1)   reads Q^T, dO^T of half 1
+    //   4: dV, dK += half 1
+    auto read_rows = [&](const Bases& b, int which, int nb, u32x4 (&dst)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) dst[ks] = row_rd(b, which, nb, ks);
+    };
+    auto read_tr = [&](const Bases& b, int which, int nb, u32x4 (&dst)[2][DB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) dst[hh][db] = tr_rd(b, which, nb, hh, db);
+    };
+    auto sdp = [&](const u32x4 (&aq)[KS], const u32x4 (&ad)[KS], f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+        s = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            s = E::mfma(aq[ks], kr[ks], s);
+            dp = E::mfma(ad[ks], vr[ks], dp);
+        }
+    };
+    auto init_dp = [&](const uint8_t* sb, int nb, f32x16& dp) __attribute__((always_inline)) {
         const float* dl = reinterpret_cast<const float*>(sb + 2 * TB);
-        const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
-        f32x16 s = zero16(), dp;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl + nb * 32 + 8 * i + 4 * g);
 #pragma unroll
             for (int k = 0; k < 4; ++k) dp[4 * i + k] = d4[k];
         }
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            s = E::mfma(row_rd(qt, nb, ks), kr[ks], s);
-            dp = E::mfma(row_rd(dt, nb, ks), vr[ks], dp);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(0);
+    };
+    auto elementwise = [&](const uint8_t* sb, int nb, int qbase, f32x16& s, const f32x16& dp, uint32_t (&w2)[8],
+                           uint32_t (&u2)[8], auto m) __attribute__((always_inline)) {
+        const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
         if constexpr (decltype(m)::value == kMasked) {
             // Register r (query qbase + off) is masked before the lane's key
             // (off + lim < 0) and (window) past its window (off + lim >= W).
@@ -487,7 +531,6 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
                 if (off + lim < 0 || (kWin && off + lim >= W)) s[r] = 0.f;
             }
         }
-        uint32_t w2[8], u2[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
@@ -503,25 +546,74 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
                 u2[r >> 1] = E::pack(t0 * dp[r], t1 * dp[r + 1]);
             }
         }
-        __builtin_amdgcn_s_setprio(1);
+    };
+    auto dvdk = [&](const u32x4 (&td)[2][DB], const u32x4 (&tq)[2][DB], const uint32_t (&w2)[8],
+                    const uint32_t (&u2)[8]) __attribute__((always_inline)) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const u32x4 bw = {w2[4 * hh], w2[4 * hh + 1], w2[4 * hh + 2], w2[4 * hh + 3]};
             const u32x4 bu = {u2[4 * hh], u2[4 * hh + 1], u2[4 * hh + 2], u2[4 * hh + 3]};
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                acc_v[db] = E::mfma(tr_rd(dt, nb, hh, db), bw, acc_v[db]);
-                acc_k[db] = E::mfma(tr_rd(qt, nb, hh, db), bu, acc_k[db]);
+                acc_v[db] = E::mfma(td[hh][db], bw, acc_v[db]);
+                acc_k[db] = E::mfma(tq[hh][db], bu, acc_k[db]);
             }
         }
+    };
+    auto tile = [&](const uint8_t* sb, int i0, auto m) __attribute__((always_inline)) {
+        const Bases bs = bases_of(sb);
+        u32x4 rq0[KS], rd0[KS], rq1[KS], rd1[KS];
+        u32x4 tq0[2][DB], td0[2][DB], tq1[2][DB], td1[2][DB];
+        f32x16 s0, dp0, s1, dp1;
+        uint32_t w0[8], u0[8], w1[8], u1[8];
+        read_rows(bs, 0, 0, rq0);
+        read_rows(bs, 1, 0, rd0);
+        init_dp(sb, 0, dp0);
+        init_dp(sb, 1, dp1);
+        // 1
+        __builtin_amdgcn_s_setprio(1);
+        read_rows(bs, 0, 1, rq1);
+        read_rows(bs, 1, 1, rd1);
+        sdp(rq0, rd0, s0, dp0);
+        __builtin_amdgcn_sched_barrier(0);
+        // 2
+        __builtin_amdgcn_s_setprio(0);
+        read_tr(bs, 0, 0, tq0);
+        read_tr(bs, 1, 0, td0);
+        sdp(rq1, rd1, s1, dp1);
+        elementwise(sb, 0, i0 + 4 * g, s0, dp0, w0, u0, m);
+#pragma unroll
+        for (int i = 0; i < 2 * KS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 3
+        read_tr(bs, 0, 1, tq1);
+        read_tr(bs, 1, 1, td1);
+        dvdk(td0, tq0, w0, u0);
+        elementwise(sb, 1, i0 + 32 + 4 * g, s1, dp1, w1, u1, m);
+#pragma unroll
+        for (int i = 0; i < 4 * DB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 4
+        __builtin_amdgcn_s_setprio(1);
+        dvdk(td1, tq1, w1, u1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // Pipeline as in the dQ kernel.
+    // Pipeline as in the dQ kernel.  The stationary operands are pinned in
+    // AGPRs (MFMA reads its A/B operands from either file), leaving the
+    // VGPRs to the phases' operand buffers.
     if (ntiles > 0) issue(0);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(kr[ks]), "+a"(vr[ks]));
     if (ntiles > 1) issue(1);
     int u = 0;
     auto step = [&]() __attribute__((always_inline)) {
@@ -541,10 +633,7 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
             step();
             int soff = (u % NST) * SB;
             asm volatile("" : "+s"(soff));
-            const uint8_t* sb = smem + soff;
-            const int i0 = q_lo + u * BQ;
-            half(sb, 0, i0 + 4 * g, m);
-            half(sb, 1, i0 + 32 + 4 * g, m);
+            tile(smem + soff, q_lo + u * BQ, m);
         }
     };
     for (; u < runs.ta; ++u) step();
