@@ -37,23 +37,6 @@ struct BwdD128Cfg {
     static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
 };
 
-// Runs of a wave's tiles t = 0 .. n-1 (tile t holds rows lo + 64 t ..
-// lo + 64 t + 63 of the other side): [0, ta) invisible, [ta, tf) masked,
-// [tf, tg) full, [tg, tv) masked, [tv, n) invisible, for a wave that may see
-// rows [v0, v1] and sees all of them in full in rows [f0, f1].
-struct WaveRuns {
-    int ta, tf, tg, tv;
-    __device__ __forceinline__ WaveRuns(int lo, int n, int v0, int v1, int f0, int f1) {
-        auto rel = [&](int t) { return min(max(t, 0), n); };
-        ta = rel(v0 >= lo ? (v0 - lo) / 64 : 0);
-        tv = max(rel(v1 >= lo ? (v1 - lo) / 64 + 1 : 0), ta);
-        tf = min(max(rel(f0 > lo ? (f0 - lo + 63) / 64 : 0), ta), tv);
-        tg = min(max(rel(f1 + 1 >= lo ? (f1 - lo + 1) / 64 : 0), tf), tv);
-    }
-};
-
-constexpr int kD128Big = 1 << 29;
-
 template <class E, int MODE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(BwdArgs p) {
@@ -161,8 +144,8 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
     // This wave's rows rw .. rw + 31 see keys [rw - W + 1, rw + 31] (causal,
     // window) and all of them see keys [rw + 32 - W, rw].
     const int rw = R + 32 * wave;
-    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kD128Big,
-                        kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kD128Big);
+    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kRunsBig,
+                        kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kRunsBig);
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
@@ -392,8 +375,8 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
     const int ntiles = (q_hi - q_lo + BQ - 1) / BQ;
     // This wave's keys kw0 .. kw0 + 31 are seen by queries [kw0, kw0 + 31 +
     // W - 1] (causal, window), all of them by queries [kw0 + 31, kw0 + W - 1].
-    const WaveRuns runs(q_lo, ntiles, kCaus ? kw0 : 0, kWin ? kw0 + 31 + W - 1 : kD128Big, kCaus ? kw0 + 31 : 0,
-                        kWin ? kw0 + W - 1 : kD128Big);
+    const WaveRuns runs(q_lo, ntiles, kCaus ? kw0 : 0, kWin ? kw0 + 31 + W - 1 : kRunsBig, kCaus ? kw0 + 31 : 0,
+                        kWin ? kw0 + W - 1 : kRunsBig);
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);

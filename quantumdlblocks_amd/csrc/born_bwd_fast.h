@@ -44,6 +44,23 @@ namespace qdl {
 // belong to one document.
 constexpr int kDocOne = 1 << 30;
 
+// Runs of a wave's tiles t = 0 .. n-1 (tile t holds rows lo + 64 t ..
+// lo + 64 t + 63 of the other side): [0, ta) invisible, [ta, tf) masked,
+// [tf, tg) full, [tg, tv) masked, [tv, n) invisible, for a wave that may see
+// rows [v0, v1] and sees all of them in full in rows [f0, f1].
+struct WaveRuns {
+    int ta, tf, tg, tv;
+    __device__ __forceinline__ WaveRuns(int lo, int n, int v0, int v1, int f0, int f1) {
+        auto rel = [&](int t) { return min(max(t, 0), n); };
+        ta = rel(v0 >= lo ? (v0 - lo) / 64 : 0);
+        tv = max(rel(v1 >= lo ? (v1 - lo) / 64 + 1 : 0), ta);
+        tf = min(max(rel(f0 > lo ? (f0 - lo + 63) / 64 : 0), ta), tv);
+        tg = min(max(rel(f1 + 1 >= lo ? (f1 - lo + 1) / 64 : 0), tf), tv);
+    }
+};
+
+constexpr int kRunsBig = 1 << 29;  // "no bound" for WaveRuns
+
 // Document-id range of rows r0 .. r1-1 of one batch row's ids.
 __device__ __forceinline__ void doc_rows_range(const int32_t* __restrict__ docb, int r0, int r1, int n, bool vec,
                                                int& lo, int& hi) {
@@ -846,7 +863,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     // One 32-query half nb of a tile (rows i0 + nb * 32 + 8 (r / 4) + 4 g +
     // r % 4 for register r).  One instantiation for every tile; the causal
     // mask (key past the query) applies under the uniform flag mk.
-    auto half = [&](const uint8_t* sb, int nb, int qbase, bool mk) __attribute__((always_inline)) {
+    auto half = [&](const uint8_t* sb, int nb, int qbase, auto mk) __attribute__((always_inline)) {
         const uint8_t* qt = sb;
         const uint8_t* dt = sb + TB;
         const float* dl = reinterpret_cast<const float*>(sb + 2 * TB);
@@ -1023,7 +1040,16 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
     if (ntiles > 1) issue(1);
-    for (int u = 0; u < ntiles; ++u) {
+    // This wave's keys kw0 .. kw0 + 31 are seen by queries [kw0, kw0 + 31 +
+    // W - 1] (causal, window), all of them by queries [kw0 + 31, kw0 + W - 1]:
+    // its query tiles split into runs, the masked and the unmasked tile bodies
+    // each in a loop of its own (one body with a runtime mask flag computes
+    // the mask's compares and selects on every tile).
+    static_assert(BQ == 64, "WaveRuns counts 64-row tiles");
+    const WaveRuns runs(q_lo, ntiles, kCaus ? kw0 : 0, kWin ? kw0 + 31 + W - 1 : kRunsBig, kCaus ? kw0 + 31 : 0,
+                        kWin ? kw0 + W - 1 : kRunsBig);
+    int u = 0;
+    auto step = [&]() __attribute__((always_inline)) {
         if (u + 1 < ntiles) {
             if (wave < 2)
                 wait_vmcnt<2 * LPW + 1>();
@@ -1034,17 +1060,23 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         }
         __syncthreads();
         if (u + 2 < ntiles) issue(u + 2);
-        const int i0 = q_lo + u * BQ;
-        // This wave's keys kw0 .. kw0+31 against queries i0 .. i0+63.
-        if (kCaus && i0 + BQ - 1 < kw0) continue;  // every query before every key
-        if (kWin && i0 > kw0 + 31 + W - 1) continue;  // every query past every key's window
-        int soff = (u % NST) * SB;
-        asm volatile("" : "+s"(soff));
-        const uint8_t* sb = smem + soff;
-        const bool mk = (kCaus && i0 < kw0 + 31) || (kWin && i0 + BQ - 1 > kw0 + W - 1);
-        half(sb, 0, i0 + 4 * g, mk);
-        half(sb, 1, i0 + 32 + 4 * g, mk);
-    }
+    };
+    auto run = [&](int tend, auto mk) __attribute__((always_inline)) {
+        for (; u < tend; ++u) {
+            step();
+            int soff = (u % NST) * SB;
+            asm volatile("" : "+s"(soff));
+            const uint8_t* sb = smem + soff;
+            const int i0 = q_lo + u * BQ;
+            half(sb, 0, i0 + 4 * g, mk);
+            half(sb, 1, i0 + 32 + 4 * g, mk);
+        }
+    };
+    for (; u < runs.ta; ++u) step();
+    run(runs.tf, std::true_type{});
+    run(runs.tg, std::false_type{});
+    run(runs.tv, std::true_type{});
+    for (; u < ntiles; ++u) step();
     }
     (void)kTileLoadsW;
 
