@@ -100,6 +100,21 @@ def test_fwd_d64_block_pairs(cuda_device, T, is_causal, dtype, scale):
     _check_fwd(1, 2, T, 64, dtype, cuda_device, scale=scale, is_causal=is_causal, seed=T)
 
 
+@pytest.mark.parametrize("T", [513, 700, 1024, 1100, 1600])
+@pytest.mark.parametrize("is_causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fwd_d64_many_heads(cuda_device, T, is_causal, dtype):
+    """D = 64 with enough heads for the paired launch at scale (two 256-row
+    blocks per workgroup, two workgroups per CU): even and odd block counts,
+    ragged last blocks, per-head scales of both signs; heads covering every
+    residue of the pair index and batch row."""
+    B, H = 2, 160
+    sc = np.linspace(-9.0, 9.0, H).astype(np.float32)
+    sc[H // 2] = 8.0
+    sel = [(b, (37 * b + 11 * j) % H) for b in range(B) for j in range(4)]
+    _check_fwd(B, H, T, 64, dtype, cuda_device, scale=sc, is_causal=is_causal, std=0.125, seed=T, heads=sel)
+
+
 @pytest.mark.parametrize("D, window", [(64, 0), (64, 100), (32, 0)])
 @pytest.mark.parametrize("scale", [0.05, -0.3, 8.0])
 def test_fwd_f16_weight_range(cuda_device, D, window, scale):
