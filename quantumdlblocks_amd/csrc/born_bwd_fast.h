@@ -370,14 +370,16 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // the two workgroups sharing a SIMD overlap one's MFMAs with the other's
     // VALU work.  (Interleaving the column blocks' phases within the wave
     // measured slower.)  relu is an integer max on the float bits (no NaN
-    // canonicalisation).  One instantiation for every tile (a second one
-    // costs more registers than the wave has): the causal mask of column
-    // block qb is applied under the uniform flag mk[qb].
+    // canonicalisation).  The causal mask of column block qb is applied
+    // under mk[qb]: uniform runtime flags on the diagonal and window-edge
+    // tiles (one body for all of them; two bodies under one branch cost more
+    // registers than the wave has), compile-time false on the plain tiles,
+    // whose body has no mask code and runs in a loop of its own.
     // Documents, per tile: column block qb is tested per element (dm) or not
     // at all; kdp: this stage's key document ids.
     bool dm[NQB] = {false, false};
     const int32_t* kdp = kd_lds;
-    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const bool (&mk)[NQB], auto skip0)
+    auto half = [&](const uint8_t* kb, const uint8_t* vb, int nb, int kbase, const auto& mk, auto skip0)
         __attribute__((always_inline)) {
         // skip0: column block 0 sees none of the tile (diagonal tiles 2 and
         // 3 under causality): its MFMAs and elementwise pass are left out.
@@ -484,13 +486,17 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
-    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, const bool (&mk)[NQB], auto skip0)
+    auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, const auto& mk, auto skip0)
         __attribute__((always_inline)) {
         half(kb, vb, 0, key0 + 4 * g, mk, skip0);
         half(kb, vb, 1, key0 + 32 + 4 * g, mk, skip0);
     };
     using NoSkip = std::integral_constant<bool, false>;
     using Skip0 = std::integral_constant<bool, true>;
+    // Mask flags of a plain tile: known false at compile time.
+    struct NoMask {
+        constexpr bool operator[](int) const { return false; }
+    };
 
     // Pipeline: tiles 0 and 1 issued up front (tile 1 after the stationary
     // loads have landed, so the compiler's wait for them does not also wait
@@ -576,7 +582,8 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         asm volatile("" : "+v"(zinv[qb]), "+v"(nd[qb]));
     }
     if (ntiles > 1) issue(1);
-    for (int u = 0; u < ntiles; ++u) {
+    int u = 0;
+    auto step = [&](const uint8_t*& kb, const uint8_t*& vb) __attribute__((always_inline)) {
         if (u + 1 < ntiles)
             wait_vmcnt<kTileLoads>();
         else
@@ -585,14 +592,29 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         if (u + 2 < ntiles) issue(u + 2);
         int soff = (u % NST) * TB;
         asm volatile("" : "+s"(soff));
-        const uint8_t* kb = k_lds + soff;
-        const uint8_t* vb = v_lds + soff;
-        // Diagonal tiles t0, t0+1: block 0 cut by the mask, block 1 fully
-        // visible; t0+2, t0+3: block 0 sees none of the tile (left out),
-        // block 1 cut.  Window: both blocks tested on the window's edge
-        // tiles and on the diagonal tiles.
-        const bool medge = kWin && (u < te || u >= t0);
-        const bool mk[NQB] = {u >= t0 || medge, u >= t0 + 2 || medge};
+        kb = k_lds + soff;
+        vb = v_lds + soff;
+    };
+    // Window: the tiles before te, both blocks tested per element.
+    for (; u < te; ++u) {
+        const uint8_t *kb, *vb;
+        step(kb, vb);
+        const bool mk[NQB] = {true, true};
+        tile(kb, vb, (tb + u) * BN, mk, NoSkip{});
+    }
+    // Plain tiles: no mask.
+    for (; u < t0; ++u) {
+        const uint8_t *kb, *vb;
+        step(kb, vb);
+        tile(kb, vb, (tb + u) * BN, NoMask{}, NoSkip{});
+    }
+    // Diagonal tiles t0, t0+1: block 0 cut by the mask, block 1 fully
+    // visible; t0+2, t0+3: block 0 sees none of the tile (left out), block 1
+    // cut.  Window: both blocks tested on the diagonal tiles.
+    for (; u < ntiles; ++u) {
+        const uint8_t *kb, *vb;
+        step(kb, vb);
+        const bool mk[NQB] = {true, u >= t0 + 2 || kWin};
         if (kCaus && u >= t0 + 2)
             tile(kb, vb, (tb + u) * BN, mk, Skip0{});
         else
