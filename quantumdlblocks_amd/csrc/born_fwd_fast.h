@@ -14,15 +14,13 @@
 //     (32 banks x 4 bytes).  Each lane picks the global chunk that belongs in
 //     its fixed LDS slot.  Rows >= T lie beyond the buffer's num_records and
 //     arrive as zeros.
-//   * A workgroup handles one 256-row query block, or (the paired launch:
-//     dense Born with at least 512 pairs, and the purified and prologue
-//     launches) two blocks of one (batch, head), mb and nmb-1-mb.  Under
-//     causality a pair's key ranges add up to the same length for every
-//     pair, and the second block's Q and first K/V tiles are loaded while
-//     the first block finishes.  Causal Born launches one block per
-//     workgroup, longest key ranges first: the dispatcher then gives each
-//     CU's freed slot the next block, which evens out the two workgroups'
-//     unequal rates better than equal pairs do.
+//   * A workgroup handles one 256-row query block, or (the paired launch,
+//     dense with at least 512 pairs) two blocks of one (batch, head), mb and
+//     nmb-1-mb, the second block's Q and first K/V tiles loaded while the
+//     first block finishes.  Causal launches take one block per workgroup,
+//     longest key ranges first: the dispatcher then gives each CU's freed
+//     slot the next block, which evens out the two co-resident workgroups'
+//     unequal rates better than pairs of equal causal work do.
 //   * K/V tiles of both blocks form one sequence through a ring of three LDS
 //     stages: tile u+2 is issued right after the barrier that starts tile u,
 //     and tile u is waited for only at that barrier, so every load has two
@@ -912,7 +910,7 @@ hipError_t launch_fwd16_fast_prologue(const FwdProArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid(npair < 512u ? nsingle : npair);
+    const dim3 grid((npair < 512u || MODE == kCausal) ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, false, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
@@ -925,7 +923,7 @@ hipError_t launch_purified_fwd_fast(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid(npair < 512u ? nsingle : npair);
+    const dim3 grid((npair < 512u || MODE == kCausal) ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
