@@ -69,7 +69,11 @@ CONFIGS.update({
     "d5": (16, 8, 2048, 128, 1.0, False, None, True),
     "w3": (16, 16, 1024, 64, 0.125, False, None, False),
     "w5": (16, 16, 2048, 64, 1.0, False, None, True),
+    # purified-Born attention at head dim 128 on the same work
+    "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
+    "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
 })
+PURIFIED |= {"pd3", "pd5"}
 WINDOW = {"w3": 256, "w5": 512}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.

@@ -26,12 +26,21 @@
 // Per tile the wave runs the D == 64 kernel's four fenced phases: QK(keys
 // 0-31); QK(keys 32-63) | elementwise(0-31); PV(0-31) | elementwise(32-63);
 // PV(32-63), each phase's LDS operands read one phase ahead.
+//
+// PUR: the purified-Born weights (flash_born.py:696-811) as in the D == 64
+// fast forward: p = relu(gamma (r - tau))^4 + eps_base relu(r)^2 in fp32,
+// each weight split into bf16 hi + lo terms for the P V contraction (two
+// MFMAs), Z summed in fp32, O and Z stored in fp32 straight from the
+// accumulators.  Masks zero the weights (a zero overlap still weighs
+// relu(-gamma tau)^4 when tau < 0), so without causality the keys past T
+// are masked in the last tile too.
 #pragma once
 
 #include <type_traits>
 
 #include "born_common.h"
 #include "born_fwd_fast.h"
+#include "purified_args.h"
 
 namespace qdl {
 
@@ -43,10 +52,11 @@ struct FwdD128Cfg {
     static constexpr int NST = 3;   // K/V ring stages
 };
 
-template <class E, int MODE>
+template <class E, int MODE, bool PUR = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_fwd16_d128_kernel(FwdArgs p) {
+void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
+    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
     constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
@@ -97,8 +107,15 @@ void born_fwd16_d128_kernel(FwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
+    float pg = 0.f, pgt = 0.f, pse = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        pse = sqrtf(p.eps_base);
+    }
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
@@ -167,7 +184,36 @@ void born_fwd16_d128_kernel(FwdArgs p) {
     // Elementwise pass over one 32-key half of S^T (lane: query c, keys
     // kbase + 8 (r / 4) + r % 4): p' = relu(x|x|) packed, z += p'.  Masked
     // keys (past the row, or before its window) are zeroed first.
-    auto elementwise = [&](f32x16& s, uint32_t (&pk)[8], auto m, int kbase) __attribute__((always_inline)) {
+    constexpr int PW = PUR ? 8 : 1;  // packed low parts of the purified weights
+    auto elementwise = [&](f32x16& s, uint32_t (&pk)[8], uint32_t (&pl)[PW], auto m, int kbase)
+        __attribute__((always_inline)) {
+        if constexpr (PUR) {
+            // Weights zeroed past the row (causal) or past T (dense).
+            const int lim = (kCaus ? qrow : T - 1) - kbase;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float w[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float x = s[2 * j + e];
+                    const float t = fmaf(x, pg, pgt);
+                    const float u = __int_as_float(max(__float_as_int(t), 0));
+                    const float bq = __int_as_float(max(__float_as_int(x * pse), 0));
+                    const float u2 = u * u;
+                    float pw = fmaf(u2, u2, bq * bq);
+                    if constexpr (decltype(m)::value == kMasked) {
+                        const int r = 2 * j + e;
+                        if (8 * (r >> 2) + (r & 3) > lim) pw = 0.f;
+                    }
+                    w[e] = pw;
+                }
+                zacc[0] += w[0] + w[1];
+                const uint32_t hi = E::pack(w[0], w[1]);
+                pk[j] = hi;
+                pl[j % PW] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+            }
+            return;
+        }
         if constexpr (decltype(m)::value == kMasked) {
             const int lim = qrow - kbase;
             const int wlo = kWin ? lim - W + 1 : 0;
@@ -203,13 +249,19 @@ void born_fwd16_d128_kernel(FwdArgs p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) s = E::mfma(ops[ks], qr[ks], s);
     };
-    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[8]) __attribute__((always_inline)) {
+    auto pv_op = [&](const u32x4 (&ops)[2][DB], const uint32_t (&pk)[8], const uint32_t (&pl)[PW])
+        __attribute__((always_inline)) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
                 oacc[db] = E::mfma(ops[hh][db], bq, oacc[db]);
+                if constexpr (PUR) {
+                    const u32x4 bl = {pl[4 * hh % PW], pl[(4 * hh + 1) % PW], pl[(4 * hh + 2) % PW],
+                                      pl[(4 * hh + 3) % PW]};
+                    oacc[db] = E::mfma(ops[hh][db], bl, oacc[db]);
+                }
             }
     };
     // One tile, four fenced phases (kop: K of keys 0-31, read after the
@@ -218,9 +270,13 @@ void born_fwd16_d128_kernel(FwdArgs p) {
     //   2: S1 = QK(kop1) | elementwise(S0) -> P0  reads V(keys 0-31)  -> vop0
     //   3: O += PV(vop0, P0) | elementwise(S1)    reads V(keys 32-63) -> vop1
     //   4: O += PV(vop1, P1)
+    // Purified: twice the PV MFMAs and about four times the elementwise
+    // VALU work per weight; V of keys 32-63 is read at the start of phase 4
+    // instead (keeps the tile within the register budget).
+    constexpr int V2 = PUR ? 20 : 6, V3 = PUR ? 10 : 6;
     auto tile = [&](const uint8_t* kb, const uint8_t* vb, int key0, auto m) __attribute__((always_inline)) {
         f32x16 s0, s1;
-        uint32_t pk0[8], pk1[8];
+        uint32_t pk0[8], pk1[8], pl0[PW], pl1[PW];
         u32x4 kop1[KS], vop0[2][DB], vop1[2][DB];
         // 1
         __builtin_amdgcn_s_setprio(1);
@@ -231,28 +287,29 @@ void born_fwd16_d128_kernel(FwdArgs p) {
         __builtin_amdgcn_s_setprio(0);
         read_v(vop0, vb, 0);
         qk_op(kop1, s1);
-        elementwise(s0, pk0, m, key0 + 4 * g);
+        elementwise(s0, pk0, pl0, m, key0 + 4 * g);
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, V2, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
         }
         __builtin_amdgcn_sched_barrier(0);
         // 3
-        read_v(vop1, vb, 1);
-        pv_op(vop0, pk0);
-        elementwise(s1, pk1, m, key0 + 32 + 4 * g);
+        if constexpr (!PUR) read_v(vop1, vb, 1);
+        pv_op(vop0, pk0, pl0);
+        elementwise(s1, pk1, pl1, m, key0 + 32 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 2 * DB; ++i) {
+        for (int i = 0; i < (PUR ? 4 : 2) * DB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, V3, 1);
+            if constexpr (!PUR) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
         }
         __builtin_amdgcn_sched_barrier(0);
         // 4
         __builtin_amdgcn_s_setprio(1);
-        pv_op(vop1, pk1);
+        if constexpr (PUR) read_v(vop1, vb, 1);
+        pv_op(vop1, pk1, pl1);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -276,6 +333,7 @@ void born_fwd16_d128_kernel(FwdArgs p) {
     };
 
     uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    float* __restrict__ O32 = reinterpret_cast<float*>(p.o) + base;  // purified: fp32 rows
     float* __restrict__ Zp = p.z + (size_t)bh * T;
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
@@ -328,6 +386,24 @@ void born_fwd16_d128_kernel(FwdArgs p) {
             if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
         }
     };
+    // Purified: O = acc / (Z + eps) and Z + eps, fp32, straight from the
+    // accumulators (lane: one query row, 4 consecutive columns per store).
+    auto store_pur = [&](int mb) __attribute__((always_inline)) {
+        const float zl = zacc[0] + zacc[1];
+        const float zd = zl + __shfl_xor(zl, 32) + p.eps;
+        const int qi = mb * BM + 32 * wave + c;
+        if (qi < T) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x16& o = oacc[db];
+                    const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
+                    __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                }
+            if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
+        }
+    };
     auto start_item = [&](int mb) __attribute__((always_inline)) {
         qrow = mb * BM + 32 * wave + c;
 #pragma unroll
@@ -341,12 +417,13 @@ void born_fwd16_d128_kernel(FwdArgs p) {
     // for its share of tile u (everything issued before tile u+1), then the
     // barrier makes the whole tile visible and frees tile u-1's stage.  The
     // first item's rows are staged in LDS in the second item's first step and
-    // stored at the top of its second step; the next step drains them.
+    // stored at the top of its second step (purified: stored from registers
+    // in its first step); the next step drains them.
     constexpr int kTileLoads = 2 * LPW, kQLoads = LQW;
     const bool early_q = (nitems == 2);
     const int uq = max(1, nt_a - 4);
     auto top = [&](int u) __attribute__((always_inline)) {
-        const bool stores_out = (nitems == 2) && (u == nt_a + 2);
+        const bool stores_out = (nitems == 2) && (u == nt_a + (PUR ? 1 : 2));
         const int after = stores_out ? 0 : ((u == uq + 1 && early_q) ? kQLoads : 0) + (u + 1 < ntot ? kTileLoads : 0);
         if (after >= kQLoads + kTileLoads)
             wait_vmcnt<kQLoads + kTileLoads>();
@@ -357,7 +434,7 @@ void born_fwd16_d128_kernel(FwdArgs p) {
         __syncthreads();
         if (u == uq && early_q) issue_q(mb_b);
         if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
-        if (nitems == 2 && u == nt_a + 1) flush(mb_a);
+        if (!PUR && nitems == 2 && u == nt_a + 1) flush(mb_a);
     };
 
     issue_q(mb_a);
@@ -370,7 +447,10 @@ void born_fwd16_d128_kernel(FwdArgs p) {
         const int nt = it ? ntot - nt_a : nt_a;
         const int tb = it ? tb_b : tb_a;
         top(u);
-        if (it > 0) {
+        if constexpr (PUR) {
+            if (it > 0) store_pur(mb_a);
+            load_q();
+        } else if (it > 0) {
             pack();
             load_q();  // before the previous item's rows overwrite this wave's Q rows
             put_lds();
@@ -386,13 +466,14 @@ void born_fwd16_d128_kernel(FwdArgs p) {
         // wave's diagonal, tv the one after it).  One loop per run keeps the
         // masked and full tile bodies out of a common branch (two tile bodies
         // in one branch exceed the register budget).  The barriers and loads
-        // of every step run in every wave.
+        // of every step run in every wave.  Purified, non-causal: the keys
+        // past T are masked (the last tile is masked when T % BN != 0).
         constexpr int kBig = 1 << 29;
         const int rw = mb * BM + 32 * wave;
         const int kv0 = kWin ? max(0, rw - W + 1) : 0;
-        const int kv1 = kCaus ? rw + 31 : kBig;
+        const int kv1 = kCaus ? rw + 31 : (PUR ? T - 1 : kBig);
         const int kf0 = kWin ? max(0, rw + 32 - W) : 0;
-        const int kf1 = kCaus ? rw : kBig;
+        const int kf1 = kCaus ? rw : (PUR ? T - 1 : kBig);
         auto rel = [&](int kt) -> int { return min(max(kt - tb, 0), nt); };
         const int ta = rel(kv0 / BN);
         const int tv = max(rel(kv1 / BN + 1), ta);
@@ -435,10 +516,14 @@ void born_fwd16_d128_kernel(FwdArgs p) {
         masked_run(tv);
         idle_run(nt);
     }
-    if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
-    pack();
-    put_lds();
-    flush(nitems == 2 ? mb_b : mb_a);
+    if constexpr (PUR) {
+        store_pur(nitems == 2 ? mb_b : mb_a);
+    } else {
+        if (nitems == 2 && ntot == nt_a + 1) flush(mb_a);  // a one-tile second item: no later step
+        pack();
+        put_lds();
+        flush(nitems == 2 ? mb_b : mb_a);
+    }
 }
 
 template <class E, int MODE>
@@ -451,6 +536,19 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     const dim3 grid((npair < 256u || MODE == kWindow) ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+// Purified-Born forward through the same kernel (bf16, D == 128, dense or
+// causal, no window / documents); same grid as the Born launch.
+template <int MODE>
+hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
+    using C = FwdD128Cfg;
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
+    const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
+    const dim3 grid(npair < 256u ? nsingle : npair);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // (32, 64, 128, 256; the host zero-pads D to a multiple of 8 and the kernels
 // bound-check columns past D).
 #include "born_bwd_fast.h"
+#include "born_fwd_d128.h"
 #include "born_fwd_doc.h"
 #include "purified.h"
 
@@ -16,6 +17,10 @@ inline bool purified_fast_ok(const PurArgs& a) {
     return a.D == 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
+inline bool purified_d128_ok(const PurArgs& a) {
+    return a.D == 128 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+}
+
 inline bool purified_doc_fast_ok(const PurArgs& a) {
     return a.D == 64 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
@@ -25,6 +30,9 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
+    // bf16, D = 128, dense or causal: the D = 128 kernel's purified mode.
+    if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
+        return a.is_causal ? launch_purified_fwd_d128<kCausal>(a, s) : launch_purified_fwd_d128<kDense>(a, s);
     // bf16, D = 64, document ids without a window: the document kernel's
     // purified mode.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) return launch_purified_fwd_doc(a, s);

@@ -205,6 +205,46 @@ def test_purified_fast_forward(cuda_device, case):
     assert np.max(np.abs(f64(z) - f64(z_g)) / f64(z_g)) <= 1e-4
 
 
+# bf16, D = 128, dense or causal: the D = 128 forward kernel's purified mode
+# (eight waves on 256 query rows); ragged T around its 256-row blocks and 64-key
+# tiles, and shapes with enough heads for two query blocks per workgroup.
+D128_CASES = [
+    # (B, H, T, causal, scale, tau, eps_base, eps, std)
+    (1, 1, 1, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (2, 3, 130, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 200, False, 8.0, -0.1, 0.05, 1e-8, 0.3),
+    (2, 2, 256, False, [4.0, 9.0], [0.0, 0.2], 0.2, 1e-6, 0.3),
+    (1, 2, 300, True, [8.0, 5.0], [-0.05, 0.1], 0.05, 1e-8, 0.2),
+    (1, 1, 777, False, 8.0, -0.2, 0.05, 1e-8, 0.2),
+    (1, 2, 1100, True, 8.0, 0.0625, 0.05, 1e-8, 0.15),
+    (4, 32, 700, True, 8.0, -0.05, 0.05, 1e-8, 0.15),
+    (4, 32, 1100, False, 6.0, 0.0625, 0.05, 1e-8, 0.15),
+]
+
+
+@pytest.mark.parametrize("case", D128_CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-{'causal' if c[3] else 'dense'}")
+def test_purified_d128_forward(cuda_device, case):
+    B, H, T, causal, scale, tau, eps_base, eps, std = case
+    print(f"purified d128 fwd case B{B} H{H} T{T} causal={causal}", flush=True)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 128), seed=T + 11, std=std, n=3,
+                                                          dtype=torch.bfloat16))
+    out, z = _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps)
+    heads = [(0, 0), (B - 1, H - 1), (B // 2, H // 3)] if B * H > 8 else [(b, h) for b in range(B) for h in range(H)]
+    sc, ta = np.atleast_1d(scale), np.atleast_1d(tau)
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        O_ref, Z_ref = orc.purified_forward(f64(q[sl]), f64(k[sl]), f64(v[sl]), sc[h % sc.size], ta[h % ta.size],
+                                            eps_base, causal, eps)
+        assert rel_err(f64(out[sl]), O_ref) <= 1e-4, (b, h, rel_err(f64(out[sl]), O_ref))
+        assert np.max(np.abs(f64(z[sl]) - Z_ref) / Z_ref) <= 1e-4, (b, h)
+    # The same call through the fp32-MFMA kernels (an all-zero document id
+    # tensor: the same visibility).
+    zero_doc = torch.zeros((B, T), dtype=torch.int32, device=cuda_device)
+    out_g, z_g = _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=zero_doc)
+    assert rel_err(f64(out), f64(out_g)) <= 1e-4
+    assert np.max(np.abs(f64(z) - f64(z_g)) / f64(z_g)) <= 1e-4
+
+
 def test_purified_fast_forward_paired_launch(cuda_device):
     """The C3 shape (B16 H16 T1024): workgroups take two query blocks each;
     checked on sampled heads against the oracle."""
