@@ -21,9 +21,15 @@
 //     none of its pairs see (no work, only the barrier), tiles its diagonal
 //     or window edge cuts (masked per element), and tiles all of its pairs
 //     see (no mask), each run in a loop of its own.
+// PUR: the purified-Born gradients (flash_born.py:812-1061) as in the D == 64
+// kernels' purified mode (bf16, dense or causal): dR = (4 gamma u^3 +
+// 2 eps_base b) dP and W = p / Z rounded to bf16 before their contractions,
+// O read in fp32, and the dK/dV kernel's workgroups writing their partial
+// sums of dgamma and dtau (reduced per output afterwards in a fixed order).
 #pragma once
 
 #include "born_bwd_fast.h"
+#include "purified_args.h"
 
 namespace qdl {
 
@@ -37,10 +43,11 @@ struct BwdD128Cfg {
     static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
 };
 
-template <class E, int MODE>
+template <class E, int MODE, bool PUR = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_bwd16_dq_d128_kernel(BwdArgs p) {
+void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -76,8 +83,16 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    // Purified: t = gamma r - gamma tau; dR / dP = 4 gamma u^3 + 2 eps_base b.
+    float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+    }
 
     // Stationary operands (sign-flipped Q, dO: B operands of S^T and T^T),
     // delta_i = dO_i . O_i from the stored O (each lane holds half a row, the
@@ -88,7 +103,6 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
     {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
         const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
-        const uint16_t* __restrict__ Og = reinterpret_cast<const uint16_t*>(p.o) + base;
         const bool ok = qrow < T;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -104,26 +118,45 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
         if (ok) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const u32x4 o = ldg16(Og + (size_t)qrow * DP + (2 * ks + g) * 8);
+                if constexpr (PUR) {
+                    const float* o32 = p.o_in + base + (size_t)qrow * DP + (2 * ks + g) * 8;
+                    const f32x4 oa = *reinterpret_cast<const f32x4*>(o32);
+                    const f32x4 ob = *reinterpret_cast<const f32x4*>(o32 + 4);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    dl += E::lo(o[j]) * E::lo(dr[ks][j]) + E::hi(o[j]) * E::hi(dr[ks][j]);
+                    for (int j = 0; j < 4; ++j) {
+                        const float o0 = j < 2 ? oa[2 * j] : ob[2 * j - 4];
+                        const float o1 = j < 2 ? oa[2 * j + 1] : ob[2 * j - 3];
+                        dl += o0 * E::lo(dr[ks][j]) + o1 * E::hi(dr[ks][j]);
+                    }
+                } else {
+                    const uint16_t* Og = reinterpret_cast<const uint16_t*>(p.o) + base;
+                    const u32x4 o = ldg16(Og + (size_t)qrow * DP + (2 * ks + g) * 8);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        dl += E::lo(o[j]) * E::lo(dr[ks][j]) + E::hi(o[j]) * E::hi(dr[ks][j]);
+                }
             }
         }
         dl += __shfl_xor(dl, 32);
         const size_t row = (size_t)bh * T + qrow;
-        const float zr = ok ? p.z[row] : 1.f;
+        float zr = 1.f;
+        if (ok) {
+            if constexpr (PUR)
+                zr = p.z_in[row];
+            else
+                zr = p.z[row];
+        }
         zinv = ok ? 1.0f / zr : 0.f;
         nd = ok ? -(dl / zr) : 0.f;
         if (ok && g == 0) {
             p.ndelta[row] = -dl;
             p.zinv[row] = zinv;
-            p.delta_z[row] = dl / zr;
+            if constexpr (!PUR) p.delta_z[row] = dl / zr;
         }
     }
     // This workgroup's part of dscale = (2/s) eps sum delta / Z (closed form):
     // its rows' sum in a fixed order (lanes, then waves), one double.
-    {
+    if constexpr (!PUR) {
         float dz = (g == 0) ? -nd : 0.f;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) dz += __shfl_xor(dz, off);
@@ -212,6 +245,29 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
+        if constexpr (PUR) {
+            // A masked pair weighs zero even where its overlap is zero (u =
+            // relu(-gamma tau) > 0 for tau < 0).  Keys past T need no mask
+            // here: their K rows (zero) multiply U.
+            const int lim = qrow - kbase;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float w[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int r = 2 * j + e;
+                    const float x = s[r];
+                    const float uu = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                    const float bb = __int_as_float(max(__float_as_int(x), 0));
+                    const float f = fmaf(p4g, uu * uu * uu, p2e * bb);
+                    float d = f * fmaf(t[r], zinv, nd);
+                    if constexpr (decltype(m)::value == kMasked)
+                        if (8 * (r >> 2) + (r & 3) > lim) d = 0.f;
+                    w[e] = d;
+                }
+                pk[j] = E::pack(w[0], w[1]);
+            }
+        } else {
         if constexpr (decltype(m)::value == kMasked) {
             // Key kbase + 8 (r / 4) + r % 4 of register r: masked past the
             // lane's row, and (window) before its first key.
@@ -230,6 +286,7 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
             const float a0 = __int_as_float(max(__float_as_int(x0), 0));
             const float a1 = __int_as_float(max(__float_as_int(x1), 0));
             pk[j] = E::pack(a0 * fmaf(t[2 * j], zinv, nd), a1 * fmaf(t[2 * j + 1], zinv, nd));
+        }
         }
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -283,7 +340,7 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
     // bytes per lane and store 4 whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = 2.f * sc * fabsf(sc) / sq_pre;
+    const float f = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
     int ln = lane;
     asm volatile("" : "+v"(ln));
     {
@@ -310,10 +367,11 @@ void born_bwd16_dq_d128_kernel(BwdArgs p) {
     }
 }
 
-template <class E, int MODE>
+template <class E, int MODE, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
+void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -346,8 +404,18 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
 
     const size_t base = (size_t)bh * T * DP;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
+    if constexpr (PUR) {
+        ptau = p.tau[p.per_head_tau ? h : 0];
+        pg = sc;
+        pgt = -sc * ptau;
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+        pe = p.eps_base;
+    }
+    float dg_acc = 0.f, dt_acc = 0.f;  // purified: sum u^3 dP (r - tau), sum u^3 dP
 
     // Stationary operands: sign-flipped K and V rows of this lane's key.
     u32x4 kr[KS], vr[KS];
@@ -504,6 +572,38 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
     auto elementwise = [&](const uint8_t* sb, int nb, int qbase, f32x16& s, const f32x16& dp, uint32_t (&w2)[8],
                            uint32_t (&u2)[8], auto m) __attribute__((always_inline)) {
         const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
+        if constexpr (PUR) {
+            // Masked pairs (query before the lane's key) weigh zero; queries
+            // past T have 1/Z = 0 from the workspace read.
+            const int lim = qbase - key;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    float ww[2], uu[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 4 * i + k + e;
+                        const float x = s[r];
+                        float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                        float bb = __int_as_float(max(__float_as_int(x), 0));
+                        if constexpr (decltype(m)::value == kMasked)
+                            if (8 * (r >> 2) + (r & 3) + lim < 0) u = bb = 0.f;
+                        const float u2_ = u * u;
+                        const float dpz = dp[r] * z4[k + e];
+                        const float a = u2_ * u * dpz;
+                        dg_acc = fmaf(a, x - ptau, dg_acc);
+                        dt_acc += a;
+                        ww[e] = fmaf(u2_, u2_, pe * bb * bb) * z4[k + e];
+                        uu[e] = fmaf(p4g, u2_ * u, p2e * bb) * dpz;
+                    }
+                    w2[(4 * i + k) >> 1] = E::pack(ww[0], ww[1]);
+                    u2[(4 * i + k) >> 1] = E::pack(uu[0], uu[1]);
+                }
+            }
+            return;
+        }
         if constexpr (decltype(m)::value == kMasked) {
             // Register r (query qbase + off) is masked before the lane's key
             // (off + lim < 0) and (window) past its window (off + lim >= W).
@@ -543,6 +643,9 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
             }
         }
     };
+    // VALU instructions interleaved per MFMA (the purified elementwise pass
+    // is about three times the Born one).
+    constexpr int VE = PUR ? 14 : 5;
     auto tile = [&](const uint8_t* sb, int i0, auto m) __attribute__((always_inline)) {
         const Bases bs = bases_of(sb);
         u32x4 rq0[KS], rd0[KS], rq1[KS], rd1[KS];
@@ -567,8 +670,8 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
         elementwise(sb, 0, i0 + 4 * g, s0, dp0, w0, u0, m);
 #pragma unroll
         for (int i = 0; i < 2 * KS; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, VE, 0);  // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -580,7 +683,7 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
 #pragma unroll
         for (int i = 0; i < 4 * DB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, VE, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -631,8 +734,29 @@ void born_bwd16_dkdv_d128_kernel(BwdArgs p) {
     // then read back 16 bytes per lane and stored 4 whole rows per
     // instruction.
     __syncthreads();  // every wave is done with the ring
-    const float fk = 2.f * sc * fabsf(sc) / sq_pre;
-    const float fv = (sc / sq_pre) * (sc / sq_pre);
+    const float fk = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
+    const float fv = PUR ? 1.f : (sc / sq_pre) * (sc / sq_pre);
+    if constexpr (PUR) {
+        // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
+        // waves), past the output staging; keys past T excluded (their zero
+        // K row still weighs relu(-gamma tau) when tau < 0).
+        float a = key < T ? 4.f * dg_acc : 0.f;
+        float t2 = key < T ? -4.f * sc * dt_acc : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off);
+            t2 += __shfl_xor(t2, off);
+        }
+        float* red = reinterpret_cast<float*>(smem + BK * RB);
+        if (lane == 0) red[wave] = a, red[NW + wave] = t2;
+        __syncthreads();
+        if (tid == 0) {
+            float sa = 0.f, st = 0.f;
+            for (int w = 0; w < NW; ++w) sa += red[w], st += red[NW + w];
+            p.part[bid] = sa;
+            p.part[gridDim.x + bid] = st;
+        }
+    }
     uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
     uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
     int ln = lane;
@@ -679,6 +803,23 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
                        st, a, (int)(nq * BH));
+    return hipGetLastError();
+}
+
+// The purified D == 128 backward (bf16, dense or causal): dQ (and the
+// workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
+// partials (one per dK/dV workgroup).
+template <int MODE>
+hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
+    const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0, st,
+                       a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64), 0,
+                       st, a);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // Purified-Born kernel instantiations: element type x padded head dim
 // (32, 64, 128, 256; the host zero-pads D to a multiple of 8 and the kernels
 // bound-check columns past D).
+#include "born_bwd_d128.h"
 #include "born_bwd_fast.h"
 #include "born_fwd_d128.h"
 #include "born_fwd_doc.h"
@@ -62,10 +63,24 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// bf16, D = 128, dense or causal: the D = 128 dQ and dK/dV kernels' purified
+// mode, then the same reduction.
+template <int MODE>
+static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
+    hipError_t e = launch_purified_bwd_d128<MODE>(a, s);
+    if (e != hipSuccess) return e;
+    const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 128);
+    const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
+    hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
+    return hipGetLastError();
+}
+
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
+    if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
+        return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
     // bf16, D = 64, document ids without a window: the same kernels' document
     // variants.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))

@@ -314,6 +314,79 @@ def test_purified_fast_backward(cuda_device, case):
             assert ok.all(), f"{label} {name}: {got} vs fp32-MFMA kernel {gen}"
 
 
+# bf16, D = 128, dense or causal: the D = 128 dQ and dK/dV kernels' purified
+# mode, held to the same bars as the D = 64 kernels above (against the oracle,
+# and against the fp32-MFMA kernels reached through a window longer than T).
+D128_BWD_CASES = [
+    # (B, H, T, causal, scale, tau, eps_base, eps, std)
+    (1, 1, 1, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (2, 3, 130, True, 8.0, 0.0625, 0.05, 1e-8, 0.3),
+    (1, 2, 200, False, 8.0, -0.1, 0.05, 1e-8, 0.3),
+    (2, 2, 256, False, [4.0, 9.0], [0.0, 0.2], 0.2, 1e-6, 0.3),
+    (1, 2, 300, True, [8.0, 5.0], [-0.05, 0.1], 0.05, 1e-8, 0.2),
+    (1, 1, 777, False, 8.0, -0.2, 0.05, 1e-8, 0.2),
+    (1, 2, 1100, True, 6.0, 0.0625, 0.05, 1e-8, 0.15),
+]
+
+
+@pytest.mark.parametrize("case", D128_BWD_CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-{'causal' if c[3] else 'dense'}")
+def test_purified_d128_backward(cuda_device, case):
+    B, H, T, causal, scale, tau, eps_base, eps, std = case
+    print(f"purified d128 bwd case B{B} H{H} T{T} causal={causal}", flush=True)
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 128), seed=T + 13, std=std, n=4,
+                                                              dtype=torch.bfloat16))
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    kw = dict(eps_base=eps_base, is_causal=causal, eps=eps)
+    fast = _run(q, k, v, do, sc, ta, **kw)
+    generic = _run(q, k, v, do, sc, ta, window_size=T + 1, **kw)
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau), f64(do), **kw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.atleast_1d(scale), np.atleast_1d(tau),
+                                           f64(do), **kw)
+    for i, name in enumerate(("dq", "dk", "dv")):
+        got, gen, want, m = f64(fast[1 + i]), f64(generic[1 + i]), ref[i], mag[i]
+        er = rel_err(got, want)
+        ef = max_abs(got, want) / m.max() if m.max() > 0 else max_abs(got, want)
+        assert er <= 2e-2 or ef <= 1e-4, f"{name}: rel {er:.3e} vs oracle (term scale {ef:.3e})"
+        eg = rel_err(got, gen)
+        efg = max_abs(got, gen) / m.max() if m.max() > 0 else max_abs(got, gen)
+        assert eg <= 5e-3 or efg <= 1e-4, f"{name}: rel {eg:.3e} vs the fp32-MFMA kernel"
+    for name, got, gen, want, m in (("dscale", fast[4], generic[4], ref[3], mag[3]),
+                                    ("dtau", fast[5], generic[5], ref[4], mag[4])):
+        got = np.atleast_1d(f64(got))
+        gen = np.atleast_1d(f64(gen))
+        ok = (np.abs(got - want) <= 2e-2 * np.abs(want)) | (np.abs(got - want) <= 1e-4 * m)
+        assert ok.all(), f"{name}: {got} vs oracle {want} (term scale {m})"
+        ok = (np.abs(got - gen) <= 5e-3 * np.abs(gen)) | (np.abs(got - gen) <= 1e-4 * m)
+        assert ok.all(), f"{name}: {got} vs fp32-MFMA kernel {gen}"
+
+
+def test_purified_d128_backward_many_heads(cuda_device):
+    """B2 H16 T700, causal, per-head gamma and tau: every head's dgamma and
+    dtau against the oracle (to the bf16 bar of their value or of the scale
+    of their terms, as above), gradients on sampled heads."""
+    B, H, T = 2, 16, 700
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, 128), seed=31, std=0.15, n=4,
+                                                              dtype=torch.bfloat16))
+    scale = np.linspace(3.0, 9.0, H).astype(np.float32)
+    tau = np.linspace(-0.1, 0.1, H).astype(np.float32)
+    sc = torch.tensor(scale, device=cuda_device)
+    ta = torch.tensor(tau, device=cuda_device)
+    fast = _run(q, k, v, do, sc, ta, is_causal=True)
+    dsc, dta = f64(fast[4]), f64(fast[5])
+    for h in range(H):
+        sl = (slice(None), slice(h, h + 1))
+        args = (f64(q[sl]), f64(k[sl]), f64(v[sl]), scale[h], tau[h], f64(do[sl]))
+        ref = orc.purified_backward(*args)
+        mag = orc.purified_backward_magnitudes(*args)
+        if h in (0, 7, 15):
+            for i in range(3):
+                assert rel_err(f64(fast[1 + i][sl]), ref[i]) <= 2e-2, (h, i)
+        for name, got, want, m in (("dscale", dsc[h], ref[3], mag[3]), ("dtau", dta[h], ref[4], mag[4])):
+            err = abs(got - float(np.squeeze(want)))
+            assert err <= 2e-2 * abs(float(np.squeeze(want))) or err <= 1e-4 * float(np.squeeze(m)), (name, h, got, want, m)
+
+
 def test_purified_fast_backward_full_size(cuda_device):
     """The C5 shape (B16 H16 T2048): gradients checked on sampled heads
     against the oracle; dgamma / dtau against the fp32-MFMA kernels."""
