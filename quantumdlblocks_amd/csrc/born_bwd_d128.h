@@ -26,9 +26,13 @@
 // 2 eps_base b) dP and W = p / Z rounded to bf16 before their contractions,
 // O read in fp32, and the dK/dV kernel's workgroups writing their partial
 // sums of dgamma and dtau (reduced per output afterwards in a fixed order).
+// PAD: a head dim D < 128 (a multiple of 8) as in the D == 128 forward: the
+// tile loads of chunks past D return zeros, the stationary rows are zero
+// there, and the output chunks past D are not stored.
 #pragma once
 
 #include "born_bwd_fast.h"
+#include "born_fwd_d128.h"
 #include "purified_args.h"
 
 namespace qdl {
@@ -43,7 +47,7 @@ struct BwdD128Cfg {
     static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
 };
 
-template <class E, int MODE, bool PUR = false>
+template <class E, int MODE, bool PUR = false, bool PAD = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
@@ -81,7 +85,10 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const int c = lane & 31, g = lane >> 5;
     const int qrow = R + 32 * wave + c;  // this lane's query row
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
@@ -107,9 +114,9 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
-            if (ok) {
-                x = ldg16(Qg + (size_t)qrow * DP + (2 * ks + g) * 8);
-                y = ldg16(dOg + (size_t)qrow * DP + (2 * ks + g) * 8);
+            if (ok && (!PAD || 2 * ks + g < CG)) {
+                x = ldg16(Qg + (size_t)qrow * D + (2 * ks + g) * 8);
+                y = ldg16(dOg + (size_t)qrow * D + (2 * ks + g) * 8);
             }
             qr[ks] = x ^ flip;
             dr[ks] = y;
@@ -118,8 +125,9 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         if (ok) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
+                if (PAD && 2 * ks + g >= CG) continue;  // dO is zero there
                 if constexpr (PUR) {
-                    const float* o32 = p.o_in + base + (size_t)qrow * DP + (2 * ks + g) * 8;
+                    const float* o32 = p.o_in + base + (size_t)qrow * D + (2 * ks + g) * 8;
                     const f32x4 oa = *reinterpret_cast<const f32x4*>(o32);
                     const f32x4 ob = *reinterpret_cast<const f32x4*>(o32 + 4);
 #pragma unroll
@@ -130,7 +138,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     }
                 } else {
                     const uint16_t* Og = reinterpret_cast<const uint16_t*>(p.o) + base;
-                    const u32x4 o = ldg16(Og + (size_t)qrow * DP + (2 * ks + g) * 8);
+                    const u32x4 o = ldg16(Og + (size_t)qrow * D + (2 * ks + g) * 8);
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         dl += E::lo(o[j]) * E::lo(dr[ks][j]) + E::hi(o[j]) * E::hi(dr[ks][j]);
@@ -180,7 +188,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kRunsBig,
                         kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kRunsBig);
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
 
@@ -195,7 +203,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (key0 + row) * RB + ((pc ^ swz256(row)) << 4);
+            const int ch = pc ^ swz256(row);
+            const int off = (PAD && ch >= CG) ? kBufOOB : (key0 + row) * (2 * D) + (ch << 4);
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
         }
@@ -363,11 +372,12 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         const int row = 32 * wave + 4 * i + (ln >> 4);
         const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 15)) << 4));
         const int q = R + row;
-        if (q < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * DP + chunk * 8));
+        if (q < T && (!PAD || chunk < CG))
+            __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * D + chunk * 8));
     }
 }
 
-template <class E, int MODE, bool PUR = false>
+template <class E, int MODE, bool PUR = false, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
@@ -402,7 +412,10 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const int kw0 = K0 + 32 * wave;  // first key of this wave
     const int key = kw0 + c;         // this lane's key
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
@@ -426,9 +439,9 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
-            if (ok) {
-                x = ldg16(Kg + (size_t)key * DP + (2 * ks + g) * 8);
-                y = ldg16(Vg + (size_t)key * DP + (2 * ks + g) * 8);
+            if (ok && (!PAD || 2 * ks + g < CG)) {
+                x = ldg16(Kg + (size_t)key * D + (2 * ks + g) * 8);
+                y = ldg16(Vg + (size_t)key * D + (2 * ks + g) * 8);
             }
             kr[ks] = x ^ flip;
             vr[ks] = y;
@@ -446,7 +459,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const WaveRuns runs(q_lo, ntiles, kCaus ? kw0 : 0, kWin ? kw0 + 31 + W - 1 : kRunsBig, kCaus ? kw0 + 31 : 0,
                         kWin ? kw0 + W - 1 : kRunsBig);
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
     const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
@@ -461,7 +474,8 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (i0 + row) * RB + ((pc ^ swz256(row)) << 4);
+            const int ch = pc ^ swz256(row);
+            const int off = (PAD && ch >= CG) ? kBufOOB : (i0 + row) * (2 * D) + (ch << 4);
             dma_load16(rq, lds_addr(sb + (wave * LPW + i) * 1024), off);
             dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
         }
@@ -783,23 +797,25 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             const int r2 = 32 * wave + 4 * i + (ln >> 4);
             const u32x4 x = *reinterpret_cast<const u32x4*>(smem + r2 * RB + ((chunk ^ (r2 & 15)) << 4));
             const int kk = K0 + r2;
-            if (kk < T)
-                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * DP + chunk * 8));
+            if (kk < T && (!PAD || chunk < CG))
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * D + chunk * 8));
         }
     }
 }
 
 // The D == 128 backward: dQ (and the workspace), dK/dV, then dscale from the
 // dQ kernel's per-workgroup sums.
-template <class E, int MODE>
+template <class E, int MODE, bool PAD = false>
 hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64),
+                       0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
                        st, a, (int)(nq * BH));
@@ -809,17 +825,17 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
 // The purified D == 128 backward (bf16, dense or causal): dQ (and the
 // workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
 // partials (one per dK/dV workgroup).
-template <int MODE>
+template <int MODE, bool PAD = false>
 hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0, st,
-                       a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true, PAD>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64), 0,
-                       st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true, PAD>), dim3(nk * BH),
+                       dim3(BwdD128Cfg::NWK * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -34,6 +34,12 @@
 // accumulators.  Masks zero the weights (a zero overlap still weighs
 // relu(-gamma tau)^4 when tau < 0), so without causality the keys past T
 // are masked in the last tile too.
+//
+// PAD: a head dim D < 128 (a multiple of 8) on the same kernel.  The rows in
+// HBM are 2 D bytes; the loads of the 16-byte chunks past D are sent out of
+// the buffer's range, so they land in LDS as zeros, and the output chunks
+// past D are not stored.  The arithmetic is that of D == 128 with zero
+// columns (which add nothing to any overlap).
 #pragma once
 
 #include <type_traits>
@@ -52,7 +58,10 @@ struct FwdD128Cfg {
     static constexpr int NST = 3;   // K/V ring stages
 };
 
-template <class E, int MODE, bool PUR = false>
+// Offset sent to a buffer load that must return zeros (past every range).
+constexpr int kBufOOB = 0x7ffffff0;
+
+template <class E, int MODE, bool PUR = false, bool PAD = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
@@ -105,7 +114,11 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const int c = lane & 31, g = lane >> 5;
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int RBG = 2 * D;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
@@ -117,7 +130,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         pse = sqrtf(p.eps_base);
     }
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RBG;
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
@@ -132,9 +145,10 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (key0 + row) * RB;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 15)) << 4));
-            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 2)) << 4));
+            const int off = (key0 + row) * RBG;
+            const int kc = pc ^ (row & 15), vc = pc ^ ((row & 3) << 2);
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), (PAD && kc >= CG) ? kBufOOB : off + (kc << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
     };
     auto issue_q = [&](int mb) __attribute__((always_inline)) {
@@ -142,8 +156,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         for (int i = 0; i < LQW; ++i) {
             const int slot = (wave * LQW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
+            const int qc = pc ^ (row & 15);
             dma_load16<true>(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
-                             (mb * BM + row) * RB + ((pc ^ (row & 15)) << 4));
+                             (PAD && qc >= CG) ? kBufOOB : (mb * BM + row) * RBG + (qc << 4));
         }
     };
 
@@ -383,7 +398,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             const int row = 32 * wave + 4 * i + (ln >> 4);
             const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 15)) << 4));
             const int qi = mb * BM + row;
-            if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
+            if (qi < T && (!PAD || chunk < CG))
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * D + chunk * 8));
         }
     };
     // Purified: O = acc / (Z + eps) and Z + eps, fp32, straight from the
@@ -399,7 +415,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 for (int j = 0; j < 4; ++j) {
                     const f32x16& o = oacc[db];
                     const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
-                    __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                    const int col = db * 32 + 8 * j + 4 * g;
+                    if (!PAD || col < D)
+                        __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * D + col));
                 }
             if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
         }
@@ -526,29 +544,50 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     }
 }
 
-template <class E, int MODE>
+// One workgroup per CU (160 KiB of LDS), so the launch runs in rounds of 256
+// workgroups.  Paired or unpaired, by the estimated finishing time of each in
+// tile steps: paired workgroups all carry about the same work (causal: a pair
+// (mb, nmb-1-mb) holds 4 (nmb + 1) tiles; dense: 2 nt) and finish in whole
+// rounds; unpaired blocks go out longest first, so the CUs' loads even out
+// to about the average plus one short block.  Paired when that is no later
+// (it overlaps the second block's start-up with the first's tail): d3, d5
+// (one and two full rounds) pair; B8 H10 T2048 (320 pairs, 1.25 rounds)
+// does not.
+inline bool d128_fwd_paired(int B, int H, int T, bool causal) {
+    constexpr int64_t S = 256;  // CUs
+    const int64_t BH = (int64_t)B * H;
+    const int64_t nmb = (T + 255) / 256, nt = (T + 63) / 64;
+    const int64_t rounds = (BH * ((nmb + 1) / 2) + S - 1) / S;
+    if (causal) {
+        const int64_t total = BH * 2 * nmb * (nmb + 1);  // sum over blocks of 4 (mb + 1)
+        return rounds * 4 * (nmb + 1) <= (total + S - 1) / S + 4;
+    }
+    return rounds * 2 * nt <= (BH * nmb + S - 1) / S * nt;
+}
+
+template <class E, int MODE, bool PAD = false>
 hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
-    // One workgroup per CU (160 KiB of LDS): pair query blocks unless that
-    // leaves fewer workgroups than CUs (256).  Windows: never paired.
+    // Windows: never paired.
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid((npair < 256u || MODE == kWindow) ? nsingle : npair);
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE>), grid, dim3(C::NW * 64), 0, st, a);
+    const bool pair = MODE != kWindow && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
+    const dim3 grid(pair ? npair : nsingle);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 
 // Purified-Born forward through the same kernel (bf16, D == 128, dense or
 // causal, no window / documents); same grid as the Born launch.
-template <int MODE>
+template <int MODE, bool PAD = false>
 hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid(npair < 256u ? nsingle : npair);
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true>), grid, dim3(C::NW * 64), 0, st, a);
+    const dim3 grid(d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal) ? npair : nsingle);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -188,6 +188,17 @@ def test_bwd_d128_sliding_window(cuda_device, dtype, window):
                std=0.7, check_dscale=True)
 
 
+@pytest.mark.parametrize("D", [72, 96, 120])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["causal", "dense", "window"])
+def test_bwd_d128_padded_head_dims(cuda_device, D, dtype, mode):
+    """64 < D < 128 runs the D = 128 dQ and dK/dV kernels with the columns
+    past D zero and not stored: ragged T, causal, dense, a causal window,
+    dscale."""
+    kw = dict(is_causal=mode != "dense", window_size=100 if mode == "window" else 0)
+    _check_bwd(2, 2, 555, D, dtype, cuda_device, scale=[0.09, -0.2], std=0.7, seed=D + 3, check_dscale=True, **kw)
+
+
 def test_bwd_d128_config_d5(cuda_device):
     """d5: bf16 B16 H8 T2048 D128 forward + backward (the C5 work at head dim
     128), N(0,1); 16 heads covering every batch row and block residue."""

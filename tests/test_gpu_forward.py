@@ -169,13 +169,14 @@ def test_fwd_d128_kernel(cuda_device, T, is_causal, dtype, scale):
     _check_fwd(1, 2, T, 128, dtype, cuda_device, scale=scale, is_causal=is_causal, seed=T + 1)
 
 
-@pytest.mark.parametrize("T", [700, 1100])
+@pytest.mark.parametrize("B,H,T", [(4, 32, 700), (5, 17, 1100), (2, 64, 1024), (8, 10, 1100)])
 @pytest.mark.parametrize("is_causal", [True, False])
-def test_fwd_d128_block_pairs(cuda_device, T, is_causal):
-    """Enough heads for the paired launch (blocks mb and nmb-1-mb in one
-    workgroup, the odd block count's middle block alone); per-head scales of
+def test_fwd_d128_block_pairs(cuda_device, B, H, T, is_causal):
+    """Shapes where the launch pairs blocks (mb and nmb-1-mb in one
+    workgroup, the odd block count's middle block alone: every dense case,
+    causal T 700, 1024 and 1100 with 85 heads) and where it does not (causal
+    T 1100 with 80 heads: the pairs would run 1.25 rounds); per-head scales of
     both signs; heads covering every residue of the pair index."""
-    B, H = 4, 32
     sc = np.linspace(-0.2, 0.2, H).astype(np.float32)
     sc[H // 2] = 0.13
     sel = [(b, (7 * b + 5 * j) % H) for b in range(B) for j in range(3)]
@@ -189,6 +190,17 @@ def test_fwd_d128_sliding_window(cuda_device, dtype, window):
     """Causal windows at D = 128: windows starting inside, on and beside a
     wave's 32 rows, a 64-key tile and a 256-row block, longer than T."""
     _check_fwd(2, 2, 1100, 128, dtype, cuda_device, window_size=window, scale=0.09, seed=window + 11)
+
+
+@pytest.mark.parametrize("D", [104, 112, 120])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["causal", "dense", "window"])
+def test_fwd_d128_padded_head_dims(cuda_device, D, dtype, mode):
+    """96 < D < 128 runs the D = 128 kernel with the columns past D loaded as
+    zeros and not stored: ragged T, causal, dense and a causal window."""
+    kw = dict(is_causal=mode != "dense", window_size=100 if mode == "window" else 0)
+    _check_fwd(2, 2, 777, D, dtype, cuda_device, scale=0.11, seed=D, **kw)
+    _check_fwd(4, 32, 300, D, dtype, cuda_device, scale=0.11, seed=D + 1, heads=[(0, 0), (1, 7), (3, 31)], **kw)
 
 
 def test_fwd_d128_config_d3(cuda_device):

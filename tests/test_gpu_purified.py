@@ -219,6 +219,7 @@ D128_CASES = [
     (1, 2, 1100, True, 8.0, 0.0625, 0.05, 1e-8, 0.15),
     (4, 32, 700, True, 8.0, -0.05, 0.05, 1e-8, 0.15),
     (4, 32, 1100, False, 6.0, 0.0625, 0.05, 1e-8, 0.15),
+    (2, 64, 1024, False, 6.0, -0.05, 0.05, 1e-8, 0.15),  # dense, paired
 ]
 
 
@@ -243,6 +244,45 @@ def test_purified_d128_forward(cuda_device, case):
     out_g, z_g = _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=zero_doc)
     assert rel_err(f64(out), f64(out_g)) <= 1e-4
     assert np.max(np.abs(f64(z) - f64(z_g)) / f64(z_g)) <= 1e-4
+
+
+@pytest.mark.parametrize("D", [72, 96, 120])
+@pytest.mark.parametrize("causal", [True, False])
+def test_purified_d128_padded_head_dims(cuda_device, D, causal):
+    """64 < D < 128 (bf16) runs the D = 128 purified kernels with the columns
+    past D zero: forward against the oracle to 1e-4, gradients, dgamma and
+    dtau against the oracle and the fp32-MFMA kernels (through a window longer
+    than T), tau < 0 with T not a multiple of 64."""
+    B, H, T = 1, 2, 333
+    print(f"purified padded D{D} causal={causal}", flush=True)
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 17, std=0.25, n=4,
+                                                              dtype=torch.bfloat16))
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    out, z = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, causal,
+                                        1e-8)
+    assert rel_err(f64(out), O_ref) <= 1e-4, rel_err(f64(out), O_ref)
+    assert np.max(np.abs(f64(z) - Z_ref) / Z_ref) <= 1e-4
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    kw = dict(eps_base=0.05, is_causal=causal, eps=1e-8)
+    fast = _run(q, k, v, do, sc, ta, **kw)
+    generic = _run(q, k, v, do, sc, ta, window_size=T + 1, **kw)
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do), **kw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do),
+                                           **kw)
+    for i, name in enumerate(("dq", "dk", "dv")):
+        got, gen, want, m = f64(fast[1 + i]), f64(generic[1 + i]), ref[i], mag[i]
+        ef = max_abs(got, want) / m.max()
+        assert rel_err(got, want) <= 2e-2 or ef <= 1e-4, (name, rel_err(got, want), ef)
+        assert rel_err(got, gen) <= 5e-3 or max_abs(got, gen) / m.max() <= 1e-4, (name, rel_err(got, gen))
+    for name, got, gen, want, m in (("dscale", fast[4], generic[4], ref[3], mag[3]),
+                                    ("dtau", fast[5], generic[5], ref[4], mag[4])):
+        got, gen = np.atleast_1d(f64(got)), np.atleast_1d(f64(gen))
+        ok = (np.abs(got - want) <= 2e-2 * np.abs(want)) | (np.abs(got - want) <= 1e-4 * m)
+        assert ok.all(), (name, got, want, m)
+        ok = (np.abs(got - gen) <= 5e-3 * np.abs(gen)) | (np.abs(got - gen) <= 1e-4 * m)
+        assert ok.all(), (name, got, gen)
 
 
 def test_purified_fast_forward_paired_launch(cuda_device):
