@@ -69,6 +69,9 @@ CONFIGS.update({
     "d5": (16, 8, 2048, 128, 1.0, False, None, True),
     "w3": (16, 16, 1024, 64, 0.125, False, None, False),
     "w5": (16, 16, 2048, 64, 1.0, False, None, True),
+    # C4's documents at head dim 128 (half the heads, same flops and bytes)
+    "dc4": (4, 8, 8192, 128, 1.0, False, 512.0, False),
+    "dc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
     # purified-Born attention at head dim 128 on the same work
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),

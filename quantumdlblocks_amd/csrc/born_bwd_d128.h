@@ -47,18 +47,21 @@ struct BwdD128Cfg {
     static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
 };
 
-template <class E, int MODE, bool PUR = false, bool PAD = false>
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!DOC || (MODE != kWindow && !PUR), "documents: Born, no window");
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
-    constexpr int kTileLoads = 2 * LPW;
+    constexpr int CAP = 256;               // documents: candidate tiles screened per pass
+    // Loads per wave per tile: K, V (documents: and 8 of the key document ids).
+    constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB && BM == 32 * NW, "tile split / staging");
     constexpr bool kWin = (MODE == kWindow);
     constexpr bool kCaus = (MODE == kCausal) || kWin;
@@ -66,6 +69,10 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // The K/V ring during the tile loop, the output staging afterwards.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
     __shared__ float s_dz[NW];
+    // Documents: key document ids per stage, the kept-tile list and screening scratch.
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[2 * NW + 1];
     uint8_t* const k_lds = smem;
     uint8_t* const v_lds = smem + NST * TB;
 
@@ -191,12 +198,18 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
 
-    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
-    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    // Tile u (documents: kept tile u of the list) -> stage u % NST:
+    // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane,
+    // slot = row * CPR + chunk'; documents: also this wave's 8 key document
+    // ids (lanes 0-1, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
-        const int key0 = (tb + u) * BN;
+        int key0 = (tb + u) * BN;
+        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -208,6 +221,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
         }
+        if constexpr (DOC)
+            if (lane < 2) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 8), (key0 + wave * 8 + lane * 4) * 4);
     };
 
     // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, T^T);
@@ -235,9 +250,15 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = zero16();
 
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the row's document id (INT_MIN past T); per tile, whether
+    // this wave tests it per element (dmw) and the stage's key ids (kdp).
+    const int qdoc = (DOC && qrow < T) ? docb[qrow] : INT_MIN;
+    bool dmw = true;
+    const int32_t* kdp = kd_lds;
     // One 32-key half nb of a tile:
     //   S^T = K Q^T, T^T = V dO^T      (A = K, V rows; B = Q^T, dO^T)
     //   U = relu(S^T) (T^T / Z - delta / Z), masked keys zeroed
@@ -288,6 +309,20 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
             }
         }
+        if constexpr (decltype(m)::value == kDocm) {
+            // Masked past the lane's row (causal) or in another document.
+            if (dmw) {
+                const int lim = kCaus ? qrow - kbase : INT_MAX;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
+                    const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (8 * i + k > lim || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             float x0 = s[2 * j], x1 = s[2 * j + 1];
@@ -312,6 +347,68 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // Pipeline: tiles 0 and 1 issued up front (tile 1 after the stationary
     // loads have landed), tile u+2 right after the barrier that starts step
     // u; at that barrier each wave has waited for its share of tile u.
+    if constexpr (DOC) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]), "+v"(dr[ks]));
+        asm volatile("" : "+v"(zinv), "+v"(nd));
+        // Document range of this wave's valid rows (uniform; wone: one
+        // document) and of the whole block.
+        int wlo = qrow < T ? qdoc : INT_MAX, whi = qrow < T ? qdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            wlo = min(wlo, __shfl_xor(wlo, off));
+            whi = max(whi, __shfl_xor(whi, off));
+        }
+        wlo = __builtin_amdgcn_readfirstlane(wlo);
+        whi = __builtin_amdgcn_readfirstlane(whi);
+        const bool wone = wlo == whi;
+        if (lane == 0) {
+            s_rng[2 * wave] = wlo;
+            s_rng[2 * wave + 1] = whi;
+        }
+        __syncthreads();
+        int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_rng[2 * w]);
+            bq_hi = max(bq_hi, s_rng[2 * w + 1]);
+        }
+        // The kept tiles of each chunk of candidates through the same
+        // pipeline.  Per tile and wave: nothing to do when the tile lies past
+        // the wave's rows or is one document none of them belongs to; no
+        // per-element test when it is before the wave's first row and one
+        // document that all of them belong to.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            if (n > 1) issue(1);
+            for (int u = 0; u < n; ++u) {
+                if (u + 1 < n)
+                    wait_vmcnt<kTileLoads>();
+                else
+                    wait_vmcnt<0>();
+                __syncthreads();
+                if (u + 2 < n) issue(u + 2);
+                int soff = (u % NST) * TB;
+                asm volatile("" : "+s"(soff));
+                const uint8_t* kb = k_lds + soff;
+                const uint8_t* vb = v_lds + soff;
+                kdp = kd_lds + (soff / TB) * BN;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int key0 = (e & ~kDocOne) * BN;
+                const bool one = (e & kDocOne) != 0;
+                const bool vis = !(kCaus && key0 > rw + 31) && !(one && (td < wlo || td > whi));
+                dmw = (kCaus && key0 + BN - 1 > rw) || !(one && wone && td == wlo);
+                if (vis) {
+                    half(kb, vb, 0, key0 + 4 * g, Docm{});
+                    half(kb, vb, 1, key0 + 32 + 4 * g, Docm{});
+                }
+            }
+            __syncthreads();  // the list and the ring are reused by the next chunk
+        }
+    } else {
     if (ntiles > 0) issue(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]), "+v"(dr[ks]));
@@ -343,6 +440,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
+    }
 
     // Epilogue: scale, pack, stage this wave's rows in the idle ring (row r
     // at smem + RB r, chunks XOR-swizzled by r & 15), read them back 16
@@ -377,24 +475,29 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     }
 }
 
-template <class E, int MODE, bool PUR = false, bool PAD = false>
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!DOC || (MODE != kWindow && !PUR), "documents: Born, no window");
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BQ * RB;            // bytes per Q or dO tile
-    constexpr int SB = 2 * TB + 2 * BQ * 4;  // bytes per stage: Q, dO, -delta, 1/Z
+    // Bytes per stage: Q, dO, -delta, 1/Z (documents: and the query document ids).
+    constexpr int SB = 2 * TB + (DOC ? 3 : 2) * BQ * 4;
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
+    constexpr int CAP = 256;               // documents: candidate tiles screened per pass
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && BK * RB <= NST * SB && BK == 32 * NW,
                   "tile split / staging");
     constexpr bool kWin = (MODE == kWindow);
     constexpr bool kCaus = (MODE == kCausal) || kWin;
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[2 * NW + 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -464,12 +567,18 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
     const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
 
-    // Tile u -> stage u % NST.  Waves 0 and 1 also bring the tile's -delta
-    // and 1/Z (lanes 0-15, 16 bytes each): one more load per tile.
+    // Tile u (documents: kept tile u of the list) -> stage u % NST.  Waves 0
+    // and 1 also bring the tile's -delta and 1/Z, wave 2 (documents) its
+    // query document ids (lanes 0-15, 16 bytes each): one more load per tile.
+    constexpr int kRowLoaders = DOC ? 3 : 2;
     auto issue = [&](int u) __attribute__((always_inline)) {
         uint8_t* sb = smem + (u % NST) * SB;
-        const int i0 = q_lo + u * BQ;
+        int i0 = q_lo + u * BQ;
+        if constexpr (DOC) i0 = q_lo + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BQ;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
@@ -485,6 +594,8 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 dma_load16(rdl, la, (i0 + 4 * lane) * 4);
             else if (wave == 1)
                 dma_load16(rzi, la, (i0 + 4 * lane) * 4);
+            else if (DOC && wave == 2)
+                dma_load16(rdoc, la, (i0 + 4 * lane) * 4);
         }
     };
 
@@ -538,9 +649,14 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
 
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the lane's key document id (INT_MIN past T); per tile,
+    // whether this wave tests it per element.
+    const int kdoc = (DOC && key < T) ? docb[key] : INT_MIN;
+    bool dmw = true;
     // Per 32-query half nb of a tile (queries i0 + nb * 32 + 8 (r / 4) +
     // 4 g + r % 4 for register r; one key per lane):
     //   S   = Q K'^T                  (A = Q rows)
@@ -617,6 +733,21 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 }
             }
             return;
+        }
+        if constexpr (decltype(m)::value == kDocm) {
+            // Masked before the lane's key (causal) or in another document.
+            if (dmw) {
+                const int lim = kCaus ? qbase - key : INT_MAX / 2;
+                const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int4 d4 = *reinterpret_cast<const int4*>(qd + nb * 32 + 8 * i + 4 * g);
+                    const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (8 * i + k + lim < 0 || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                }
+            }
         }
         if constexpr (decltype(m)::value == kMasked) {
             // Register r (query qbase + off) is masked before the lane's key
@@ -711,6 +842,65 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     // Pipeline as in the dQ kernel.  The stationary operands are pinned in
     // AGPRs (MFMA reads its A/B operands from either file), leaving the
     // VGPRs to the phases' operand buffers.
+    if constexpr (DOC) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(kr[ks]), "+a"(vr[ks]));
+        // Document range of this wave's valid keys (uniform; kone: one
+        // document) and of the whole block.
+        int klo = key < T ? kdoc : INT_MAX, khi = key < T ? kdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            klo = min(klo, __shfl_xor(klo, off));
+            khi = max(khi, __shfl_xor(khi, off));
+        }
+        klo = __builtin_amdgcn_readfirstlane(klo);
+        khi = __builtin_amdgcn_readfirstlane(khi);
+        const bool kone = klo == khi;
+        if (lane == 0) {
+            s_rng[2 * wave] = klo;
+            s_rng[2 * wave + 1] = khi;
+        }
+        __syncthreads();
+        int bk_lo = INT_MAX, bk_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bk_lo = min(bk_lo, s_rng[2 * w]);
+            bk_hi = max(bk_hi, s_rng[2 * w + 1]);
+        }
+        // The kept query tiles of each chunk of candidates through the same
+        // pipeline.  Per tile and wave: nothing to do when the tile ends
+        // before the wave's first key or is one document none of its keys
+        // belongs to; no per-element test when it starts after the wave's
+        // last key and is one document that all of them belong to.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BQ>(docb, T, q_lo, c0, min(CAP, ntiles - c0), bk_lo, bk_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            if (n > 1) issue(1);
+            for (int u = 0; u < n; ++u) {
+                if (u + 1 < n) {
+                    if (wave < kRowLoaders)
+                        wait_vmcnt<2 * LPW + 1>();
+                    else
+                        wait_vmcnt<2 * LPW>();
+                } else {
+                    wait_vmcnt<0>();
+                }
+                __syncthreads();
+                if (u + 2 < n) issue(u + 2);
+                int soff = (u % NST) * SB;
+                asm volatile("" : "+s"(soff));
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int i0 = q_lo + (e & ~kDocOne) * BQ;
+                const bool one = (e & kDocOne) != 0;
+                const bool vis = !(kCaus && i0 + BQ - 1 < kw0) && !(one && (td < klo || td > khi));
+                dmw = (kCaus && i0 < kw0 + 31) || !(one && kone && td == klo);
+                if (vis) tile(smem + soff, i0, Docm{});
+            }
+            __syncthreads();  // the list and the ring are reused by the next chunk
+        }
+    } else {
     if (ntiles > 0) issue(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(kr[ks]), "+a"(vr[ks]));
@@ -741,6 +931,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
+    }
 
     // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre),
     // packed and staged, one output at a time, in this wave's own 32 rows of
@@ -805,17 +996,18 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 
 // The D == 128 backward: dQ (and the workspace), dK/dV, then dscale from the
 // dQ kernel's per-workgroup sums.
-template <class E, int MODE, bool PAD = false>
+// DOC: document ids (no window) on the same kernels' document mode.
+template <class E, int MODE, bool PAD = false, bool DOC = false>
 hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0,
-                       st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD, DOC>), dim3(nq * BH),
+                       dim3(BwdD128Cfg::NW * 64), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD>), dim3(nk * BH), dim3(BwdD128Cfg::NWK * 64),
-                       0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD, DOC>), dim3(nk * BH),
+                       dim3(BwdD128Cfg::NWK * 64), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
                        st, a, (int)(nq * BH));

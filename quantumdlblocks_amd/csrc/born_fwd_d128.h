@@ -40,10 +40,22 @@
 // the buffer's range, so they land in LDS as zeros, and the output chunks
 // past D are not stored.  The arithmetic is that of D == 128 with zero
 // columns (which add nothing to any overlap).
+//
+// DOC: document ids (no window; flash_born.py:145-147, 175-177), one 256-row
+// block per workgroup.  The block's candidate key tiles are screened by
+// document-id range into a list in LDS (as the D == 64 document kernels do)
+// and only the kept tiles go through the ring, each with its 64 key ids.  Per
+// tile a wave skips the work when the tile lies past its rows or is one
+// document none of its rows belongs to, and tests the tile per element
+// (document and causal) unless the tile is before its first row and one
+// document all of its rows belong to.  Q goes straight from HBM into
+// registers, and the output rows are staged in the idle ring, so the 64 KiB
+// Q block is not needed.
 #pragma once
 
 #include <type_traits>
 
+#include "born_bwd_fast.h"
 #include "born_common.h"
 #include "born_fwd_fast.h"
 #include "purified_args.h"
@@ -61,11 +73,12 @@ struct FwdD128Cfg {
 // Offset sent to a buffer load that must return zeros (past every range).
 constexpr int kBufOOB = 0x7ffffff0;
 
-template <class E, int MODE, bool PUR = false, bool PAD = false>
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
+    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!DOC || (MODE != kWindow && !PUR && !PAD), "documents: Born, D == 128, no window");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
     constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
@@ -83,7 +96,12 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 
     __shared__ __attribute__((aligned(1024))) uint8_t k_lds[NST * TB];
     __shared__ __attribute__((aligned(1024))) uint8_t v_lds[NST * TB];
-    __shared__ __attribute__((aligned(1024))) uint8_t q_lds[QB];
+    __shared__ __attribute__((aligned(1024))) uint8_t q_lds[DOC ? 16 : QB];
+    // Documents: key document ids per stage, the kept-tile list and screening scratch.
+    constexpr int CAP = 256;  // candidate tiles screened per pass
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[DOC ? 2 * NW + 1 : 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -137,8 +155,12 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 
     // Tile u of the workgroup's sequence -> stage st: wave-instruction i
     // writes LDS slots (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
     auto issue = [&](int u, int st) __attribute__((always_inline)) {
-        const int key0 = (u < nt_a ? tb_a + u : tb_b + (u - nt_a)) * BN;
+        int key0 = (u < nt_a ? tb_a + u : tb_b + (u - nt_a)) * BN;
+        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -150,6 +172,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), (PAD && kc >= CG) ? kBufOOB : off + (kc << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
+        // Documents: this wave's 8 of the tile's key ids (lanes 0-1).
+        if constexpr (DOC)
+            if (lane < 2) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 8), (key0 + wave * 8 + lane * 4) * 4);
     };
     auto issue_q = [&](int mb) __attribute__((always_inline)) {
 #pragma unroll
@@ -192,9 +217,16 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 
     // Tile forms, passed as integral constants: kFull (no mask) or kMasked
     // (key past the row, or before its window, zeroed per element).
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the row's id (INT_MIN past T); per tile, whether this wave
+    // tests it per element (dmw), its first key and the stage's key ids.
+    int qdoc = INT_MIN;
+    bool dmw = true;
+    int dkey0 = 0;
+    const int32_t* kdp = kd_lds;
 
     // Elementwise pass over one 32-key half of S^T (lane: query c, keys
     // kbase + 8 (r / 4) + r % 4): p' = relu(x|x|) packed, z += p'.  Masked
@@ -236,6 +268,21 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
                 if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
+            }
+        }
+        if constexpr (decltype(m)::value == kDocm) {
+            // Masked past the row (causal) or in another document.
+            if (dmw) {
+                const int lim = kCaus ? qrow - kbase : INT_MAX;
+                const int32_t* kd = kdp + (kbase - dkey0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int4 d4 = *reinterpret_cast<const int4*>(kd + 8 * i);
+                    const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (8 * i + k > lim || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                }
             }
         }
 #pragma unroll
@@ -373,12 +420,15 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 opk[db][j][1] = E::pack(o[4 * j + 2] * rcp, o[4 * j + 3] * rcp);
             }
     };
+    // Output staging: this wave's rows of the Q block (documents: its 32 rows
+    // of the idle ring, waves 0-3 in the K ring, 4-7 in the V ring).
+    uint8_t* const stg = DOC ? (wave < 4 ? k_lds : v_lds) + 32 * (wave & 3) * RB : q_lds + 32 * wave * RB;
     auto put_lds = [&]() __attribute__((always_inline)) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
-        const int row = 32 * wave + (ln & 31);
+        const int row = ln & 31;  // of the wave's 32 (row & 15 as for the block row)
         const int gg = ln >> 5;
-        uint8_t* rb = q_lds + row * RB;
+        uint8_t* rb = stg + row * RB;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -395,9 +445,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         const int chunk = ln & 15;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int row = 32 * wave + 4 * i + (ln >> 4);
-            const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 15)) << 4));
-            const int qi = mb * BM + row;
+            const int row = 4 * i + (ln >> 4);
+            const u32x4 x = *reinterpret_cast<const u32x4*>(stg + row * RB + ((chunk ^ (row & 15)) << 4));
+            const int qi = mb * BM + 32 * wave + row;
             if (qi < T && (!PAD || chunk < CG))
                 __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * D + chunk * 8));
         }
@@ -454,6 +504,83 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
         if (!PUR && nitems == 2 && u == nt_a + 1) flush(mb_a);
     };
+
+    if constexpr (DOC) {
+        // One block (unpaired launch).  Q rows straight into registers, the
+        // sign of the scale folded in.
+        start_item(mb_a);
+        {
+            const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 x = {0u, 0u, 0u, 0u};
+                if (qrow < T) x = ldg16(Qg + (size_t)qrow * DP + (2 * ks + g) * 8);
+                qr[ks] = x ^ flip;
+            }
+            if (qrow < T) qdoc = docb[qrow];
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
+        // Document range of this wave's valid rows (uniform; wone: one
+        // document) and of the whole block.
+        const int rw = mb_a * BM + 32 * wave;
+        int wlo = qrow < T ? qdoc : INT_MAX, whi = qrow < T ? qdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            wlo = min(wlo, __shfl_xor(wlo, off));
+            whi = max(whi, __shfl_xor(whi, off));
+        }
+        wlo = __builtin_amdgcn_readfirstlane(wlo);
+        whi = __builtin_amdgcn_readfirstlane(whi);
+        const bool wone = wlo == whi;
+        if (lane == 0) {
+            s_rng[2 * wave] = wlo;
+            s_rng[2 * wave + 1] = whi;
+        }
+        __syncthreads();
+        int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_rng[2 * w]);
+            bq_hi = max(bq_hi, s_rng[2 * w + 1]);
+        }
+        constexpr int kDocTileLoads = 2 * LPW + 1;  // K, V and 8 key ids per wave
+        const int ncand = nt_a;
+        for (int c0 = 0; c0 < ncand; c0 += CAP) {
+            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ncand - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0, 0);
+            if (n > 1) issue(1, 1);
+            for (int u = 0; u < n; ++u) {
+                if (u + 1 < n)
+                    wait_vmcnt<kDocTileLoads>();
+                else
+                    wait_vmcnt<0>();
+                __syncthreads();
+                if (u + 2 < n) issue(u + 2, (u + 2) % NST);
+                int soff = (u % NST) * TB;  // opaque: operand addresses formed per tile
+                asm volatile("" : "+s"(soff));
+                const uint8_t* kb = k_lds + soff;
+                const uint8_t* vb = v_lds + soff;
+                kdp = kd_lds + (soff / TB) * BN;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                dkey0 = (e & ~kDocOne) * BN;
+                const bool one = (e & kDocOne) != 0;
+                const bool vis = !(kCaus && dkey0 > rw + 31) && !(one && (td < wlo || td > whi));
+                dmw = (kCaus && dkey0 + BN - 1 > rw) || !(one && wone && td == wlo);
+                if (vis) {
+                    read_k(kop, kb, 0);
+                    tile(kb, vb, dkey0, Docm{});
+                }
+            }
+            __syncthreads();  // the list and the ring are reused by the next chunk (or the output)
+        }
+        pack();
+        put_lds();
+        flush(mb_a);
+        return;
+    }
 
     issue_q(mb_a);
     issue(0, 0);
@@ -563,6 +690,16 @@ inline bool d128_fwd_paired(int B, int H, int T, bool causal) {
         return rounds * 4 * (nmb + 1) <= (total + S - 1) / S + 4;
     }
     return rounds * 2 * nt <= (BH * nmb + S - 1) / S * nt;
+}
+
+// Documents (no window): one block per workgroup, the longest key ranges
+// first under causality.
+template <class E, int MODE>
+hipError_t launch_fwd16_d128_doc(const FwdArgs& a, hipStream_t st) {
+    using C = FwdD128Cfg;
+    const dim3 grid((unsigned)fast_fwd_nmb(a.T, C::BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, false, true>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
 }
 
 template <class E, int MODE, bool PAD = false>

@@ -264,6 +264,45 @@ def test_bwd_documents_fast_kernels(cuda_device, dtype, is_causal):
                check_dscale=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_bwd_d128_documents(cuda_device, dtype, is_causal):
+    """D = 128 with document ids (no window) runs the document mode of the
+    D = 128 dQ and dK/dV kernels: geometric documents, per-head scales (one
+    negative) and dscale; document edges on and beside the wave slices,
+    tiles and blocks, one-token documents, negative ids, a descending row;
+    unsorted ids."""
+    doc = orc.geometric_doc_ids(2, 1100, 90.0, seed=3)
+    _check_bwd(2, 3, 1100, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=[0.3, -0.2, 0.1],
+               std=0.7, check_dscale=True)
+    lens = [64, 1, 63, 129, 256, 1, 1, 31, 97, 200, 65, 12, 33, 32, 288]
+    ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
+    _check_bwd(2, 2, ids.size, 128, dtype, cuda_device, is_causal=is_causal, doc=np.stack([ids, -ids[::-1]]),
+               scale=0.2, std=0.7, seed=5)
+    rng = np.random.default_rng(8)
+    doc = rng.integers(0, 3, size=(1, 600)).astype(np.int32)
+    _check_bwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=8)
+
+
+def test_bwd_d128_documents_many_chunks(cuda_device):
+    """D = 128: more candidate tiles than one screening pass holds (256 key
+    tiles in dQ, 256 query tiles in dK/dV), sorted documents with one longer
+    than a pass."""
+    T = 17000
+    doc = np.zeros((1, T), dtype=np.int32)
+    doc[0, 3000:12000] = 1
+    doc[0, 12000:] = 2 + orc.geometric_doc_ids(1, T - 12000, 700.0, seed=11)[0]
+    _check_bwd(1, 1, T, 128, torch.bfloat16, cuda_device, doc=doc, scale=0.5, std=0.5, seed=11)
+
+
+def test_bwd_d128_config_c4_documents(cuda_device):
+    """C4's documents at head dim 128 with the backward (dc4b: B4 H8 T8192
+    D128); 8 heads, document by document."""
+    doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
+    _check_bwd(4, 8, 8192, 128, torch.bfloat16, cuda_device, doc=doc, scale=1.0, std=0.3,
+               heads=[(b, (3 * b + j) % 8) for b in range(4) for j in range(2)])
+
+
 def test_bwd_documents_fast_many_chunks_causal(cuda_device):
     """More candidate tiles than one screening pass holds (256 key tiles in
     dQ, 128 query tiles in dK/dV): a 17000-token row of sorted documents, one

@@ -259,6 +259,58 @@ def test_fwd_documents_many_tiles(cuda_device, T, D):
     assert worst <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("is_causal", [True, False])
+def test_fwd_d128_documents(cuda_device, dtype, is_causal):
+    """D = 128 with document ids (no window) runs the D = 128 kernel's
+    document mode: geometric documents with T not a multiple of the tile or
+    block, per-head scales (one negative); documents whose edges sit on and
+    beside the 32-row wave slices, 64-key tiles and 256-row blocks, one-token
+    documents, negative ids and a descending batch row; unsorted ids."""
+    doc = orc.geometric_doc_ids(2, 1100, 90.0, seed=3)
+    _check_fwd(2, 3, 1100, 128, dtype, cuda_device, is_causal=is_causal, doc=doc,
+               scale=np.array([0.3, -0.2, 0.1], np.float32), std=0.7, seed=3)
+    lens = [64, 1, 63, 129, 256, 1, 1, 31, 97, 200, 65, 12, 33, 32, 288]
+    ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
+    _check_fwd(2, 2, ids.size, 128, dtype, cuda_device, is_causal=is_causal, doc=np.stack([ids, -ids[::-1]]),
+               scale=0.2, std=0.7, seed=5)
+    rng = np.random.default_rng(7)
+    doc = rng.integers(0, 3, size=(1, 600)).astype(np.int32)
+    _check_fwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=7)
+
+
+def test_fwd_d128_documents_many_tiles(cuda_device):
+    """D = 128, sorted documents over more candidate key tiles than one
+    screening pass holds (256 tiles): every document against the oracle on
+    its own span."""
+    from quantumdlblocks_amd import flash_born_attention
+
+    T, D = 17000, 128
+    doc = np.zeros((1, T), dtype=np.int32)
+    doc[0, 3000:12000] = 1
+    doc[0, 12000:] = 2 + orc.geometric_doc_ids(1, T - 12000, 700.0, seed=11)[0]
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((1, 2, T, D), seed=9, std=0.3, dtype=torch.bfloat16))
+    out = flash_born_attention(q, k, v, 1.0, doc_ids=torch.as_tensor(doc, device=cuda_device))
+    got = f64(out)
+    qn, kn, vn = f64(q), f64(k), f64(v)
+    ids = doc[0]
+    starts = np.flatnonzero(np.r_[True, ids[1:] != ids[:-1]])
+    ends = np.r_[starts[1:], T]
+    worst = 0.0
+    for s, e in zip(starts, ends):
+        ref, _ = orc.forward(qn[:, :, s:e], kn[:, :, s:e], vn[:, :, s:e], 1.0, True, 1e-12)
+        worst = max(worst, rel_err(got[:, :, s:e], ref))
+    print(f"documents T={T} D={D}: {len(starts)} docs, worst rel={worst:.3e}", flush=True)
+    assert worst <= 2e-2
+
+
+def test_fwd_d128_config_c4_documents(cuda_device):
+    """C4's documents at head dim 128 (dc4: B4 H8 T8192 D128); 16 heads."""
+    doc = orc.geometric_doc_ids(4, 8192, 512.0, seed=0)
+    sel = [(b, (3 * b + j) % 8) for b in range(4) for j in range(4)]
+    _check_fwd(4, 8, 8192, 128, torch.bfloat16, cuda_device, doc=doc, scale=1.0, std=128 ** -0.5, heads=sel)
+
+
 def test_fwd_document_and_window(cuda_device):
     doc = orc.geometric_doc_ids(2, 333, 60.0, seed=2)
     _check_fwd(2, 4, 333, 64, torch.bfloat16, cuda_device, window_size=37, doc=doc)
