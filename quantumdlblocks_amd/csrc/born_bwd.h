@@ -348,13 +348,18 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 //   S   = Q K'^T          (C layout: one key per lane, 16 queries per block)
 //   dPz = dO V^T - delta  (accumulator initialised with -delta)
 //   t = relu(S) / Z_i;  dV^T += dO^T (t relu(S)),  dK^T += Q^T (t dPz)
+// CS column splits: with CS == 2 two workgroups share a key block, each
+// forming S and dPz over the whole head dim but accumulating dK, dV for half
+// of its columns (the wide head dims' full accumulators and stationary rows
+// exceed even one wave's 512 registers).
 // ---------------------------------------------------------------------------
-template <class E, int DP, int NW, int BQ, int MODE, int WPE>
+template <class E, int DP, int NW, int BQ, int MODE, int WPE, int CS = 1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void born_bwd_dkdv16_kernel(BwdArgs p) {
     constexpr int BK = NW * 32;
     constexpr int KS = DP / 16;
-    constexpr int DB = DP / 32;
+    constexpr int DBF = DP / 32;                // column blocks of the head dim
+    constexpr int DB = (DBF + CS - 1) / CS;     // column blocks accumulated here (at most)
     constexpr int NQ = BQ / 32;
     constexpr int NT = NW * 64;
     constexpr int RS = DP + 8;
@@ -377,10 +382,13 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     const int window = (MODE == kGeneral) ? p.window : 0;
     const bool has_doc = kDoc && p.doc != nullptr;
 
-    // Key blocks in ascending order: under causality the first sees the most queries.
-    const int bid = blockIdx.x;
+    // Key blocks in ascending order: under causality the first sees the most
+    // queries.  Column split: workgroups bid and bid + 1 share a key block.
+    const int cs = (CS > 1) ? (int)(blockIdx.x % CS) : 0;
+    const int bid = blockIdx.x / CS;
     const int bh = bid % BH;
     const int kb = bid / BH;
+    const int db0 = cs * DB;  // first column block accumulated here
     const int b = bh / p.H, h = bh % p.H;
     const int k0 = kb * BK;
     const int tid = threadIdx.x;
@@ -552,7 +560,8 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
                     const u32x4 bu = {u2[4 * hh], u2[4 * hh + 1], u2[4 * hh + 2], u2[4 * hh + 3]};
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
-                        const int off = (db * 32 + c) * TS + qs * 32 + hh * 16 + g * 4;
+                        if (DBF % CS != 0 && db0 + db >= DBF) break;  // the last split's short share
+                        const int off = ((db0 + db) * 32 + c) * TS + qs * 32 + hh * 16 + g * 4;
                         const u32x2 dlo = *reinterpret_cast<const u32x2*>(&dt_lds[buf][off]);
                         const u32x2 dhi = *reinterpret_cast<const u32x2*>(&dt_lds[buf][off + 8]);
                         const u32x2 qlo = *reinterpret_cast<const u32x2*>(&qt_lds[buf][off]);
@@ -578,7 +587,7 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int d = db * 32 + 8 * j + 4 * g;
+                const int d = (db0 + db) * 32 + 8 * j + 4 * g;
                 if (d < D) {
                     u32x2 wk, wv;
                     wk[0] = E::pack(dk[db][4 * j] * fk, dk[db][4 * j + 1] * fk);
@@ -1051,6 +1060,10 @@ struct Bwd16Cfg {
     static constexpr int DQ_WPE = DP <= 64 ? 2 : 1;
     static constexpr int KV_BQ = DP <= 64 ? 64 : 32;
     static constexpr int KV_WPE = DP <= 64 ? 2 : 1;
+    // dK/dV column splits: at DP >= 192 (64-305 spills unsplit; B8 T2048:
+    // D = 256 step 1914 -> 1098 us, D = 192 1414 -> 1202); DP = 160 spills
+    // little unsplit and runs faster so (1088 against 1379 us).
+    static constexpr int KV_CS = DP >= 192 ? 2 : 1;
     static constexpr int NW = 4;
 };
 
@@ -1158,8 +1171,8 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     if (!fast && (e = launch_bwd_common_pre<E, false>(a, st)) != hipSuccess) return e;
     if (!fast) {
         constexpr int BK = C::NW * 32;
-        const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH);
-        hipLaunchKernelGGL((born_bwd_dkdv16_kernel<E, DP, C::NW, C::KV_BQ, MODE, C::KV_WPE>), grid,
+        const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH * C::KV_CS);
+        hipLaunchKernelGGL((born_bwd_dkdv16_kernel<E, DP, C::NW, C::KV_BQ, MODE, C::KV_WPE, C::KV_CS>), grid,
                            dim3(C::NW * 64), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }

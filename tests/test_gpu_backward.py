@@ -145,6 +145,19 @@ def test_bwd_head_dims(cuda_device, D, dtype):
     _check_bwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
 
 
+@pytest.mark.parametrize("D", [160, 224, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["causal", "dense", "window", "documents"])
+def test_bwd_wide_head_dims_column_split(cuda_device, D, dtype, mode):
+    """Wide head dims (16-bit): D >= 192 runs two dK/dV workgroups per key
+    block, each holding half of the column blocks (seven split unevenly at
+    D = 224), D = 160 one; several key blocks and query tiles, every mask
+    mode, per-head scales, dscale."""
+    kw = dict(is_causal=mode != "dense", window_size=90 if mode == "window" else 0,
+              doc=orc.geometric_doc_ids(2, 300, 60.0, seed=D) if mode == "documents" else None)
+    _check_bwd(2, 2, 300, D, dtype, cuda_device, scale=[0.2, -0.1], std=0.5, seed=D + 1, check_dscale=True, **kw)
+
+
 def test_bwd_head_dim_above_256_takes_the_eager_path(cuda_device):
     """D > 256: autograd through the reference's eager formulation on the GPU
     (flash_born.py:670-690), gradients against the oracle."""
