@@ -75,8 +75,9 @@ CONFIGS.update({
     # purified-Born attention at head dim 128 on the same work
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
+    "pdc4b": (4, 8, 8192, 128, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
 })
-PURIFIED |= {"pd3", "pd5"}
+PURIFIED |= {"pd3", "pd5", "pdc4b"}
 WINDOW = {"w3": 256, "w5": 512}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.

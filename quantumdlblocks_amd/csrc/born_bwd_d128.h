@@ -52,7 +52,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || (MODE != kWindow && !PUR), "documents: Born, no window");
+    static_assert(!DOC || MODE != kWindow, "documents: no window");
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -280,6 +280,22 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             // relu(-gamma tau) > 0 for tau < 0).  Keys past T need no mask
             // here: their K rows (zero) multiply U.
             const int lim = qrow - kbase;
+            // Documents: bit r set for a register masked by the diagonal
+            // (causal) or another document.
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int dlim = kCaus ? lim : INT_MAX;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > dlim || dk[k] != qdoc) dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 float w[2];
@@ -293,6 +309,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     float d = f * fmaf(t[r], zinv, nd);
                     if constexpr (decltype(m)::value == kMasked)
                         if (8 * (r >> 2) + (r & 3) > lim) d = 0.f;
+                    if constexpr (decltype(m)::value == kDocm)
+                        if ((dmask >> r) & 1u) d = 0.f;
                     w[e] = d;
                 }
                 pk[j] = E::pack(w[0], w[1]);
@@ -480,7 +498,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || (MODE != kWindow && !PUR), "documents: Born, no window");
+    static_assert(!DOC || MODE != kWindow, "documents: no window");
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -703,9 +721,25 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                            uint32_t (&u2)[8], auto m) __attribute__((always_inline)) {
         const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
         if constexpr (PUR) {
-            // Masked pairs (query before the lane's key) weigh zero; queries
-            // past T have 1/Z = 0 from the workspace read.
+            // Masked pairs (query before the lane's key; documents: in
+            // another document) weigh zero; queries past T have 1/Z = 0 from
+            // the workspace read.
             const int lim = qbase - key;
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int dlim = kCaus ? lim : INT_MAX / 2;
+                    const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(qd + nb * 32 + 8 * i + 4 * g);
+                        const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k + dlim < 0 || dq[k] != kdoc) dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
@@ -720,6 +754,8 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         float bb = __int_as_float(max(__float_as_int(x), 0));
                         if constexpr (decltype(m)::value == kMasked)
                             if (8 * (r >> 2) + (r & 3) + lim < 0) u = bb = 0.f;
+                        if constexpr (decltype(m)::value == kDocm)
+                            if ((dmask >> r) & 1u) u = bb = 0.f;
                         const float u2_ = u * u;
                         const float dpz = dp[r] * z4[k + e];
                         const float a = u2_ * u * dpz;
@@ -1017,16 +1053,16 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
 // The purified D == 128 backward (bf16, dense or causal): dQ (and the
 // workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
 // partials (one per dK/dV workgroup).
-template <int MODE, bool PAD = false>
+template <int MODE, bool PAD = false, bool DOC = false>
 hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true, PAD>), dim3(nq * BH), dim3(BwdD128Cfg::NW * 64), 0,
-                       st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true, PAD, DOC>), dim3(nq * BH),
+                       dim3(BwdD128Cfg::NW * 64), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true, PAD>), dim3(nk * BH),
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true, PAD, DOC>), dim3(nk * BH),
                        dim3(BwdD128Cfg::NWK * 64), 0, st, a);
     return hipGetLastError();
 }

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || (MODE != kWindow && !PUR && !PAD), "documents: Born, D == 128, no window");
+    static_assert(!DOC || (MODE != kWindow && !PAD), "documents: D == 128, no window");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
     constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
@@ -235,8 +235,23 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     auto elementwise = [&](f32x16& s, uint32_t (&pk)[8], uint32_t (&pl)[PW], auto m, int kbase)
         __attribute__((always_inline)) {
         if constexpr (PUR) {
-            // Weights zeroed past the row (causal) or past T (dense).
+            // Weights zeroed past the row (causal) or past T (dense), and
+            // (documents) in another document: bit r of dmask for register r.
             const int lim = (kCaus ? qrow : T - 1) - kbase;
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int32_t* kd = kdp + (kbase - dkey0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kd + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > lim || dk[k] != qdoc) dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 float w[2];
@@ -252,6 +267,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                         const int r = 2 * j + e;
                         if (8 * (r >> 2) + (r & 3) > lim) pw = 0.f;
                     }
+                    if constexpr (decltype(m)::value == kDocm)
+                        if ((dmask >> (2 * j + e)) & 1u) pw = 0.f;
                     w[e] = pw;
                 }
                 zacc[0] += w[0] + w[1];
@@ -568,7 +585,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 dkey0 = (e & ~kDocOne) * BN;
                 const bool one = (e & kDocOne) != 0;
                 const bool vis = !(kCaus && dkey0 > rw + 31) && !(one && (td < wlo || td > whi));
-                dmw = (kCaus && dkey0 + BN - 1 > rw) || !(one && wone && td == wlo);
+                dmw = (kCaus && dkey0 + BN - 1 > rw) || !(one && wone && td == wlo) || (PUR && dkey0 + BN > T);
                 if (vis) {
                     read_k(kop, kb, 0);
                     tile(kb, vb, dkey0, Docm{});
@@ -576,9 +593,13 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             }
             __syncthreads();  // the list and the ring are reused by the next chunk (or the output)
         }
-        pack();
-        put_lds();
-        flush(mb_a);
+        if constexpr (PUR) {
+            store_pur(mb_a);
+        } else {
+            pack();
+            put_lds();
+            flush(mb_a);
+        }
         return;
     }
 
@@ -712,6 +733,15 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
     const bool pair = MODE != kWindow && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
     const dim3 grid(pair ? npair : nsingle);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
+}
+
+// Purified-Born forward with document ids (bf16, D == 128, no window).
+template <int MODE>
+hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
+    using C = FwdD128Cfg;
+    const dim3 grid((unsigned)fast_fwd_nmb(a.T, C::BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, false, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

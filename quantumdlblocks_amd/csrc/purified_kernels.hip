@@ -23,6 +23,11 @@ inline bool purified_d128_ok(const PurArgs& a) {
     return a.D > 64 && a.D <= 128 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
+// D == 128 with document ids (no window): the D = 128 kernels' document mode.
+inline bool purified_d128_doc_ok(const PurArgs& a) {
+    return a.D == 128 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+}
+
 inline bool purified_doc_fast_ok(const PurArgs& a) {
     return a.D == 64 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
@@ -38,6 +43,9 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
             return a.is_causal ? launch_purified_fwd_d128<kCausal>(a, s) : launch_purified_fwd_d128<kDense>(a, s);
         return a.is_causal ? launch_purified_fwd_d128<kCausal, true>(a, s) : launch_purified_fwd_d128<kDense, true>(a, s);
     }
+    // bf16, D = 128, document ids without a window: its document mode.
+    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
+        return a.is_causal ? launch_purified_fwd_d128_doc<kCausal>(a, s) : launch_purified_fwd_d128_doc<kDense>(a, s);
     // bf16, D = 64, document ids without a window: the document kernel's
     // purified mode.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) return launch_purified_fwd_doc(a, s);
@@ -69,9 +77,11 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
 
 // bf16, 64 < D <= 128, dense or causal: the D = 128 dQ and dK/dV kernels' purified
 // mode, then the same reduction.
-template <int MODE>
+template <int MODE, bool DOC = false>
 static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
-    hipError_t e = a.D == 128 ? launch_purified_bwd_d128<MODE>(a, s) : launch_purified_bwd_d128<MODE, true>(a, s);
+    hipError_t e = DOC           ? launch_purified_bwd_d128<MODE, false, DOC>(a, s)
+                   : a.D == 128 ? launch_purified_bwd_d128<MODE>(a, s)
+                                : launch_purified_bwd_d128<MODE, true>(a, s);
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 128);
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
@@ -85,6 +95,8 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
         return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
+    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
+        return a.is_causal ? purified_bwd_d128<kCausal, true>(a, s) : purified_bwd_d128<kDense, true>(a, s);
     // bf16, D = 64, document ids without a window: the same kernels' document
     // variants.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))

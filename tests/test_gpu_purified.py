@@ -88,7 +88,7 @@ def test_purified_forward_backward(cuda_device, case):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
     """Arbitrary (unsorted, repeating) document ids, tau < 0 (masked pairs
@@ -101,15 +101,16 @@ def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("is_causal", [True, False])
-def test_purified_document_tile_edges(cuda_device, dtype, is_causal):
+def test_purified_document_tile_edges(cuda_device, dtype, D, is_causal):
     """Sorted documents with edges on and next to the 32- and 64-row tile
     edges, one-token documents, negative ids, one batch row in descending
     order, and tau < 0."""
-    lens = [64, 1, 63, 129, 32, 1, 1, 31, 97, 65, 12, 33]
+    lens = [64, 1, 63, 129, 32, 1, 1, 31, 97, 65, 12, 33, 256, 3]
     ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
     doc = np.stack([ids, -ids[::-1]])
-    _check_pur((2, 2, ids.size, 64, dtype, dict(is_causal=is_causal), [8.0, 4.0], [-0.05, 0.1], 0.3), cuda_device,
+    _check_pur((2, 2, ids.size, D, dtype, dict(is_causal=is_causal), [8.0, 4.0], [-0.05, 0.1], 0.3), cuda_device,
                doc)
 
 
@@ -275,6 +276,49 @@ def test_purified_d128_padded_head_dims(cuda_device, D, causal):
         got, gen, want, m = f64(fast[1 + i]), f64(generic[1 + i]), ref[i], mag[i]
         ef = max_abs(got, want) / m.max()
         assert rel_err(got, want) <= 2e-2 or ef <= 1e-4, (name, rel_err(got, want), ef)
+        assert rel_err(got, gen) <= 5e-3 or max_abs(got, gen) / m.max() <= 1e-4, (name, rel_err(got, gen))
+    for name, got, gen, want, m in (("dscale", fast[4], generic[4], ref[3], mag[3]),
+                                    ("dtau", fast[5], generic[5], ref[4], mag[4])):
+        got, gen = np.atleast_1d(f64(got)), np.atleast_1d(f64(gen))
+        ok = (np.abs(got - want) <= 2e-2 * np.abs(want)) | (np.abs(got - want) <= 1e-4 * m)
+        assert ok.all(), (name, got, want, m)
+        ok = (np.abs(got - gen) <= 5e-3 * np.abs(gen)) | (np.abs(got - gen) <= 1e-4 * m)
+        assert ok.all(), (name, got, gen)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_purified_d128_documents(cuda_device, causal):
+    """bf16, D = 128 with document ids: the D = 128 kernels' purified
+    document mode; tau < 0 (masked pairs weigh zero only if zeroed), T not a
+    multiple of the tile or block, per-head gamma and tau; forward (fp32
+    output) against the oracle and the fp32-MFMA kernels to 1e-4, gradients,
+    dgamma and dtau against both to the bf16 bars."""
+    B, H, T, D = 2, 2, 1100, 128
+    print(f"purified d128 documents causal={causal}", flush=True)
+    docs = orc.geometric_doc_ids(B, T, 90.0, seed=5)
+    doc_t = torch.tensor(docs, dtype=torch.int32, device=cuda_device)
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=23, std=0.2, n=4,
+                                                              dtype=torch.bfloat16))
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    o32, z32 = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8, doc=doc_t)
+    o32g, z32g = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8, doc=doc_t, window=T + 1)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, causal,
+                                        1e-8, 0, docs)
+    assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
+    assert rel_err(f64(o32), f64(o32g)) <= 1e-4
+    assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    kw = dict(eps_base=0.05, is_causal=causal, eps=1e-8)
+    fast = _run(q, k, v, do, sc, ta, doc_ids=doc_t, **kw)
+    generic = _run(q, k, v, do, sc, ta, doc_ids=doc_t, window_size=T + 1, **kw)
+    okw = dict(kw, window_size=0, doc_ids=docs)
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do), **okw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do),
+                                           **okw)
+    for i, name in enumerate(("dq", "dk", "dv")):
+        got, gen, want, m = f64(fast[1 + i]), f64(generic[1 + i]), ref[i], mag[i]
+        assert rel_err(got, want) <= 2e-2 or max_abs(got, want) / m.max() <= 1e-4, (name, rel_err(got, want))
         assert rel_err(got, gen) <= 5e-3 or max_abs(got, gen) / m.max() <= 1e-4, (name, rel_err(got, gen))
     for name, got, gen, want, m in (("dscale", fast[4], generic[4], ref[3], mag[3]),
                                     ("dtau", fast[5], generic[5], ref[4], mag[4])):
