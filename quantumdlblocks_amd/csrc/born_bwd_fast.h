@@ -128,10 +128,13 @@ __device__ int screen_doc_tiles(const int32_t* __restrict__ docb, int T, int row
 // `.to(k.dtype)` rounds it; O is the forward's fp32 output.  The dscale
 // closed form is Born's only: the purified dgamma / dtau come from the dK/dV
 // kernel.
-template <class E, int DP, int MODE, bool PUR = false, bool DOC = false>
+// PAD (purified only): a head dim D < 64 (a multiple of 8), as in the
+// forward: chunks past D load as zeros and are not stored.
+template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
+    static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
@@ -179,7 +182,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // Rows: column c of block qb -> row R + 128 qb + 64 (c / 16) + 16 wave + c % 16.
     const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
@@ -230,9 +236,9 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
-                if (ok) {
-                    x = ldg16(Qg + (size_t)qi * DP + (2 * ks + g) * 8);
-                    y = ldg16(dOg + (size_t)qi * DP + (2 * ks + g) * 8);
+                if (ok && (!PAD || 2 * ks + g < CG)) {
+                    x = ldg16(Qg + (size_t)qi * D + (2 * ks + g) * 8);
+                    y = ldg16(dOg + (size_t)qi * D + (2 * ks + g) * 8);
                 }
                 qr[qb][ks] = x ^ flip;
                 dr[qb][ks] = y;
@@ -241,9 +247,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             if (ok) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
+                    if (PAD && 2 * ks + g >= CG) continue;  // dO is zero there
                     if constexpr (PUR) {
-                        const f32x4 oa = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * DP + (2 * ks + g) * 8);
-                        const f32x4 ob = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * DP + (2 * ks + g) * 8 + 4);
+                        const f32x4 oa = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * D + (2 * ks + g) * 8);
+                        const f32x4 ob = *reinterpret_cast<const f32x4*>(Og32 + (size_t)qi * D + (2 * ks + g) * 8 + 4);
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
                             const float o0 = j < 2 ? oa[2 * j] : ob[2 * j - 4];
@@ -251,7 +258,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                             dl += o0 * E::lo(dr[qb][ks][j]) + o1 * E::hi(dr[qb][ks][j]);
                         }
                     } else {
-                        const u32x4 o = ldg16(Og + (size_t)qi * DP + (2 * ks + g) * 8);
+                        const u32x4 o = ldg16(Og + (size_t)qi * D + (2 * ks + g) * 8);
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             dl += E::lo(o[j]) * E::lo(dr[qb][ks][j]) + E::hi(o[j]) * E::hi(dr[qb][ks][j]);
@@ -304,7 +311,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // block's last row sees keys from R + BM - W on).
     const int te = kWin ? min(max((R + BM - W + BN - 1) / BN - tb, 0), t0) : 0;
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
     const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
@@ -324,9 +331,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (key0 + row) * RB;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ kswz(row)) << 4));
-            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
+            const int off = (key0 + row) * (2 * D);
+            const int kc = pc ^ kswz(row), vc = pc ^ (row & 7);
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), (PAD && kc >= CG) ? kBufOOB : off + (kc << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
         if constexpr (DOC)
             if (lane < 4) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 16), (key0 + wave * 16 + lane * 4) * 4);
@@ -653,7 +661,8 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
         const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
         const int q = R + row;
-        if (q < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * DP + chunk * 8));
+        if (q < T && (!PAD || chunk < CG))
+            __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dQ + (size_t)q * D + chunk * 8));
     }
 }
 
@@ -724,10 +733,11 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 // past T are left out of those sums (their zero K row still weighs
 // relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
 // workspace read, so they add nothing.
-template <class E, int DP, int MODE, bool PUR = false, bool DOC = false>
+template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && DOC) ? 2 : 3, (PUR && DOC) ? 2 : 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
+    static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
@@ -770,7 +780,10 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const int kw0 = K0 + 32 * wave;  // first key of this wave
     const int key = kw0 + c;         // this lane's key
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
@@ -794,9 +807,9 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
-            if (ok) {
-                x = ldg16(Kg + (size_t)key * DP + (2 * ks + g) * 8);
-                y = ldg16(Vg + (size_t)key * DP + (2 * ks + g) * 8);
+            if (ok && (!PAD || 2 * ks + g < CG)) {
+                x = ldg16(Kg + (size_t)key * D + (2 * ks + g) * 8);
+                y = ldg16(Vg + (size_t)key * D + (2 * ks + g) * 8);
             }
             kr[ks] = x ^ flip;
             vr[ks] = y;
@@ -818,7 +831,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const int q_hi = kWin ? (int)min((int64_t)T, (int64_t)K0 + BK - 1 + W) : T;
     const int ntiles = (K0 < T) ? (q_hi - q_lo + BQ - 1) / BQ : 0;
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
+    const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rq = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.q) + base, nrec);
     const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
@@ -841,7 +854,8 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (i0 + row) * RB + ((pc ^ swz(row)) << 4);
+            const int ch = pc ^ swz(row);
+            const int off = (PAD && ch >= CG) ? kBufOOB : (i0 + row) * (2 * D) + (ch << 4);
             dma_load16(rq, lds_addr(sb + (wave * LPW + i) * 1024), off);
             dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
         }
@@ -1159,8 +1173,8 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             const int row = 32 * wave + 8 * i + (ln >> 3);
             const u32x4 x = *reinterpret_cast<const u32x4*>(smem + (which * BK + row) * RB + ((chunk ^ (row & 7)) << 4));
             const int kk = K0 + row;
-            if (kk < T)
-                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * DP + chunk * 8));
+            if (kk < T && (!PAD || chunk < CG))
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * D + chunk * 8));
         }
 }
 

@@ -70,9 +70,6 @@ struct FwdD128Cfg {
     static constexpr int NST = 3;   // K/V ring stages
 };
 
-// Offset sent to a buffer load that must return zeros (past every range).
-constexpr int kBufOOB = 0x7ffffff0;
-
 template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {

@@ -71,6 +71,9 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t nbytes) 
     return r;
 }
 
+// Offset sent to a buffer load that must return zeros (past every range).
+constexpr int kBufOOB = 0x7ffffff0;
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(size_t)(lds_void*)(p);
 }
@@ -127,7 +130,10 @@ __host__ __device__ inline int fast_fwd_npair(int T, int BM) { return (fast_fwd_
 // pairs have their weight zeroed (a zero overlap still weighs
 // relu(-gamma tau)^4 when tau < 0).  Output rows are stored straight from the
 // accumulators.
-template <class E, int DP, int MODE, bool PUR = false, bool PRO = false>
+// PAD (purified only): a head dim D < 64 (a multiple of 8); the rows in HBM
+// are 2 D bytes, the chunks past D are loaded from outside the buffer's range
+// (zeros in LDS) and the output columns past D are not stored.
+template <class E, int DP, int MODE, bool PUR = false, bool PRO = false, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_fast_kernel(
     typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
@@ -135,6 +141,7 @@ void born_fwd16_fast_kernel(
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
     static_assert(MODE != kWindow || (!PUR && !PRO), "sliding windows: Born forward");
+    static_assert(!PAD || (PUR && MODE != kWindow), "narrow head dims: purified");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
     constexpr int KS = DP / 16;
@@ -198,7 +205,11 @@ void born_fwd16_fast_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
     const int c = lane & 31, g = lane >> 5;
 
-    const size_t base = (size_t)bh * T * DP;
+    // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
+    const int D = PAD ? p.D : DP;
+    const int RBG = 2 * D;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
@@ -212,11 +223,11 @@ void born_fwd16_fast_kernel(
     // reference's (s r)^2 does too; p = s2 * (accumulated weight).
     const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
 
-    const uint32_t nrec = (uint32_t)T * (uint32_t)RB;
-    // Bytes between consecutive Q / K rows: RB, or the raw rows' time stride
+    const uint32_t nrec = (uint32_t)T * (uint32_t)RBG;
+    // Bytes between consecutive Q / K rows: 2 D, or the raw rows' time stride
     // when the prologue is fused (the host keeps (T + 256) rows of it within
     // 32-bit offsets).
-    uint32_t qrow_b = RB;
+    uint32_t qrow_b = RBG;
     size_t qbase = base;
     if constexpr (PRO) {
         qrow_b = (uint32_t)p.q_st * 2u;
@@ -236,9 +247,10 @@ void born_fwd16_fast_kernel(
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
-            const int off = (key0 + row) * RB;
-            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ lds_swz(row)) << 4));
-            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
+            const int off = (key0 + row) * RBG;
+            const int kc = pc ^ lds_swz(row), vc = pc ^ ((row & 3) << 1);
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), (PAD && kc >= CG) ? kBufOOB : off + (kc << 4));
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
     };
     auto issue_q = [&](int mb) __attribute__((always_inline)) {
@@ -246,8 +258,9 @@ void born_fwd16_fast_kernel(
         for (int i = 0; i < LQW; ++i) {
             const int slot = (wave * LQW + i) * 64 + lane;
             const int row = slot / CPR, pc = slot % CPR;
+            const int qc = pc ^ (row & 7);
             dma_load16<true>(rq, lds_addr(q_lds + (wave * LQW + i) * 1024),
-                             (mb * BM + row) * (int)qrow_b + ((pc ^ (row & 7)) << 4));
+                             (PAD && qc >= CG) ? kBufOOB : (mb * BM + row) * (int)qrow_b + (qc << 4));
         }
     };
 
@@ -713,7 +726,8 @@ void born_fwd16_fast_kernel(
             const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
             const u32x4 x = *reinterpret_cast<const u32x4*>(q_lds + row * RB + ((chunk ^ (row & 7)) << 4));
             const int qi = mb * BM + row;
-            if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
+            if (qi < T && (!PAD || chunk < CG))
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * D + chunk * 8));
         }
     };
     // Purified: O = acc / (Z + eps) and Z + eps, fp32, straight from the
@@ -731,7 +745,9 @@ void born_fwd16_fast_kernel(
                     for (int j = 0; j < 4; ++j) {
                         const f32x16& o = oacc[db][qb];
                         const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
-                        __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                        const int col = db * 32 + 8 * j + 4 * g;
+                        if (!PAD || col < D)
+                            __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * D + col));
                     }
                 if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
             }
@@ -917,14 +933,14 @@ hipError_t launch_fwd16_fast_prologue(const FwdProArgs& a, hipStream_t st) {
 
 // Purified-Born forward through the same kernel (bf16, D == 64, dense or
 // causal, no window / documents).
-template <int MODE>
+template <int MODE, bool PAD = false>
 hipError_t launch_purified_fwd_fast(const PurArgs& a, hipStream_t st) {
     using C = FastFwdCfg<64>;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     const dim3 grid((npair < 512u || MODE == kCausal) ? nsingle : npair);
-    hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true>), grid, dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -18,6 +18,11 @@ inline bool purified_fast_ok(const PurArgs& a) {
     return a.D == 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
+// D < 64 (a multiple of 8) on the D = 64 kernels with the columns past D zero.
+inline bool purified_narrow_ok(const PurArgs& a) {
+    return a.D < 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * 64 * 2 < ((int64_t)1 << 31);
+}
+
 // D == 128, and 64 < D < 128 with the columns past D zero.
 inline bool purified_d128_ok(const PurArgs& a) {
     return a.D > 64 && a.D <= 128 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
@@ -37,6 +42,8 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
+    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a))
+        return a.is_causal ? launch_purified_fwd_fast<kCausal, true>(a, s) : launch_purified_fwd_fast<kDense, true>(a, s);
     // bf16, 64 < D <= 128, dense or causal: the D = 128 kernel's purified mode.
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
         if (a.D == 128)
@@ -59,16 +66,16 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
 // bf16, D = 64, dense or causal: the bf16-MFMA dQ kernel (which also writes
 // -delta and 1/Z) before the dK/dV kernel (which writes the dgamma / dtau
 // partials), then the fixed-order reduction.
-template <int MODE, bool DOC = false>
+template <int MODE, bool DOC = false, bool PAD = false>
 static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     const unsigned BH = (unsigned)(a.B * a.H);
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC>),
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC, PAD>),
                        dim3((unsigned)((a.T + 255) / 256) * BH), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 64);
-    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<BF16, 64, MODE, true, DOC>), dim3((unsigned)nwg), dim3(256), 0, s,
-                       a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<BF16, 64, MODE, true, DOC, PAD>), dim3((unsigned)nwg), dim3(256), 0,
+                       s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
     hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
@@ -93,6 +100,8 @@ template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
+    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a))
+        return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
         return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
     if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))

@@ -247,13 +247,14 @@ def test_purified_d128_forward(cuda_device, case):
     assert np.max(np.abs(f64(z) - f64(z_g)) / f64(z_g)) <= 1e-4
 
 
-@pytest.mark.parametrize("D", [72, 96, 120])
+@pytest.mark.parametrize("D", [8, 24, 32, 56, 72, 96, 120])
 @pytest.mark.parametrize("causal", [True, False])
-def test_purified_d128_padded_head_dims(cuda_device, D, causal):
-    """64 < D < 128 (bf16) runs the D = 128 purified kernels with the columns
-    past D zero: forward against the oracle to 1e-4, gradients, dgamma and
-    dtau against the oracle and the fp32-MFMA kernels (through a window longer
-    than T), tau < 0 with T not a multiple of 64."""
+def test_purified_padded_head_dims(cuda_device, D, causal):
+    """bf16 head dims below 64 run the D = 64 purified kernels, 64 < D < 128
+    the D = 128 ones, with the columns past D zero: forward against the
+    oracle to 1e-4, gradients, dgamma and dtau against the oracle and the
+    fp32-MFMA kernels (through a window longer than T), tau < 0 with T not a
+    multiple of 64."""
     B, H, T = 1, 2, 333
     print(f"purified padded D{D} causal={causal}", flush=True)
     q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 17, std=0.25, n=4,
