@@ -89,3 +89,12 @@ def test_noalloc_generic_kernels_and_documents(cuda_device):
 @pytest.mark.gpu
 def test_noalloc_c5_shape(cuda_device):
     _run_pair(cuda_device, 16, 16, 2048, 64, torch.bfloat16, seed=5)
+
+
+@pytest.mark.gpu
+def test_noalloc_d128_kernels(cuda_device):
+    # The D = 128 kernels: causal, with document ids, and a padded head dim.
+    _run_pair(cuda_device, 2, 4, 1100, 128, torch.bfloat16, seed=6)
+    doc = np.repeat(np.arange(11, dtype=np.int32), 100)[None].repeat(2, 0)
+    _run_pair(cuda_device, 2, 2, 1100, 128, torch.bfloat16, doc=doc, seed=7)
+    _run_pair(cuda_device, 1, 3, 700, 96, torch.float16, scale=(0.5, -1.0, 2.0), seed=8)
