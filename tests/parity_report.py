@@ -110,7 +110,7 @@ def run(name, dtype, dev):
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--out", default=os.path.join("gpurun_out", "parity_report.md"))
+    ap.add_argument("--out", default="parity_report.md")
     ap.add_argument("--configs", default=",".join(CONFIGS))
     args = ap.parse_args()
     dev = torch.device("cuda:0")
