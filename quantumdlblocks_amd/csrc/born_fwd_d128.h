@@ -520,10 +520,13 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     };
 
     if constexpr (DOC) {
-        // One block (unpaired launch).  Q rows straight into registers, the
-        // sign of the scale folded in.
+        // One block (unpaired launch).  The rows' documents first: the
+        // screening needs them; Q (straight into registers, the sign of the
+        // scale folded in) is loaded after the first chunk's first two tiles
+        // are issued, so its loads overlap theirs.
         start_item(mb_a);
-        {
+        if (qrow < T) qdoc = docb[qrow];
+        auto load_q_regs = [&]() __attribute__((always_inline)) {
             const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -531,10 +534,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 if (qrow < T) x = ldg16(Qg + (size_t)qrow * DP + (2 * ks + g) * 8);
                 qr[ks] = x ^ flip;
             }
-            if (qrow < T) qdoc = docb[qrow];
-        }
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
+            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
+        };
         // Document range of this wave's valid rows (uniform; wone: one
         // document) and of the whole block.
         const int rw = mb_a * BM + 32 * wave;
@@ -565,6 +567,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                                                t_list, t_doc, &s_rng[2 * NW]);
             if (n > 0) issue(0, 0);
             if (n > 1) issue(1, 1);
+            if (c0 == 0) load_q_regs();
             for (int u = 0; u < n; ++u) {
                 if (u + 1 < n)
                     wait_vmcnt<kDocTileLoads>();
