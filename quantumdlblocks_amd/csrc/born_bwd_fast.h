@@ -67,7 +67,8 @@ __device__ __forceinline__ void doc_rows_range(const int32_t* __restrict__ docb,
     lo = INT_MAX;
     hi = INT_MIN;
     if (vec && r1 - r0 == n) {
-#pragma unroll 2
+        // Eight 16-byte loads in flight per round trip.
+#pragma unroll 8
         for (int j = 0; j < n / 4; ++j) {
             const int4 x = *reinterpret_cast<const int4*>(docb + r0 + 4 * j);
             lo = min(lo, min(min(x.x, x.y), min(x.z, x.w)));
