@@ -72,13 +72,15 @@ CONFIGS.update({
     # C4's documents at head dim 128 (half the heads, same flops and bytes)
     "dc4": (4, 8, 8192, 128, 1.0, False, 512.0, False),
     "dc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
+    # the same with a 256-key causal window (documents and window together)
+    "dwc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
     # purified-Born attention at head dim 128 on the same work
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
     "pdc4b": (4, 8, 8192, 128, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
 })
 PURIFIED |= {"pd3", "pd5", "pdc4b"}
-WINDOW = {"w3": 256, "w5": 512}
+WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
@@ -188,19 +190,25 @@ def make_inputs(cfg, seed, device, dtype):
 
 def visible_pairs(cfg, doc, window=0):
     """Visible (b, i, j) pairs summed over the batch, per head (causal; with a
-    sliding window row i sees min(i + 1, window) keys)."""
-    B, H, T = cfg[0], cfg[1], cfg[2]
-    if window > 0:
-        w = min(window, T)
-        return B * (w * (w + 1) // 2 + (T - w) * w)
-    if doc is None:
-        return B * T * (T + 1) // 2
+    sliding window row i sees min(i + 1, window) keys of its run: the whole
+    row, or each document's contiguous run)."""
     import numpy as np
 
+    B, T = cfg[0], cfg[2]
+
+    def run_pairs(n):  # causal pairs of a run of n rows
+        n = np.asarray(n, dtype=np.int64)
+        if window <= 0:
+            return n * (n + 1) // 2
+        w = np.minimum(window, n)
+        return w * (w + 1) // 2 + (n - w) * w
+
+    if doc is None:
+        return B * int(run_pairs(T))
     total = 0
     for row in doc.cpu().numpy():
         _, counts = np.unique(row, return_counts=True)  # documents are contiguous runs
-        total += int((counts * (counts + 1) // 2).sum())
+        total += int(run_pairs(counts).sum())
     return total
 
 

@@ -1145,11 +1145,14 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
             if (MODE == kDense || MODE == kCausal) return launch_bwd16_d128<E, MODE == kCausal ? kCausal : kDense>(a, st);
         }
     }
-    // D == 128 with document ids (no window): the same kernels' document mode.
+    // D == 128 with document ids (and a causal window): the same kernels'
+    // document mode.
     if constexpr (DP == 128 && MODE == kGeneral) {
-        if (a.D == 128 && a.doc != nullptr && a.window == 0 && addr32)
+        if (a.D == 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+            if (a.window > 0) return launch_bwd16_d128<E, kWindow, false, true>(a, st);
             return a.is_causal ? launch_bwd16_d128<E, kCausal, false, true>(a, st)
                                : launch_bwd16_d128<E, kDense, false, true>(a, st);
+        }
     }
     if constexpr (DP == 96 || DP == 128) {
         if (a.D > 64 && a.D < 128 && a.doc == nullptr && addr32) {

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || MODE != kWindow, "documents: no window");
+
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -209,7 +209,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
         int key0 = (tb + u) * BN;
-        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
+        if constexpr (DOC) key0 = (tb + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne)) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -331,13 +331,14 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             // Masked past the lane's row (causal) or in another document.
             if (dmw) {
                 const int lim = kCaus ? qrow - kbase : INT_MAX;
+                const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
                     const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k > lim || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                        if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc) s[4 * i + k] = 0.f;
                 }
             }
         }
@@ -397,7 +398,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         // per-element test when it is before the wave's first row and one
         // document that all of them belong to.
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
-            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+            const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
             if (n > 0) issue(0);
             if (n > 1) issue(1);
@@ -415,10 +416,12 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 kdp = kd_lds + (soff / TB) * BN;
                 const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
                 const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
-                const int key0 = (e & ~kDocOne) * BN;
+                const int key0 = (tb + (e & ~kDocOne)) * BN;
                 const bool one = (e & kDocOne) != 0;
-                const bool vis = !(kCaus && key0 > rw + 31) && !(one && (td < wlo || td > whi));
-                dmw = (kCaus && key0 + BN - 1 > rw) || !(one && wone && td == wlo);
+                // Window: as in the forward.
+                const bool vis = !(kCaus && key0 > rw + 31) && !(kWin && key0 + BN - 1 < rw - W + 1) &&
+                                 !(one && (td < wlo || td > whi));
+                dmw = (kCaus && key0 + BN - 1 > rw) || (kWin && key0 < rw + 32 - W) || !(one && wone && td == wlo);
                 if (vis) {
                     half(kb, vb, 0, key0 + 4 * g, Docm{});
                     half(kb, vb, 1, key0 + 32 + 4 * g, Docm{});
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || MODE != kWindow, "documents: no window");
+
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -781,7 +784,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k + lim < 0 || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc) s[4 * i + k] = 0.f;
                 }
             }
         }
@@ -930,8 +933,12 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
                 const int i0 = q_lo + (e & ~kDocOne) * BQ;
                 const bool one = (e & kDocOne) != 0;
-                const bool vis = !(kCaus && i0 + BQ - 1 < kw0) && !(one && (td < klo || td > khi));
-                dmw = (kCaus && i0 < kw0 + 31) || !(one && kone && td == klo);
+                // Window: the tile is past every key's window when it starts
+                // after the last key's, and cut by one when it ends after
+                // the first key's.
+                const bool vis = !(kCaus && i0 + BQ - 1 < kw0) && !(kWin && i0 > kw0 + 31 + W - 1) &&
+                                 !(one && (td < klo || td > khi));
+                dmw = (kCaus && i0 < kw0 + 31) || (kWin && i0 + BQ - 1 >= kw0 + W) || !(one && kone && td == klo);
                 if (vis) tile(smem + soff, i0, Docm{});
             }
             __syncthreads();  // the list and the ring are reused by the next chunk

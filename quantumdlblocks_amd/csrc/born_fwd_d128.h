@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
     static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
-    static_assert(!DOC || (MODE != kWindow && !PAD), "documents: D == 128, no window");
+    static_assert(!DOC || !PAD, "documents: D == 128");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
     constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
@@ -157,7 +157,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
     auto issue = [&](int u, int st) __attribute__((always_inline)) {
         int key0 = (u < nt_a ? tb_a + u : tb_b + (u - nt_a)) * BN;
-        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
+        if constexpr (DOC) key0 = (tb_a + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne)) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -288,6 +288,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             // Masked past the row (causal) or in another document.
             if (dmw) {
                 const int lim = kCaus ? qrow - kbase : INT_MAX;
+                const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
                 const int32_t* kd = kdp + (kbase - dkey0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -295,7 +296,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                     const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k > lim || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                        if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc) s[4 * i + k] = 0.f;
                 }
             }
         }
@@ -563,7 +564,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         constexpr int kDocTileLoads = 2 * LPW + 1;  // K, V and 8 key ids per wave
         const int ncand = nt_a;
         for (int c0 = 0; c0 < ncand; c0 += CAP) {
-            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ncand - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+            const int n = screen_doc_tiles<BN>(docb, T, tb_a * BN, c0, min(CAP, ncand - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
             if (n > 0) issue(0, 0);
             if (n > 1) issue(1, 1);
@@ -582,10 +583,15 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 kdp = kd_lds + (soff / TB) * BN;
                 const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
                 const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
-                dkey0 = (e & ~kDocOne) * BN;
+                dkey0 = (tb_a + (e & ~kDocOne)) * BN;
                 const bool one = (e & kDocOne) != 0;
-                const bool vis = !(kCaus && dkey0 > rw + 31) && !(one && (td < wlo || td > whi));
-                dmw = (kCaus && dkey0 + BN - 1 > rw) || !(one && wone && td == wlo) || (PUR && dkey0 + BN > T);
+                // Window: the tile is past every row's window when it ends
+                // before the first row's, and cut by one when it starts
+                // before the last row's.
+                const bool vis = !(kCaus && dkey0 > rw + 31) && !(kWin && dkey0 + BN - 1 < rw - W + 1) &&
+                                 !(one && (td < wlo || td > whi));
+                dmw = (kCaus && dkey0 + BN - 1 > rw) || (kWin && dkey0 < rw + 32 - W) ||
+                      !(one && wone && td == wlo) || (PUR && dkey0 + BN > T);
                 if (vis) {
                     read_k(kop, kb, 0);
                     tile(kb, vb, dkey0, Docm{});
@@ -713,8 +719,8 @@ inline bool d128_fwd_paired(int B, int H, int T, bool causal) {
     return rounds * 2 * nt <= (BH * nmb + S - 1) / S * nt;
 }
 
-// Documents (no window): one block per workgroup, the longest key ranges
-// first under causality.
+// Documents (with or without a causal window): one block per workgroup, the
+// longest key ranges first under causality.
 template <class E, int MODE>
 hipError_t launch_fwd16_d128_doc(const FwdArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;

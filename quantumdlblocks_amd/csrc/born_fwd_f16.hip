@@ -18,9 +18,12 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
     // Causal sliding window (no documents): the fast kernel's window mode.
     if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32)
         return launch_fwd16_fast<F16, 64, kWindow>(a, s);
-    // D == 128 with document ids (no window): the D == 128 kernel's document mode.
-    if (a.D == 128 && a.doc != nullptr && a.window == 0 && addr32)
+    // D == 128 with document ids (and a causal window): the D == 128 kernel's
+    // document mode.
+    if (a.D == 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+        if (a.window > 0) return launch_fwd16_d128_doc<F16, kWindow>(a, s);
         return a.is_causal ? launch_fwd16_d128_doc<F16, kCausal>(a, s) : launch_fwd16_d128_doc<F16, kDense>(a, s);
+    }
     // D == 128: dense, causal or causal sliding window (no documents).
     if (a.D == 128 && a.doc == nullptr && addr32 && (a.window == 0 || a.is_causal)) {
         if (a.window > 0) return launch_fwd16_d128<F16, kWindow>(a, s);

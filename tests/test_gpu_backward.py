@@ -297,6 +297,17 @@ def test_bwd_d128_documents(cuda_device, dtype, is_causal):
     _check_bwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=8)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
+def test_bwd_d128_documents_and_window(cuda_device, dtype, window):
+    """D = 128 with document ids and a causal sliding window: the document
+    mode of the dQ and dK/dV kernels with the window's tile ranges, skips and
+    per-element tests; dscale."""
+    doc = orc.geometric_doc_ids(2, 1100, 150.0, seed=window)
+    _check_bwd(2, 2, 1100, 128, dtype, cuda_device, doc=doc, window_size=window, scale=[0.2, -0.1], std=0.7,
+               seed=window + 4, check_dscale=True)
+
+
 def test_bwd_d128_documents_many_chunks(cuda_device):
     """D = 128: more candidate tiles than one screening pass holds (256 key
     tiles in dQ, 256 query tiles in dK/dV), sorted documents with one longer

@@ -279,6 +279,17 @@ def test_fwd_d128_documents(cuda_device, dtype, is_causal):
     _check_fwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=7)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
+def test_fwd_d128_documents_and_window(cuda_device, dtype, window):
+    """D = 128 with document ids and a causal sliding window: the document
+    mode's window bounds (candidate tiles from the block's first window,
+    per-wave skips and per-element tests at the window edge)."""
+    doc = orc.geometric_doc_ids(2, 1100, 150.0, seed=window)
+    _check_fwd(2, 2, 1100, 128, dtype, cuda_device, doc=doc, window_size=window, scale=0.2, std=0.7,
+               seed=window + 2)
+
+
 def test_fwd_d128_documents_many_tiles(cuda_device):
     """D = 128, sorted documents over more candidate key tiles than one
     screening pass holds (256 tiles): every document against the oracle on
