@@ -74,13 +74,14 @@ CONFIGS.update({
     "dc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
     # the same with a 256-key causal window (documents and window together)
     "dwc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
+    "wc4b": (4, 16, 8192, 64, 1.0, False, 512.0, True),
     # purified-Born attention at head dim 128 on the same work
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
     "pdc4b": (4, 8, 8192, 128, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
 })
 PURIFIED |= {"pd3", "pd5", "pdc4b"}
-WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256}
+WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}

@@ -1120,15 +1120,21 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
             return hipGetLastError();
         }
     }
-    // Documents without a window: the same two fast kernels' document
-    // variants (tile lists screened by document range).
+    // Documents (with or without a causal window): the same two fast
+    // kernels' document variants (tile lists screened by document range).
     if constexpr (DP == 64 && MODE == kGeneral) {
-        if (a.D == 64 && a.doc != nullptr && a.window == 0 && addr32) {
-            e = a.is_causal ? launch_bwd16_dq_fast<E, 64, kCausal, true>(a, st)
-                            : launch_bwd16_dq_fast<E, 64, kDense, true>(a, st);
-            if (e != hipSuccess) return e;
-            e = a.is_causal ? launch_bwd16_dkdv_fast<E, 64, kCausal, true>(a, st)
-                            : launch_bwd16_dkdv_fast<E, 64, kDense, true>(a, st);
+        if (a.D == 64 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+            if (a.window > 0) {
+                e = launch_bwd16_dq_fast<E, 64, kWindow, true>(a, st);
+                if (e != hipSuccess) return e;
+                e = launch_bwd16_dkdv_fast<E, 64, kWindow, true>(a, st);
+            } else {
+                e = a.is_causal ? launch_bwd16_dq_fast<E, 64, kCausal, true>(a, st)
+                                : launch_bwd16_dq_fast<E, 64, kDense, true>(a, st);
+                if (e != hipSuccess) return e;
+                e = a.is_causal ? launch_bwd16_dkdv_fast<E, 64, kCausal, true>(a, st)
+                                : launch_bwd16_dkdv_fast<E, 64, kDense, true>(a, st);
+            }
             if (e != hipSuccess) return e;
             const int nwg = ((a.T + 255) / 256) * a.B * a.H;
             hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),

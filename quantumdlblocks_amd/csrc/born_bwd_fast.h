@@ -138,7 +138,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
+    static_assert(MODE != kWindow || !PUR, "sliding windows: Born gradients");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -325,7 +325,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
         int key0 = (tb + u) * BN;
-        if constexpr (DOC) key0 = (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BN;
+        if constexpr (DOC) key0 = (tb + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne)) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -450,6 +450,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 // the lane's row (causal) or in another document.
                 if (dm[qb]) {
                     const int lim = kCaus ? qrow[qb] - kbase : INT_MAX;
+                    const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
                     const int rd = r_doc[128 * qb + 64 * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -457,7 +458,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                         const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k > lim || dk[k] != rd) s[qb][4 * i + k] = 0.f;
+                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != rd) s[qb][4 * i + k] = 0.f;
                     }
                 }
             } else if (mk[qb]) {
@@ -552,7 +553,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         }
         // The kept tiles of each chunk of candidates through the same pipeline.
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
-            const int n = screen_doc_tiles<BN>(docb, T, 0, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+            const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
             if (n > 0) issue(0);
             if (n > 1) issue(1);
@@ -573,12 +574,14 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 const int ti = e & ~kDocOne;
                 const bool one = (e & kDocOne) != 0;
                 // A column block is tested per element on the causal diagonal
-                // (as in the plain loop below) and unless the tile's keys and
-                // all of its rows are one and the same document.
-                const bool mk[NQB] = {ti >= t0, ti >= t0 + 2};
+                // (as in the plain loop below; window: block 1 on every
+                // diagonal tile, both on the tiles before te) and unless the
+                // tile's keys and all of its rows are one and the same
+                // document.
+                const bool mk[NQB] = {ti >= t0 || (kWin && ti < te), ti >= t0 + 2 || (kWin && (ti < te || ti >= t0))};
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) dm[qb] = mk[qb] || !(one && qone[qb] && td == qsd[qb]);
-                tile(kb, vb, ti * BN, mk, NoSkip{});
+                tile(kb, vb, (tb + ti) * BN, mk, NoSkip{});
             }
             __syncthreads();  // the list and the ring are reused by the next chunk
         }
@@ -741,7 +744,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(MODE != kWindow || (!PUR && !DOC), "sliding windows: Born gradients, no documents");
+    static_assert(MODE != kWindow || !PUR, "sliding windows: Born gradients");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -967,7 +970,8 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k + lim < 0 || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                            s[4 * i + k] = 0.f;
                 }
             }
         } else if (mk) {
@@ -1059,13 +1063,14 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
                 const int i0 = q_lo + (e & ~kDocOne) * BQ;
                 if (kCaus && i0 + BQ - 1 < kw0) continue;  // every query before every key
+                if (kWin && i0 > kw0 + 31 + W - 1) continue;  // every query past every key's window
                 int soff = (u % NST) * SB;
                 asm volatile("" : "+s"(soff));
                 const uint8_t* sb = smem + soff;
-                const bool mk = kCaus && i0 < kw0 + 31;
-                // Tested per element on the causal diagonal and unless the
-                // tile's queries and all of the wave's keys are one and the
-                // same document.
+                const bool mk = (kCaus && i0 < kw0 + 31) || (kWin && i0 + BQ - 1 >= kw0 + W);
+                // Tested per element on the causal diagonal, at a window's
+                // end, and unless the tile's queries and all of the wave's
+                // keys are one and the same document.
                 xm = mk || !((e & kDocOne) != 0 && kone && td == ksd);
                 half(sb, 0, i0 + 4 * g, mk);
                 half(sb, 1, i0 + 32 + 4 * g, mk);

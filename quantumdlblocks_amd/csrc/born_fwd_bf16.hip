@@ -15,6 +15,9 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
     const bool addr32 = ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
     // Documents (no window): the document-aware fast kernel.
     if (a.D == 64 && a.doc != nullptr && a.window == 0 && addr32) return launch_fwd16_doc<BF16, 64>(a, s);
+    // Documents with a causal sliding window: the same kernel's window mode.
+    if (a.D == 64 && a.doc != nullptr && a.window > 0 && a.is_causal && addr32)
+        return launch_fwd16_doc<BF16, 64, true>(a, s);
     // Causal sliding window (no documents): the fast kernel's window mode.
     if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32)
         return launch_fwd16_fast<BF16, 64, kWindow>(a, s);

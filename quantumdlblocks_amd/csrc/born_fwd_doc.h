@@ -1,5 +1,5 @@
 // Flash-Born forward with document ids, head dim D == 64: the C4 path
-// (causal or not, no sliding window).
+// (causal or not; WIN: causal with a sliding window too).
 //
 // Same arithmetic, row layout and four-phase tile as born_fwd16_fast_kernel
 // (born_fwd_fast.h).  What differs is the set of key tiles a query block
@@ -39,11 +39,16 @@ namespace qdl {
 // into two bf16 terms for the P V contraction, Z summed in fp32, the output
 // in fp32.  A masked pair (or a key past T) weighs zero even where its
 // overlap is zero, so the masks zero the weights, not the overlaps.
-template <class E, int DP, bool PUR = false>
+// WIN: a causal sliding window with the documents (flash_born.py:173-174):
+// candidate tiles start at the block's first row's window, tiles that start
+// before the block's last row's window are tested per element, and the test
+// also drops keys before the row's window.
+template <class E, int DP, bool PUR = false, bool WIN = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
+    static_assert(!(PUR && WIN), "sliding windows: Born forward");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = 256;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -72,7 +77,8 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     const int T = p.T;
     const int BH = p.B * p.H;
     const int nmb = (T + BM - 1) / BM;
-    const bool causal = p.is_causal != 0;
+    const bool causal = WIN || p.is_causal != 0;
+    const int W = WIN ? p.window : 0;
     const int bid = blockIdx.x;
     const int bh = bid % BH;
     const int mb = causal ? (nmb - 1 - bid / BH) : (bid / BH);
@@ -121,8 +127,12 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     }
 
     const int kv_hi = causal ? min(T, R + BM) : T;
-    const int ncand = (kv_hi + BN - 1) / BN;
+    // Window: candidates from the tile of the block's first row's first key.
+    const int tb = WIN ? max(0, R - W + 1) / BN : 0;
+    const int ncand = (kv_hi + BN - 1) / BN - tb;
     const int t0 = causal ? R / BN : INT_MAX;  // first diagonal tile
+    // Window: tiles starting before this key are cut by some row's window.
+    const int kwin = WIN ? R + BM - W : 0;
 
     // Document-id range of candidate tile `tid` of the first screening chunk,
     // loaded here so its latency overlaps the Q loads'.  All loads of a
@@ -149,7 +159,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
         }
     };
     int tlo0 = INT_MAX, thi0 = INT_MIN;
-    if (tid < min(CAP, ncand)) tile_range(tid, tlo0, thi0);
+    if (tid < min(CAP, ncand)) tile_range(tb + tid, tlo0, thi0);
 
     // Document range of each column block's valid rows (uniform per wave):
     // qsd[qb] is the one document of all 32 rows, or INT_MIN + 1 when they
@@ -187,7 +197,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     auto screen = [&](int c0, int nc) -> int {
         if (tid < nc) {
             int lo = tlo0, hi = thi0;
-            if (c0 > 0) tile_range(c0 + tid, lo, hi);
+            if (c0 > 0) tile_range(tb + c0 + tid, lo, hi);
             t_keep[tid] = (hi >= bq_lo && lo <= bq_hi) ? 1 : 0;
             t_tdoc[tid] = (lo == hi) ? lo : INT_MIN;
         }
@@ -217,7 +227,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     // wave's 16 key document ids (lanes 0-3, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
-        const int key0 = __builtin_amdgcn_readfirstlane(t_list[u]) * BN;
+        const int key0 = (tb + __builtin_amdgcn_readfirstlane(t_list[u])) * BN;
         uint8_t* kb = k_lds + st * TB;
         uint8_t* vb = v_lds + st * TB;
 #pragma unroll
@@ -284,11 +294,14 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     auto apply_mask = [&](f32x16& s, int qb, int key0h, const int32_t* kd, bool single, bool vis)
         __attribute__((always_inline)) {
         int lim = causal ? qrow[qb] - (key0h + 4 * g) : INT_MAX;
+        const int wlo = WIN ? lim - W + 1 : 0;  // window: first visible key
         if (single) {
             if (!vis) lim = -1;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + (r & 3) > lim) s[r] = 0.f;
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off > lim || (WIN && off < wlo)) s[r] = 0.f;
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -296,7 +309,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
                 const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    if (8 * i + k > lim || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
+                    if (8 * i + k > lim || (WIN && 8 * i + k < wlo) || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
             }
         }
     };
@@ -496,7 +509,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             const uint8_t* kb = k_lds + soff;
             const uint8_t* vb = v_lds + soff;
             const int32_t* kd = kd_lds + (soff / TB) * BN;
-            const int ti = __builtin_amdgcn_readfirstlane(t_list[u]);
+            const int ti = tb + __builtin_amdgcn_readfirstlane(t_list[u]);
             const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
             read_k(kop, kb, 0);
             // A column block needs the element test on the causal diagonal
@@ -510,8 +523,10 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             // Purified: a tile holding keys past T is tested per element (the
             // zero rows of those keys still weigh relu(-gamma tau)).
             const bool tail = PUR && (ti + 1) * BN > T;
-            const bool m0 = rel >= 0 || mixed || tail;
-            const bool m1 = rel >= 2 || mixed || tail;
+            // Window: both blocks tested where a row's window starts.
+            const bool cut = WIN && ti * BN < kwin;
+            const bool m0 = rel >= 0 || mixed || tail || cut;
+            const bool m1 = rel >= 2 || mixed || tail || cut;
             tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td, !mixed);
         }
         __syncthreads();  // the list and the ring are reused by the next chunk
@@ -582,10 +597,10 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     }
 }
 
-template <class E, int DP>
+template <class E, int DP, bool WIN = false>
 hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP, false, WIN>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

