@@ -79,9 +79,13 @@ CONFIGS.update({
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
     "pdc4b": (4, 8, 8192, 128, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
+    # purified with the wavelet models' 384-key causal window, C5 work, and
+    # with C4's documents too
+    "pw5": (16, 16, 2048, 64, 0.125, False, None, True),
+    "pwc4b": (4, 16, 8192, 64, 0.125, False, 512.0, True),
 })
-PURIFIED |= {"pd3", "pd5", "pdc4b"}
-WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256}
+PURIFIED |= {"pd3", "pd5", "pdc4b", "pw5", "pwc4b"}
+WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
@@ -229,7 +233,8 @@ def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None, window=0):
 
     def eager(q, k, v, sc):
         if purified:
-            return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS, doc_ids=doc_row)
+            return purified_eager_fp32_torch(q, k, v, sc, PUR_TAU, PUR_EPS_BASE, True, PUR_EPS, window_size=window,
+                                             doc_ids=doc_row)
         return eager_fp32_torch(q, k, v, sc, window_size=window, doc_ids=doc_row)
 
     cores = len(os.sched_getaffinity(0))
@@ -267,13 +272,7 @@ def cpu_baseline(cfg, budget_s, seed, purified=False, doc=None, window=0):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    if window > 0:
-        pairs = visible_pairs((1, 1, T), None, window)
-    elif doc_row is None:
-        pairs = T * (T + 1) // 2
-    else:
-        _, counts = np.unique(doc_row.numpy()[0], return_counts=True)  # documents are contiguous runs
-        pairs = int((counts * (counts + 1) // 2).sum())
+    pairs = visible_pairs((1, 1, T), doc_row, window)
     flops = 4.0 * D * pairs * n * (3.5 if backward else 1.0)
     cpu_model = "unknown"
     try:
@@ -383,14 +382,14 @@ def main():
         q, k, v, _, out, z, _ = s
         rc = lib.qdl_flash_purified_born_fwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                              out.data_ptr(), z.data_ptr(), scale.data_ptr(), 1, tau.data_ptr(), 1,
-                                             PUR_EPS_BASE, doc_ptr, 1, 0, PUR_EPS, stream)
+                                             PUR_EPS_BASE, doc_ptr, 1, window, PUR_EPS, stream)
         _native.check(rc, "qdl_flash_purified_born_fwd")
 
     def pur_bwd(s):
         q, k, v, do, out, z, (dq, dk, dv) = s
         rc = lib.qdl_flash_purified_born_bwd(code, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                              out.data_ptr(), do.data_ptr(), z.data_ptr(), scale.data_ptr(), 1,
-                                             tau.data_ptr(), 1, PUR_EPS_BASE, doc_ptr, 1, 0, dq.data_ptr(),
+                                             tau.data_ptr(), 1, PUR_EPS_BASE, doc_ptr, 1, window, dq.data_ptr(),
                                              dk.data_ptr(), dv.data_ptr(), dscale.data_ptr(), dtau.data_ptr(),
                                              ws.data_ptr(), ws.numel(), stream)
         _native.check(rc, "qdl_flash_purified_born_bwd")

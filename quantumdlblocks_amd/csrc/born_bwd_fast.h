@@ -135,10 +135,9 @@ template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PA
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
-    static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
+    static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(MODE != kWindow || !PUR, "sliding windows: Born gradients");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -433,9 +432,11 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                         // A masked pair weighs zero even where its overlap is
                         // zero (u = relu(-gamma tau) > 0 for tau < 0).
                         if constexpr (DOC) {
-                            if (dm[qb] && ((kCaus && off > lim) || kdp[nb * 32 + 4 * g + off] != rd)) dr_ = 0.f;
+                            if (dm[qb] && ((kCaus && off > lim) || (kWin && off < lim - W + 1) ||
+                                           kdp[nb * 32 + 4 * g + off] != rd))
+                                dr_ = 0.f;
                         } else {
-                            if (mk[qb] && off > lim) dr_ = 0.f;
+                            if (mk[qb] && (off > lim || (kWin && off < lim - W + 1))) dr_ = 0.f;
                         }
                         w[e] = dr_;
                     }
@@ -738,13 +739,13 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 // relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
 // workspace read, so they add nothing.
 template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && DOC) ? 2 : 3, (PUR && DOC) ? 2 : 3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && (DOC || MODE == kWindow)) ? 2 : 3,
+                                                                     (PUR && (DOC || MODE == kWindow)) ? 2 : 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
-    static_assert(!PAD || (PUR && !DOC && MODE != kWindow), "narrow head dims: purified");
+    static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(MODE != kWindow || !PUR, "sliding windows: Born gradients");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -941,9 +942,11 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const int off = 8 * (r >> 2) + (r & 3);
                         if constexpr (DOC) {
                             const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
-                            if (xm && ((kCaus && off + lim < 0) || qd[nb * 32 + 4 * g + off] != kdoc)) u = bb = 0.f;
+                            if (xm && ((kCaus && off + lim < 0) || (kWin && off + lim >= W) ||
+                                       qd[nb * 32 + 4 * g + off] != kdoc))
+                                u = bb = 0.f;
                         } else {
-                            if (mk && off + lim < 0) u = bb = 0.f;
+                            if (mk && (off + lim < 0 || (kWin && off + lim >= W))) u = bb = 0.f;
                         }
                         const float u2_ = u * u;
                         const float dpz = dp[r] * z4[k + e];

@@ -48,7 +48,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
-    static_assert(!(PUR && WIN), "sliding windows: Born forward");
     constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = 256;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -371,6 +370,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             int lim = (causal ? qrow[qb] : T - 1) - (key0h + 4 * g);
+            const int wlo = WIN ? lim - W + 1 : 0;  // window: first visible key
             if (single && !vv[qb]) lim = -1;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -387,7 +387,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
                     float pw = fmaf(u2, u2, bq * bq);
                     bool masked = false;
                     if (mm[qb]) {
-                        masked = off > lim;
+                        masked = off > lim || (WIN && off < wlo);
                         if (!single) masked = masked || kd[4 * g + off] != qdoc[qb];
                     } else if (ll[qb]) {
                         masked = !vv[qb];
@@ -604,10 +604,12 @@ hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Purified-Born forward with document ids (bf16, D = 64, no window).
-inline hipError_t launch_purified_fwd_doc(const PurArgs& a, hipStream_t st) {
+// Purified-Born forward with document ids (bf16, D = 64; WIN: with a causal
+// sliding window).
+template <bool WIN = false>
+hipError_t launch_purified_fwd_doc(const PurArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true, WIN>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

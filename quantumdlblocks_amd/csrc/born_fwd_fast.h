@@ -140,8 +140,8 @@ void born_fwd16_fast_kernel(
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
-    static_assert(MODE != kWindow || (!PUR && !PRO), "sliding windows: Born forward");
-    static_assert(!PAD || (PUR && MODE != kWindow), "narrow head dims: purified");
+    static_assert(MODE != kWindow || !PRO, "sliding windows: no fused prologue");
+    static_assert(!PAD || PUR, "narrow head dims: purified");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
     constexpr int KS = DP / 16;
@@ -316,6 +316,7 @@ void born_fwd16_fast_kernel(
             for (int qb = 0; qb < NQB; ++qb) {
                 if (M[qb] == kSkip) continue;
                 const int lim = mlim[qb] - kbase;
+                const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float w[2];
@@ -329,7 +330,8 @@ void born_fwd16_fast_kernel(
                         float pw = fmaf(u2, u2, bq * bq);
                         if (M[qb] == kMasked) {
                             const int r = 2 * j + e;
-                            if (8 * (r >> 2) + (r & 3) > lim) pw = 0.f;
+                            const int off = 8 * (r >> 2) + (r & 3);
+                            if (off > lim || (kWin && off < wlo)) pw = 0.f;
                         }
                         w[e] = pw;
                     }
@@ -931,15 +933,15 @@ hipError_t launch_fwd16_fast_prologue(const FwdProArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Purified-Born forward through the same kernel (bf16, D == 64, dense or
-// causal, no window / documents).
+// Purified-Born forward through the same kernel (bf16, D == 64, dense,
+// causal or causal sliding window; no documents).
 template <int MODE, bool PAD = false>
 hipError_t launch_purified_fwd_fast(const PurArgs& a, hipStream_t st) {
     using C = FastFwdCfg<64>;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid((npair < 512u || MODE == kCausal) ? nsingle : npair);
+    const dim3 grid((npair < 512u || MODE != kDense) ? nsingle : npair);
     hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }

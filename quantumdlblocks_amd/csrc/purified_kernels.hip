@@ -14,13 +14,17 @@ inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <
 // The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
 // offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
 // kernels, as the Born dispatch does.
+// D = 64 (and below) also takes a causal sliding window (the wavelet models'
+// purified layers run causal with a window and document ids).
+inline bool purified_window_ok(const PurArgs& a) { return a.window == 0 || a.is_causal; }
+
 inline bool purified_fast_ok(const PurArgs& a) {
-    return a.D == 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D == 64 && purified_window_ok(a) && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 // D < 64 (a multiple of 8) on the D = 64 kernels with the columns past D zero.
 inline bool purified_narrow_ok(const PurArgs& a) {
-    return a.D < 64 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * 64 * 2 < ((int64_t)1 << 31);
+    return a.D < 64 && purified_window_ok(a) && a.doc == nullptr && ((int64_t)a.T + 256) * 64 * 2 < ((int64_t)1 << 31);
 }
 
 // D == 128, and 64 < D < 128 with the columns past D zero.
@@ -34,16 +38,21 @@ inline bool purified_d128_doc_ok(const PurArgs& a) {
 }
 
 inline bool purified_doc_fast_ok(const PurArgs& a) {
-    return a.D == 64 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D == 64 && purified_window_ok(a) && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 template <class IN>
 static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
-    // bf16, D = 64, dense or causal: the bf16-MFMA kernel with split weights.
-    if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
+    // bf16, D = 64 (and below, zero columns), dense, causal or causal
+    // window: the bf16-MFMA kernel with split weights.
+    if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
+        if (a.window > 0) return launch_purified_fwd_fast<kWindow>(a, s);
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
-    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a))
+    }
+    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
+        if (a.window > 0) return launch_purified_fwd_fast<kWindow, true>(a, s);
         return a.is_causal ? launch_purified_fwd_fast<kCausal, true>(a, s) : launch_purified_fwd_fast<kDense, true>(a, s);
+    }
     // bf16, 64 < D <= 128, dense or causal: the D = 128 kernel's purified mode.
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
         if (a.D == 128)
@@ -53,9 +62,10 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 128, document ids without a window: its document mode.
     if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
         return a.is_causal ? launch_purified_fwd_d128_doc<kCausal>(a, s) : launch_purified_fwd_d128_doc<kDense>(a, s);
-    // bf16, D = 64, document ids without a window: the document kernel's
-    // purified mode.
-    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) return launch_purified_fwd_doc(a, s);
+    // bf16, D = 64, document ids (with or without a causal window): the
+    // document kernel's purified mode.
+    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))
+        return a.window > 0 ? launch_purified_fwd_doc<true>(a, s) : launch_purified_fwd_doc(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);
@@ -98,18 +108,24 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
 
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
-    if (std::is_same<IN, BF16>::value && purified_fast_ok(a))
+    if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
+        if (a.window > 0) return purified_bwd_fast<kWindow>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
-    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a))
+    }
+    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
+        if (a.window > 0) return purified_bwd_fast<kWindow, false, true>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
+    }
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
         return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
     if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
         return a.is_causal ? purified_bwd_d128<kCausal, true>(a, s) : purified_bwd_d128<kDense, true>(a, s);
-    // bf16, D = 64, document ids without a window: the same kernels' document
-    // variants.
-    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))
+    // bf16, D = 64, document ids (with or without a causal window): the same
+    // kernels' document variants.
+    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) {
+        if (a.window > 0) return purified_bwd_fast<kWindow, true>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal, true>(a, s) : purified_bwd_fast<kDense, true>(a, s);
+    }
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);
         case 64: return launch_purified_bwd<IN, 64>(a, s);
