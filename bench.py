@@ -79,13 +79,14 @@ CONFIGS.update({
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
     "pd5": (16, 8, 2048, 128, 0.125, False, None, True),
     "pdc4b": (4, 8, 8192, 128, 0.125, False, 512.0, True),  # C4 documents, fwd + bwd
-    # purified with the wavelet models' 384-key causal window, C5 work, and
-    # with C4's documents too
+    # purified with the wavelet models' 384-key causal window, C5 work, with
+    # C4's documents too, and at head dim 128
     "pw5": (16, 16, 2048, 64, 0.125, False, None, True),
     "pwc4b": (4, 16, 8192, 64, 0.125, False, 512.0, True),
+    "pdw5": (16, 8, 2048, 128, 0.125, False, None, True),
 })
-PURIFIED |= {"pd3", "pd5", "pdc4b", "pw5", "pwc4b"}
-WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384}
+PURIFIED |= {"pd3", "pd5", "pdc4b", "pw5", "pwc4b", "pdw5"}
+WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384, "pdw5": 384}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}

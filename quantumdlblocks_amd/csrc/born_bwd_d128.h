@@ -51,7 +51,7 @@ template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = fals
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
 
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
@@ -280,8 +280,9 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             // relu(-gamma tau) > 0 for tau < 0).  Keys past T need no mask
             // here: their K rows (zero) multiply U.
             const int lim = qrow - kbase;
+            const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
             // Documents: bit r set for a register masked by the diagonal
-            // (causal) or another document.
+            // (causal), the window or another document.
             uint32_t dmask = 0;
             if constexpr (decltype(m)::value == kDocm) {
                 if (dmw) {
@@ -292,7 +293,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                         const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k > dlim || dk[k] != qdoc) dmask |= 1u << (4 * i + k);
+                            if (8 * i + k > dlim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc)
+                                dmask |= 1u << (4 * i + k);
                     }
                 }
             }
@@ -307,8 +309,10 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     const float bb = __int_as_float(max(__float_as_int(x), 0));
                     const float f = fmaf(p4g, uu * uu * uu, p2e * bb);
                     float d = f * fmaf(t[r], zinv, nd);
-                    if constexpr (decltype(m)::value == kMasked)
-                        if (8 * (r >> 2) + (r & 3) > lim) d = 0.f;
+                    if constexpr (decltype(m)::value == kMasked) {
+                        const int off = 8 * (r >> 2) + (r & 3);
+                        if (off > lim || (kWin && off < wlo)) d = 0.f;
+                    }
                     if constexpr (decltype(m)::value == kDocm)
                         if ((dmask >> r) & 1u) d = 0.f;
                     w[e] = d;
@@ -500,7 +504,7 @@ template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = fals
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
 
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
@@ -739,7 +743,8 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k + dlim < 0 || dq[k] != kdoc) dmask |= 1u << (4 * i + k);
+                            if (8 * i + k + dlim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                                dmask |= 1u << (4 * i + k);
                     }
                 }
             }
@@ -755,8 +760,10 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const float x = s[r];
                         float u = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
                         float bb = __int_as_float(max(__float_as_int(x), 0));
-                        if constexpr (decltype(m)::value == kMasked)
-                            if (8 * (r >> 2) + (r & 3) + lim < 0) u = bb = 0.f;
+                        if constexpr (decltype(m)::value == kMasked) {
+                            const int off = 8 * (r >> 2) + (r & 3);
+                            if (off + lim < 0 || (kWin && off + lim >= W)) u = bb = 0.f;
+                        }
                         if constexpr (decltype(m)::value == kDocm)
                             if ((dmask >> r) & 1u) u = bb = 0.f;
                         const float u2_ = u * u;

@@ -74,7 +74,7 @@ template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = fals
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    static_assert(!PUR || (std::is_same<E, BF16>::value && MODE != kWindow), "purified: bf16, no window");
+    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
     static_assert(!DOC || !PAD, "documents: D == 128");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
@@ -232,9 +232,11 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     auto elementwise = [&](f32x16& s, uint32_t (&pk)[8], uint32_t (&pl)[PW], auto m, int kbase)
         __attribute__((always_inline)) {
         if constexpr (PUR) {
-            // Weights zeroed past the row (causal) or past T (dense), and
-            // (documents) in another document: bit r of dmask for register r.
+            // Weights zeroed past the row (causal) or past T (dense), before
+            // the row's window, and (documents) in another document: bit r of
+            // dmask for register r.
             const int lim = (kCaus ? qrow : T - 1) - kbase;
+            const int wlo = kWin ? lim - W + 1 : 0;
             uint32_t dmask = 0;
             if constexpr (decltype(m)::value == kDocm) {
                 if (dmw) {
@@ -245,7 +247,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                         const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k > lim || dk[k] != qdoc) dmask |= 1u << (4 * i + k);
+                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc)
+                                dmask |= 1u << (4 * i + k);
                     }
                 }
             }
@@ -261,8 +264,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                     const float u2 = u * u;
                     float pw = fmaf(u2, u2, bq * bq);
                     if constexpr (decltype(m)::value == kMasked) {
-                        const int r = 2 * j + e;
-                        if (8 * (r >> 2) + (r & 3) > lim) pw = 0.f;
+                        const int r = 2 * j + e, off = 8 * (r >> 2) + (r & 3);
+                        if (off > lim || (kWin && off < wlo)) pw = 0.f;
                     }
                     if constexpr (decltype(m)::value == kDocm)
                         if ((dmask >> (2 * j + e)) & 1u) pw = 0.f;
@@ -742,7 +745,8 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Purified-Born forward with document ids (bf16, D == 128, no window).
+// Purified-Born forward with document ids (bf16, D == 128; with or without a
+// causal window).
 template <int MODE>
 hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
@@ -751,15 +755,16 @@ hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Purified-Born forward through the same kernel (bf16, D == 128, dense or
-// causal, no window / documents); same grid as the Born launch.
+// Purified-Born forward through the same kernel (bf16, 64 < D <= 128, dense,
+// causal or causal window, no documents); same grid as the Born launch.
 template <int MODE, bool PAD = false>
 hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const dim3 grid(d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal) ? npair : nsingle);
+    const bool pair = MODE != kWindow && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
+    const dim3 grid(pair ? npair : nsingle);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }

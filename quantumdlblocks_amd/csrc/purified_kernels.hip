@@ -29,12 +29,13 @@ inline bool purified_narrow_ok(const PurArgs& a) {
 
 // D == 128, and 64 < D < 128 with the columns past D zero.
 inline bool purified_d128_ok(const PurArgs& a) {
-    return a.D > 64 && a.D <= 128 && a.window == 0 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D > 64 && a.D <= 128 && purified_window_ok(a) && a.doc == nullptr &&
+           ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
-// D == 128 with document ids (no window): the D = 128 kernels' document mode.
+// D == 128 with document ids: the D = 128 kernels' document mode.
 inline bool purified_d128_doc_ok(const PurArgs& a) {
-    return a.D == 128 && a.window == 0 && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D == 128 && purified_window_ok(a) && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 inline bool purified_doc_fast_ok(const PurArgs& a) {
@@ -53,15 +54,22 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
         if (a.window > 0) return launch_purified_fwd_fast<kWindow, true>(a, s);
         return a.is_causal ? launch_purified_fwd_fast<kCausal, true>(a, s) : launch_purified_fwd_fast<kDense, true>(a, s);
     }
-    // bf16, 64 < D <= 128, dense or causal: the D = 128 kernel's purified mode.
+    // bf16, 64 < D <= 128, dense, causal or causal window: the D = 128
+    // kernel's purified mode.
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
-        if (a.D == 128)
+        if (a.D == 128) {
+            if (a.window > 0) return launch_purified_fwd_d128<kWindow>(a, s);
             return a.is_causal ? launch_purified_fwd_d128<kCausal>(a, s) : launch_purified_fwd_d128<kDense>(a, s);
+        }
+        if (a.window > 0) return launch_purified_fwd_d128<kWindow, true>(a, s);
         return a.is_causal ? launch_purified_fwd_d128<kCausal, true>(a, s) : launch_purified_fwd_d128<kDense, true>(a, s);
     }
-    // bf16, D = 128, document ids without a window: its document mode.
-    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
+    // bf16, D = 128, document ids (with or without a causal window): its
+    // document mode.
+    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a)) {
+        if (a.window > 0) return launch_purified_fwd_d128_doc<kWindow>(a, s);
         return a.is_causal ? launch_purified_fwd_d128_doc<kCausal>(a, s) : launch_purified_fwd_d128_doc<kDense>(a, s);
+    }
     // bf16, D = 64, document ids (with or without a causal window): the
     // document kernel's purified mode.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))
@@ -92,8 +100,8 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// bf16, 64 < D <= 128, dense or causal: the D = 128 dQ and dK/dV kernels' purified
-// mode, then the same reduction.
+// bf16, 64 < D <= 128, dense, causal or causal window: the D = 128 dQ and
+// dK/dV kernels' purified mode, then the same reduction.
 template <int MODE, bool DOC = false>
 static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
     hipError_t e = DOC           ? launch_purified_bwd_d128<MODE, false, DOC>(a, s)
@@ -116,10 +124,14 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         if (a.window > 0) return purified_bwd_fast<kWindow, false, true>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
     }
-    if (std::is_same<IN, BF16>::value && purified_d128_ok(a))
+    if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
+        if (a.window > 0) return purified_bwd_d128<kWindow>(a, s);
         return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
-    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a))
+    }
+    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a)) {
+        if (a.window > 0) return purified_bwd_d128<kWindow, true>(a, s);
         return a.is_causal ? purified_bwd_d128<kCausal, true>(a, s) : purified_bwd_d128<kDense, true>(a, s);
+    }
     // bf16, D = 64, document ids (with or without a causal window): the same
     // kernels' document variants.
     if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) {

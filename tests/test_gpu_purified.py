@@ -330,17 +330,18 @@ def test_purified_d128_documents(cuda_device, causal):
         assert ok.all(), (name, got, gen)
 
 
-@pytest.mark.parametrize("D", [64, 32])
+@pytest.mark.parametrize("D", [64, 32, 128, 96])
 @pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
 @pytest.mark.parametrize("docs", [False, True])
 def test_purified_window_fast(cuda_device, D, window, docs):
     """bf16 purified attention with a causal sliding window (the wavelet
-    models' purified layers pass one, with document ids): the D = 64 kernels'
-    window mode (D = 32 with zero columns), and the document kernels' window
-    mode; tau < 0, per-head gamma and tau.  Forward (fp32 output) against the
-    oracle to 1e-4; gradients, dgamma and dtau to the bf16 bars."""
-    if docs and D != 64:
-        pytest.skip("documents: D = 64")
+    models' purified layers pass one, with document ids): the D = 64 and
+    D = 128 kernels' window mode (D = 32 and 96 with zero columns), and their
+    document modes with a window; tau < 0, per-head gamma and tau.  Forward
+    (fp32 output) against the oracle to 1e-4; gradients, dgamma and dtau to
+    the bf16 bars."""
+    if docs and D not in (64, 128):
+        pytest.skip("documents: D = 64 and 128")
     B, H, T = 2, 2, 700
     print(f"purified window D{D} W{window} docs={docs}", flush=True)
     doc = orc.geometric_doc_ids(B, T, 120.0, seed=window) if docs else None
