@@ -74,6 +74,8 @@ CONFIGS.update({
     "dc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
     # the same with a 256-key causal window (documents and window together)
     "dwc4b": (4, 8, 8192, 128, 1.0, False, 512.0, True),
+    # w5's 512-key window at head dim 128 (C5 work)
+    "dw5": (16, 8, 2048, 128, 1.0, False, None, True),
     "wc4b": (4, 16, 8192, 64, 1.0, False, 512.0, True),
     # purified-Born attention at head dim 128 on the same work
     "pd3": (16, 8, 1024, 128, 0.125, False, None, False),
@@ -86,7 +88,7 @@ CONFIGS.update({
     "pdw5": (16, 8, 2048, 128, 0.125, False, None, True),
 })
 PURIFIED |= {"pd3", "pd5", "pdc4b", "pw5", "pwc4b", "pdw5"}
-WINDOW = {"w3": 256, "w5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384, "pdw5": 384}
+WINDOW = {"w3": 256, "w5": 512, "dw5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384, "pdw5": 384}
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}

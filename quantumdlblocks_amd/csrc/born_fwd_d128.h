@@ -756,14 +756,20 @@ hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
 }
 
 // Purified-Born forward through the same kernel (bf16, 64 < D <= 128, dense,
-// causal or causal window, no documents); same grid as the Born launch.
+// causal or causal window, no documents); the Born launch's grid, except that
+// window blocks (about equal work each) are paired too when two rounds of
+// pairs take no longer than the rounds of single blocks: the second block's
+// loads then overlap the first block's fp32 output stores (B16 H8 T2048,
+// window 384: step 632 -> 620 us; the Born window forward gains nothing).
 template <int MODE, bool PAD = false>
 hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const bool pair = MODE != kWindow && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
+    constexpr unsigned kCUs = 256;
+    const bool pair = MODE == kWindow ? 2 * ((npair + kCUs - 1) / kCUs) <= (nsingle + kCUs - 1) / kCUs
+                                      : d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
     const dim3 grid(pair ? npair : nsingle);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();

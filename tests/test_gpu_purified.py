@@ -370,6 +370,21 @@ def test_purified_window_fast(cuda_device, D, window, docs):
         assert ok.all(), (name, got, want, m)
 
 
+def test_purified_d128_window_paired_launch(cuda_device):
+    """Head dim 128 with a causal window on a grid of 256 block pairs
+    (B4 H16 T2048, window 384: the launch pairs blocks nmb-1-mb and mb);
+    sampled heads against the oracle, fp32 output to 1e-4."""
+    B, H, T, D, W = 4, 16, 2048, 128, 384
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=11, std=0.125, n=3,
+                                                          dtype=torch.bfloat16))
+    out, z = _pur_fwd_abi(q, k, v, 8.0, 0.0625, 0.05, True, 1e-8, window=W)
+    for b, h in ((0, 0), (1, 7), (3, 15), (2, 10)):
+        O_ref, Z_ref = orc.purified_forward(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, h:h + 1]),
+                                            f64(v[b:b + 1, h:h + 1]), 8.0, 0.0625, 0.05, True, 1e-8, W)
+        assert rel_err(f64(out[b:b + 1, h:h + 1]), O_ref) <= 1e-4, (b, h)
+        assert np.max(np.abs(f64(z[b:b + 1, h:h + 1]) - Z_ref) / Z_ref) <= 1e-4, (b, h)
+
+
 def test_purified_fast_forward_paired_launch(cuda_device):
     """The C3 shape (B16 H16 T1024): workgroups take two query blocks each;
     checked on sampled heads against the oracle."""
