@@ -548,7 +548,8 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
                     for (int j = 0; j < 4; ++j) {
                         const f32x16& o = oacc[db][qb];
                         const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
-                        __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g));
+                        // plain store: L2 merges each row's 32-byte pieces into whole lines
+                        *reinterpret_cast<f32x4*>(O32 + (size_t)qi * DP + db * 32 + 8 * j + 4 * g) = w;
                     }
                 if (g == 0) __builtin_nontemporal_store(zd, Zp + qi);
             }
