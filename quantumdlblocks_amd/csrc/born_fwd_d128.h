@@ -524,6 +524,15 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         if (u == uq && early_q) issue_q(mb_b);
         if (u + 2 < ntot) issue(u + 2, (u + 2) % NST);
         if (!PUR && nitems == 2 && u == nt_a + 1) flush(mb_a);
+        // The waits above cover the second item's Q block from step uq + 2
+        // on.  A first item of one or two tiles (a short last block under a
+        // window: uq = 1 and the second item starts at step 1 or 2) starts
+        // the second item before that, so its Q block is drained here, and
+        // the barrier makes every wave's share visible before any reads it.
+        if (early_q && u == nt_a && nt_a < uq + 2) {
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
     };
 
     if constexpr (DOC) {

@@ -339,9 +339,9 @@ def test_purified_window_fast(cuda_device, D, window, docs):
     D = 128 kernels' window mode (D = 32 and 96 with zero columns), and their
     document modes with a window; tau < 0, per-head gamma and tau.  Forward
     (fp32 output) against the oracle to 1e-4; gradients, dgamma and dtau to
-    the bf16 bars."""
-    if docs and D not in (64, 128):
-        pytest.skip("documents: D = 64 and 128")
+    the bf16 bars.  With documents at D = 32 and 96 the calls take the
+    fp32-MFMA purified kernels (the document modes of the bf16-MFMA kernels
+    are built for D = 64 and 128), held to the same bars."""
     B, H, T = 2, 2, 700
     print(f"purified window D{D} W{window} docs={docs}", flush=True)
     doc = orc.geometric_doc_ids(B, T, 120.0, seed=window) if docs else None
@@ -382,6 +382,26 @@ def test_purified_d128_window_paired_launch(cuda_device):
         O_ref, Z_ref = orc.purified_forward(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, h:h + 1]),
                                             f64(v[b:b + 1, h:h + 1]), 8.0, 0.0625, 0.05, True, 1e-8, W)
         assert rel_err(f64(out[b:b + 1, h:h + 1]), O_ref) <= 1e-4, (b, h)
+        assert np.max(np.abs(f64(z[b:b + 1, h:h + 1]) - Z_ref) / Z_ref) <= 1e-4, (b, h)
+
+
+@pytest.mark.parametrize("T,W", [(1800, 50), (1850, 1)])
+def test_purified_d128_window_paired_short_first_block(cuda_device, T, W):
+    """Paired window launch whose first item (the last query block) has two
+    key tiles (T 1800, W 50) or one (T 1850, W 1): the second item (block 0)
+    starts before the usual waits cover its Q block, which the kernel drains
+    first.  Every head's block 0 comes from such a pair, so whole heads are
+    held to the oracle (fp32 output to 1e-4, Z to 1e-4 per row)."""
+    B, H, D = 4, 16, 128
+    print(f"purified d128 window paired T{T} W{W}", flush=True)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=T + W, std=0.125, n=3,
+                                                          dtype=torch.bfloat16))
+    out, z = _pur_fwd_abi(q, k, v, 8.0, 0.0625, 0.05, True, 1e-8, window=W)
+    for b, h in ((0, 0), (1, 9), (3, 15)):
+        O_ref, Z_ref = orc.purified_forward(f64(q[b:b + 1, h:h + 1]), f64(k[b:b + 1, h:h + 1]),
+                                            f64(v[b:b + 1, h:h + 1]), 8.0, 0.0625, 0.05, True, 1e-8, W)
+        assert rel_err(f64(out[b:b + 1, h:h + 1]), O_ref) <= 1e-4, (b, h)
+        assert rel_err(f64(out[b:b + 1, h:h + 1, :256]), O_ref[:, :, :256]) <= 1e-4, (b, h, "block 0")
         assert np.max(np.abs(f64(z[b:b + 1, h:h + 1]) - Z_ref) / Z_ref) <= 1e-4, (b, h)
 
 
