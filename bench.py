@@ -12,7 +12,10 @@ TFLOP/s (4*D*visible_pairs*B*H per forward) and its fraction of the MI355X
 dense bf16 MFMA peak, plus ``roofline`` (the kernel's HIP-event-timed
 average launch against the HBM roof) and ``cpu_baseline`` (the reference's
 eager CPU path, restated in oracle/born_oracle.py, timed on a bounded sample
-on this host).
+on this host).  The default run then times the north star's other configs
+the same way (C2, C4 with its documents, the C5 forward alone and the C5
+forward + backward), each with its own roofline, measured traffic and CPU
+baseline, under ``detail.north_star_configs`` (``--no-extra`` skips them).
 
     python bench.py [--steps K] [--warmup W] [--config c3|c2|c4|c4b|c5fwd|c5|p3|p5|p4b|qk3|qk5]
 
@@ -109,6 +112,9 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="c3 only: skip the other north-star configs (C2, C4, C5 forward, C5 forward + backward) "
+                         "that the default run also times under detail.north_star_configs")
     ap.add_argument("--profile", action="store_true",
                     help="run for rocprofv3: 500 warm-up steps, then 20 rotated and 20 hot steps (no CPU leg)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -343,6 +349,34 @@ def main():
         fused_main(args)
         return
 
+    steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
+    line = attention_leg(args.config, args, steps, warmup, args.cpu_seconds)
+    if args.config == "c3" and not (args.no_extra or args.profile):
+        # The north star's other numbers in the same run, after the headline:
+        # C2, C4 (documents, visible-pair flops), C5 forward alone and C5
+        # forward + backward, each with its roofline, measured traffic and a
+        # bounded CPU baseline of its own.
+        extra = {}
+        for name in NORTH_STAR_EXTRA:
+            leg = attention_leg(name, args, steps, warmup, args.cpu_seconds / 4.0)
+            extra[name] = {k: leg[k] for k in ("metric", "value", "unit", "ms_per_step", "pct_of_bf16_peak",
+                                              "roofline", "cpu_baseline", "config")}
+            extra[name]["kernel_us_per_step_events"] = leg["detail"]["kernel_us_per_step_events"]
+            extra[name]["hot_kernel_us_per_step_events"] = leg["detail"]["hot_kernel_us_per_step_events"]
+            extra[name]["steps"], extra[name]["warmup"] = steps, warmup
+        line["detail"]["north_star_configs"] = extra
+    print(json.dumps(line), flush=True)
+
+
+# Timed after the headline by the default run (config c3).
+NORTH_STAR_EXTRA = ("c2", "c4", "c5fwd", "c5")
+
+
+def attention_leg(config, args, steps, warmup, cpu_seconds):
+    """Times `steps` steps of one attention config (after `warmup` steps and
+    the clock ramp) and returns its JSON line as a dict."""
+    import gc
+
     import torch
 
     from quantumdlblocks_amd import _native
@@ -351,12 +385,13 @@ def main():
     lib = _native.load()
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[config]
     B, H, T, D = cfg[:4]
     backward = cfg[7]
-    purified = args.config in PURIFIED
-    window = WINDOW.get(args.config, 0)
-    steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
+    purified = config in PURIFIED
+    window = WINDOW.get(config, 0)
+    gc.collect()
+    torch.cuda.empty_cache()
 
     sets = []
     doc = None
@@ -465,11 +500,11 @@ def main():
         roof = {"bound": "mfma", "achieved": round(achieved_tflops, 1), "peak": mfma_peak,
                 "unit": "TFLOP/s", "frac": round(achieved_tflops / mfma_peak, 4)}
     # HBM bytes per step measured by rocprofv3 (all of the step's kernels).
-    roof["traffic"] = load_traffic(args.config)
+    roof["traffic"] = load_traffic(config)
 
     cpu = None
     if not (args.no_cpu_baseline or args.profile):
-        cpu = cpu_baseline(cfg, args.cpu_seconds, args.seed, purified,
+        cpu = cpu_baseline(cfg, cpu_seconds, args.seed, purified,
                            None if doc is None else doc.cpu().numpy(), window)
         cpu["speedup_of_gpu"] = round(value / cpu["value"], 1)
 
@@ -489,7 +524,7 @@ def main():
         "dtype": "bf16 (fp32 weights as two bf16 terms in the forward)" if purified else "bf16",
         "data": "synthetic (seeded N(0,%g) Q, K, V; %d rotated input sets)" % (cfg[4] ** 2, len(sets)),
         "config": {
-            "workload": args.config + (" (headline)" if args.config == "c3" else ""),
+            "workload": config + (" (headline)" if config == "c3" else ""),
             "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
             "doc_mask": doc is not None, "window": window, "backward": backward, "scale": 8.0,
             "eps": PUR_EPS if purified else 1e-12,
@@ -514,7 +549,7 @@ def main():
             "host": platform.node(),
         },
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def prologue_tables(T, n, device=None):
