@@ -38,7 +38,11 @@ How each function is pinned (tests/test_oracle.py):
     independently of this file) on small shapes; hand-computed closed forms
     (T=1, T=2 with D=1); invariants (constant V, scale invariance, window=1,
     window >= T, all-equal / all-distinct doc ids, permutation equivariance,
-    all-negative overlaps give O = 0, row weights sum to (Z-eps)/Z).
+    all-negative overlaps give O = 0, row weights sum to (Z-eps)/Z).  Its
+    ``weight_dtype`` mode (the P.V weights rounded as the reference's kernel
+    casts them): one-key rows whose weights sit on fp16's subnormal edges,
+    worked by hand, and torch evaluating the reference kernel's arithmetic
+    op by op in fp32 (fp16 and bf16).
   * ``backward``: torch.autograd of an independent float64 torch statement of
     the forward, float64 finite differences (torch.autograd.gradcheck), the
     C brute force, and the closed form dscale = (2/s) sum delta eps / Z; the
@@ -71,6 +75,8 @@ float64 finite differences (gradcheck), dg and dtau included.
 from __future__ import annotations
 
 import numpy as np
+
+from .qk_prologue_oracle import round_to
 
 __all__ = [
     "compute_document_ids",
@@ -151,8 +157,14 @@ def born_weights(q, k, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=
     return p / (p.sum(-1, keepdims=True) + eps)
 
 
-def forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None):
-    """Born attention forward in float64.  Returns (O, Z), O (B,H,T,D), Z (B,H,T)."""
+def forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=None, weight_dtype=None):
+    """Born attention forward in float64.  Returns (O, Z), O (B,H,T,D), Z (B,H,T).
+
+    ``weight_dtype`` ("f16" or "bf16"): the weights enter the P.V product
+    rounded to that dtype from their fp32 value, as the reference's kernel
+    casts them (``p.to(v.dtype)``, flash_born.py:182-183), while Z sums them
+    unrounded (:182); a weight below the dtype's smallest subnormal then
+    contributes nothing to O.  None: exact."""
     q, k, v = _f64(q), _f64(k), _f64(v)
     B, H, T, D = q.shape
     r = q @ np.swapaxes(k, -1, -2)
@@ -160,7 +172,8 @@ def forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc_ids=No
     a = a * visible_mask(T, is_causal, window_size, None if doc_ids is None else _f64(doc_ids))
     p = a * a
     Z = p.sum(-1) + eps
-    O = (p @ v) / Z[..., None]
+    pv = p if weight_dtype is None else round_to(p.astype(np.float32), weight_dtype).astype(np.float64)
+    O = (pv @ v) / Z[..., None]
     return O, Z
 
 

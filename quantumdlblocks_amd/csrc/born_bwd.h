@@ -144,9 +144,9 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
-    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
-    // c = min(|s|, 1) (see E::kScaleInSquare); the epilogue divides c back out.
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16 scales the overlap by c = 2|s|, so the dS operand is the
+    // reference's 2 a dP (see E::kScaleInSquare); the epilogue divides c out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     auto pre = [&](float x) __attribute__((always_inline)) {
         if constexpr (E::kScaleInSquare) return x * sq_pre;
         else return x;
@@ -317,7 +317,7 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     }
 
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = 2.f * sc * fabsf(sc) / sq_pre;
+    const float f = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const int qi = q0 + qb * 32 + c;
@@ -408,9 +408,9 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
-    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
-    // c = min(|s|, 1) (see E::kScaleInSquare); the epilogue divides c back out.
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16 scales the overlap by c = 2|s|, so the dS operand is the
+    // reference's 2 a dP (see E::kScaleInSquare); the epilogue divides c out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     auto pre = [&](float x) __attribute__((always_inline)) {
         if constexpr (E::kScaleInSquare) return x * sq_pre;
         else return x;
@@ -581,8 +581,8 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     if (key < T) {
         uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
         uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
-        const float fk = 2.f * sc * fabsf(sc) / sq_pre;
-        const float fv = (sc / sq_pre) * (sc / sq_pre);
+        const float fk = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+        const float fv = E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll

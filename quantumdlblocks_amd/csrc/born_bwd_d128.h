@@ -98,7 +98,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     // Purified: t = gamma r - gamma tau; dR / dP = 4 gamma u^3 + 2 eps_base b.
     float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
     if constexpr (PUR) {
@@ -472,7 +472,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // bytes per lane and store 4 whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
+    const float f = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     {
@@ -546,7 +546,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
     if constexpr (PUR) {
         ptau = p.tau[p.per_head_tau ? h : 0];
@@ -983,14 +983,15 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     for (; u < ntiles; ++u) step();
     }
 
-    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre),
+    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre: 1,
+    // or 2|s| for fp16, where the factors are s and 1/4),
     // packed and staged, one output at a time, in this wave's own 32 rows of
     // the idle ring (row r at smem + RB r, chunks XOR-swizzled by r & 15),
     // then read back 16 bytes per lane and stored 4 whole rows per
     // instruction.
     __syncthreads();  // every wave is done with the ring
-    const float fk = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
-    const float fv = PUR ? 1.f : (sc / sq_pre) * (sc / sq_pre);
+    const float fk = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+    const float fv = PUR ? 1.f : E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
     if constexpr (PUR) {
         // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
         // waves), past the output staging; keys past T excluded (their zero

@@ -188,9 +188,9 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
-    // fp16 keeps its 16-bit dot operands in range by scaling the overlap by
-    // min(|s|, 1) (see E::kScaleInSquare); the epilogue divides it back out.
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16 scales the overlap by c = 2|s|, so the dS operand is the
+    // reference's 2 a dP (see E::kScaleInSquare); the epilogue divides c out.
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     // Purified: t = gamma r - gamma tau; dR / dP = 4 gamma u^3 + 2 eps_base b.
     float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
     if constexpr (PUR) {
@@ -640,7 +640,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // per lane and store 8 whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
+    const float f = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
@@ -791,7 +791,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
-    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? fminf(fabsf(sc), 1.f) : 1.f;
+    const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
     float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
     if constexpr (PUR) {
         ptau = p.tau[p.per_head_tau ? h : 0];
@@ -1125,12 +1125,13 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     }
     (void)kTileLoadsW;
 
-    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre;
+    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre: 1,
+    // or 2|s| for fp16, where the factors are s and 1/4;
     // purified: the accumulators as they are), packed, staged in the idle
     // ring (rows: dK at 0, dV at 128 rows) and stored 16 bytes per lane.
     __syncthreads();
-    const float fk = PUR ? 1.f : 2.f * sc * fabsf(sc) / sq_pre;
-    const float fv = PUR ? 1.f : (sc / sq_pre) * (sc / sq_pre);
+    const float fk = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+    const float fv = PUR ? 1.f : E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
     if constexpr (PUR) {
         // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
         // waves); keys past T excluded.

@@ -52,10 +52,13 @@ __device__ __forceinline__ uint32_t relu_pk16(uint32_t u) {
 // Where the scale enters the 16-bit weights.  bf16 keeps fp32's exponent
 // range, so the scale is folded out of the tile loop (p' = r|r| from the
 // unscaled overlap r, p = s^2 p', restored once per row in the epilogue).
-// fp16 saturates at 65504: it squares c r with c = min(|s|, 1) before the
-// cast (p = (s/c)^2 p').  For |s| < 1 that is the reference's own (s r)^2
-// (flash_born.py:180-183); for |s| >= 1 it is r^2 <= (s r)^2.  Either way a
-// weight overflows only where the reference's overflows too.
+// fp16 (kScaleInSquare) runs the reference's own arithmetic: the forward
+// squares c r with c = |s|, i.e. p = relu(s r)^2 in fp32, and rounds it to
+// fp16 only as the P.V operand (flash_born.py:166-183), so a weight flushes
+// or overflows exactly where the reference's does; the backward scales by
+// c = 2|s|, so its dS operand is the reference's 2 a dP (flash_born.py:
+// 305-311) and its p/Z operand 4 p/Z (at most 4: it flushes later and never
+// overflows).  The epilogues divide c back out.
 struct BF16 {
     static constexpr int kDtype = 2;
     static constexpr bool kScaleInSquare = false;
@@ -100,6 +103,30 @@ struct F16 {
         return (float)__builtin_bit_cast(f16x2, u)[1];
     }
 };
+
+__device__ __forceinline__ float relu_f32(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
+// One pair of Born weights of a tile, packed for the P.V product, added to
+// the row's running sum z.  x0, x1: the overlaps r' (fp32; the sign of the
+// scale folded into Q, masked elements already zero); c: the fp16 scale |s|.
+//   bf16: p' = relu(r')|r'|, rounded to bf16 (the scale goes back in per row
+//         in the epilogue); z adds the rounded weights (one v_dot2c).
+//   fp16: p = relu(c r')^2 = relu(s r)^2 in fp32, the reference's weight
+//         (flash_born.py:166-182), rounded to fp16 only as the P.V operand
+//         (:183); z adds the fp32 weights, as the reference's z_acc does.
+template <class E>
+__device__ __forceinline__ uint32_t born_weight_pair(float x0, float x1, float c, float& z) {
+    if constexpr (E::kScaleInSquare) {
+        const float a0 = relu_f32(x0 * c), a1 = relu_f32(x1 * c);
+        const float p0 = a0 * a0, p1 = a1 * a1;
+        z = (z + p0) + p1;
+        return E::pack(p0, p1);
+    } else {
+        const uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
+        z = E::sum2(u, z);
+        return u;
+    }
+}
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);

@@ -95,9 +95,9 @@ void born_fwd16_kernel(FwdArgs p) {
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
-    // fp16: square min(|s|, 1) r, so no weight overflows unless the
-    // reference's (s r)^2 does too; p = s2 * (accumulated weight).
-    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16: the weights are the reference's relu(s r)^2 (c = |s| times the
+    // sign-folded overlap; born_weight_pair); bf16: s^2 goes back in per row.
+    const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
 
     // Q^T operand, resident for the whole kernel.
     u32x4 qr[NQB][KS];
@@ -270,12 +270,7 @@ void born_fwd16_kernel(FwdArgs p) {
             for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
-                    if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
-                    uint32_t u = E::pack(x0 * fabsf(x0), x1 * fabsf(x1));
-                    u = relu_pk16(u);
-                    zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
-                    pk[qb][j] = u;
+                    pk[qb][j] = born_weight_pair<E>(s[qb][2 * j], s[qb][2 * j + 1], sq_pre, zacc[qb][j & 1]);
                 }
             }
             // V^T operand of the 16-key chunk (nb, hh): lane group G = lane / 16

@@ -136,7 +136,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
-    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16: the reference's weights relu(s r)^2 (born_weight_pair).
+    const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
     // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
     float pg = 0.f, pgt = 0.f, pse = 0.f;
     if constexpr (PUR) {
@@ -305,11 +306,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float x0 = s[2 * j], x1 = s[2 * j + 1];
-            if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
-            const uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
-            zacc[j & 1] = E::sum2(u, zacc[j & 1]);
-            pk[j] = u;
+            pk[j] = born_weight_pair<E>(s[2 * j], s[2 * j + 1], sq_pre, zacc[j & 1]);
         }
     };
 

@@ -94,7 +94,8 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     const int32_t* __restrict__ docb = p.doc + (size_t)b * T;
     const float sc = p.scale[p.per_head_scale ? h : 0];
     const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
-    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16: the reference's weights relu(s r)^2 (born_weight_pair).
+    const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
     // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
     float pg = 0.f, pgt = 0.f, pse = 0.f;
     if constexpr (PUR) {
@@ -275,11 +276,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
         for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
-                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
-                uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
-                zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
-                pk[qb][j] = u;
+                pk[qb][j] = born_weight_pair<E>(s[qb][2 * j], s[qb][2 * j + 1], sq_pre, zacc[qb][j & 1]);
             }
         }
     };

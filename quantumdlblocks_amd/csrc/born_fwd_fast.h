@@ -14,13 +14,13 @@
 //     (32 banks x 4 bytes).  Each lane picks the global chunk that belongs in
 //     its fixed LDS slot.  Rows >= T lie beyond the buffer's num_records and
 //     arrive as zeros.
-//   * A workgroup handles one 256-row query block, or (the paired launch,
-//     dense with at least 512 pairs) two blocks of one (batch, head), mb and
-//     nmb-1-mb, the second block's Q and first K/V tiles loaded while the
-//     first block finishes.  Causal launches take one block per workgroup,
-//     longest key ranges first: the dispatcher then gives each CU's freed
-//     slot the next block, which evens out the two co-resident workgroups'
-//     unequal rates better than pairs of equal causal work do.
+//   * A workgroup handles one 256-row query block, or (the paired launch)
+//     two blocks of one (batch, head), mb and nmb-1-mb, the second block's Q
+//     and first K/V tiles loaded while the first block finishes.  Dense
+//     launches pair when that still gives every CU two workgroups; causal
+//     ones when a head has at most four blocks (fast_fwd_causal_paired).
+//     Otherwise one block per workgroup, longest key ranges first: the
+//     dispatcher then gives each CU's freed slot the next block.
 //   * K/V tiles of both blocks form one sequence through a ring of three LDS
 //     stages: tile u+2 is issued right after the barrier that starts tile u,
 //     and tile u is waited for only at that barrier, so every load has two
@@ -219,9 +219,9 @@ void born_fwd16_fast_kernel(
         pgt = -sc * p.tau[p.per_head_tau ? h : 0];
         pse = sqrtf(p.eps_base);
     }
-    // fp16: square min(|s|, 1) r, so no weight overflows unless the
-    // reference's (s r)^2 does too; p = s2 * (accumulated weight).
-    const float sq_pre = E::kScaleInSquare ? fminf(fabsf(sc), 1.f) : 1.f;
+    // fp16: the weights are the reference's relu(s r)^2 (c = |s| times the
+    // sign-folded overlap; born_weight_pair); bf16: s^2 goes back in per row.
+    const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)RBG;
     // Bytes between consecutive Q / K rows: 2 D, or the raw rows' time stride
@@ -359,11 +359,7 @@ void born_fwd16_fast_kernel(
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                float x0 = s[qb][2 * j], x1 = s[qb][2 * j + 1];
-                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
-                uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
-                zacc[qb][j & 1] = E::sum2(u, zacc[qb][j & 1]);
-                pk[qb][j] = u;
+                pk[qb][j] = born_weight_pair<E>(s[qb][2 * j], s[qb][2 * j + 1], sq_pre, zacc[qb][j & 1]);
             }
         }
     };

@@ -5,7 +5,9 @@ as the reference does (flash_born.py:277, 302, 387).
 
 Tolerances (normwise relative error): 2e-2 for bf16 / fp16, 1e-5 for fp32.
 dscale is compared against the scale of its terms, (2/|s|) eps sum|delta/Z|,
-because its value is itself a small difference.
+because its value is itself a small difference.  fp16 cases default to
+N(0, 0.25) inputs, inside the range where the reference's fp16 forward
+weights (s q.k)^2 do not overflow at scale 8.
 """
 
 from __future__ import annotations
@@ -44,13 +46,18 @@ FLOOR = {torch.float32: 1e-6, torch.bfloat16: 1e-4, torch.float16: 1e-4}
 
 
 def _grad_ok(got, ref, mag, dtype, tol=None):
+    """(passed, branch, normwise error, error against the term scale); branch
+    names the test a passing gradient met: "rel" (normwise within TOL) or
+    "floor" (only within FLOOR of its terms' scale), "FAIL" otherwise."""
     e_rel = rel_err(got, ref)
     e_floor = max_abs(got, ref) / mag.max() if mag.size and mag.max() > 0 else max_abs(got, ref)
-    return (e_rel <= (tol or TOL[dtype]) or e_floor <= FLOOR[dtype]), e_rel, e_floor
+    branch = "rel" if e_rel <= (tol or TOL[dtype]) else ("floor" if e_floor <= FLOOR[dtype] else "FAIL")
+    return branch != "FAIL", branch, e_rel, e_floor
 
 
 def _check_bwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, window_size=0, doc=None,
-               std=1.0, seed=0, heads=None, tol=None, check_dscale=False):
+               std=None, seed=0, heads=None, tol=None, check_dscale=False):
+    std = (0.5 if dtype == torch.float16 else 1.0) if std is None else std
     q, k, v, do = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, n=4, dtype=dtype))
     doc_t = None if doc is None else torch.as_tensor(doc, dtype=torch.int32, device=dev)
     sc_np = np.asarray(scale, dtype=np.float32)
@@ -93,8 +100,8 @@ def _check_bwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, 
     for i, name in enumerate(("dq", "dk", "dv")):
         got, ref, mag = (np.concatenate(x[i]) for x in (gots, refs, mags))
         assert np.isfinite(got).all(), name
-        ok, e_rel, e_floor = _grad_ok(got, ref, mag, dtype, tol)
-        msgs.append(f"{name}:rel={e_rel:.2e}/floor={e_floor:.2e}")
+        ok, branch, e_rel, e_floor = _grad_ok(got, ref, mag, dtype, tol)
+        msgs.append(f"{name}:rel={e_rel:.2e}/floor={e_floor:.2e}[{branch}]")
         if not ok:
             fails.append(name)
     print(f"bwd B{B} H{H} T{T} D{D} {dtype} causal={is_causal} W={window_size} doc={doc is not None} "
@@ -128,7 +135,8 @@ def test_bwd_c1_shape(cuda_device, dtype, is_causal):
 @pytest.mark.parametrize("scale", [0.05, -0.3, 8.0])
 def test_bwd_f16_operand_range(cuda_device, D, window, scale):
     """fp16 dot operands (p/Z and dS) stay in range for small scales with large
-    overlaps, as the reference's do (the kernel scales the overlap by min(|s|, 1))."""
+    overlaps, as the reference's do (the kernel's dS operand is the
+    reference's 2 a dP, its p/Z operand 4 p/Z)."""
     std = 4.0 if abs(scale) < 1 else 0.5
     _check_bwd(1, 2, 300, D, torch.float16, cuda_device, scale=scale, std=std, window_size=window, seed=3)
 

@@ -3,6 +3,13 @@ float64 CPU oracle on the same (dtype-rounded) inputs.
 
 Tolerances (normwise relative error max|out-ref|/max|ref|): 1e-5 for fp32,
 2e-2 for bf16 / fp16, as stated for this path; max-abs error is printed.
+
+fp16 runs the reference's own weight arithmetic (p = (s q.k)^2 in fp32,
+rounded to fp16 as the P.V operand, Z from the fp32 weights), so fp16 cases
+are held to the oracle that rounds the weights the same way, every row of O
+to 2e-2; their default inputs are N(0, 0.25), which keeps (s q.k)^2 inside
+fp16's range at scale 8 (beyond 65504 the reference's fp16 weights overflow,
+and the kernel's with them).
 """
 
 from __future__ import annotations
@@ -14,7 +21,7 @@ import pytest
 import torch
 
 from oracle import born_oracle as orc
-from util import TOL, abi_forward, f64, max_abs, oracle_forward_heads, rel_err, seeded_inputs
+from util import TOL, abi_forward, f64, max_abs, oracle_forward_heads, rel_err, row_errors, seeded_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -28,11 +35,19 @@ def _run(q, k, v, scale, **kw):
 
 
 def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, window_size=0,
-               doc=None, std=1.0, seed=0, heads=None, tol=None, inputs=None):
+               doc=None, std=None, seed=0, heads=None, tol=None, inputs=None, weight_dtype="auto", row_tol="auto"):
     """Run the public entry on seeded inputs and hold O to the oracle
     (normwise relative error <= tol) and Z, read through the C ABI, to the
-    oracle row by row within the rounding bound of the 16-bit weights
-    (util.z_row_bound).  ``heads``: the (b, h) heads to check, or "all"."""
+    oracle row by row within the rounding bound of the weights
+    (util.z_row_bound).  ``heads``: the (b, h) heads to check, or "all".
+    ``weight_dtype``: the oracle rounds the P.V weights as the reference's
+    kernel does (oracle.forward); ``row_tol``: every row of O is also held to
+    it (per-row normwise error; the worst row is printed either way).  fp16
+    defaults: std 0.5, weights rounded to fp16 in the oracle, rows to 2e-2."""
+    f16 = dtype == torch.float16
+    std = (0.5 if f16 else 1.0) if std is None else std
+    weight_dtype = ("f16" if f16 else None) if weight_dtype == "auto" else weight_dtype
+    row_tol = (2e-2 if f16 else None) if row_tol == "auto" else row_tol
     if inputs is None:
         q, k, v = (x.to(dev) for x in seeded_inputs((B, H, T, D), seed=seed, std=std, dtype=dtype))
     else:
@@ -52,8 +67,10 @@ def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, 
     sel = [(b, h) for b in range(B) for h in range(H)] if heads in (None, "all") else heads
     sc = np.asarray(scale, dtype=np.float64).reshape(-1)
     qn, kn, vn = f64(q), f64(k), f64(v)
-    keys, ref, zref, zb = oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, dtype)
+    keys, ref, zref, zb = oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, dtype,
+                                               weight_dtype=weight_dtype)
     got = np.stack([f64(out[b, h]) for b, h in keys])
+    rows = row_errors(got, ref) if eps != 0.0 else np.zeros(1)
     if eps == 0.0:
         # rows with no positive overlap are 0/0 in the reference formula: NaN
         # must appear exactly there, everything else is compared
@@ -69,9 +86,12 @@ def _check_fwd(B, H, T, D, dtype, dev, *, scale=8.0, is_causal=True, eps=1e-12, 
         zrel = float((zerr / np.maximum(np.abs(zref), 1e-300)).max()) if zerr.size else 0.0
         zmsg = f" Z: max row rel={zrel:.3e} (max err/bound {zratio:.3f})"
     print(f"fwd B{B} H{H} T{T} D{D} {dtype} causal={is_causal} W={window_size} doc={doc is not None} "
-          f"heads={len(keys)} rel={err:.3e} maxabs={max_abs(got, ref):.3e}{zmsg}", flush=True)
+          f"heads={len(keys)} rel={err:.3e} maxabs={max_abs(got, ref):.3e} worst row={rows.max():.3e}"
+          f"{' (weights ' + weight_dtype + ')' if weight_dtype else ''}{zmsg}", flush=True)
     assert np.isfinite(got).all()
     assert err <= (tol or TOL[dtype]), err
+    if row_tol is not None:
+        assert rows.max() <= row_tol, f"worst row of O: {rows.max():.3e}"
     if z is not None:
         assert np.all(zerr <= zb), f"Z outside its rounding bound: {zratio}"
     return out
@@ -115,15 +135,53 @@ def test_fwd_d64_many_heads(cuda_device, T, is_causal, dtype):
     _check_fwd(B, H, T, 64, dtype, cuda_device, scale=sc, is_causal=is_causal, std=0.125, seed=T, heads=sel)
 
 
-@pytest.mark.parametrize("D, window", [(64, 0), (64, 100), (32, 0)])
+@pytest.mark.parametrize("D, window", [(64, 0), (64, 100), (32, 0), (128, 0)])
 @pytest.mark.parametrize("scale", [0.05, -0.3, 8.0])
 def test_fwd_f16_weight_range(cuda_device, D, window, scale):
     """fp16 weights saturate at 65504.  With |q.k| up to ~600 a small scale
-    keeps the reference's (s q.k)^2 in range, and so must the kernel (fp16
-    squares min(|s|, 1) q.k); with scale 8 the kernel's weights stay in range
-    too (r^2 <= (s r)^2)."""
+    keeps the reference's (s q.k)^2 in range, and so must the kernel, whose
+    fp16 weights are the reference's own (s r)^2; every row of O is held to
+    the oracle that rounds the weights as the reference's kernel does."""
     std = 4.0 if abs(scale) < 1 else 0.5
-    _check_fwd(1, 2, 300, D, torch.float16, cuda_device, scale=scale, std=std, window_size=window, seed=3)
+    _check_fwd(1, 2, 300, D, torch.float16, cuda_device, scale=scale, std=std, window_size=window, seed=3,
+               weight_dtype="f16", row_tol=2e-2)
+
+
+@pytest.mark.parametrize("D", [64, 128, 48])
+@pytest.mark.parametrize("scale", [8.0, -8.0, 0.5])
+def test_fwd_f16_tiny_overlaps_flush_like_the_reference(cuda_device, D, scale):
+    """One-key rows (causal window 1) whose single weight p = (s q.k)^2 sits
+    around fp16's subnormal range: the reference's kernel rounds p to fp16 for
+    P.V (flash_born.py:183), so a row keeps v (p a subnormal) or drops to 0
+    (p below half the smallest subnormal, 2^-25) exactly where the rounded p
+    does.  q.k is exact (one non-zero coordinate each), and every row of O is
+    held to the oracle that rounds the weights the same way; the kernels that
+    squared min(|s|, 1) q.k flushed rows whose weight the reference keeps."""
+    from quantumdlblocks_amd import flash_born_attention
+
+    dev = cuda_device
+    T = 64
+    targets = 2.0 ** -np.linspace(8, 30, T)  # weights p from 2^-8 down to 2^-30
+    r = np.sqrt(targets) / abs(scale)
+    q = np.zeros((1, 2, T, D), np.float32)
+    k = np.zeros((1, 2, T, D), np.float32)
+    q[0, :, :, 3] = r.astype(np.float16).astype(np.float32)
+    k[0, :, :, 3] = 1.0
+    k[0, 1, :, 3] = np.sign(scale)  # head 1: positive overlaps under either sign of the scale
+    g = torch.Generator().manual_seed(D)
+    v = torch.randn(1, 2, T, D, generator=g)
+    qt, kt, vt = (torch.as_tensor(x).to(dev, torch.float16) for x in (q, k, v))
+    out = flash_born_attention(qt, kt, vt, scale, window_size=1)
+    torch.cuda.synchronize()
+    ref, _ = orc.forward(f64(qt), f64(kt), f64(vt), scale, True, 1e-12, 1, weight_dtype="f16")
+    exact, _ = orc.forward(f64(qt), f64(kt), f64(vt), scale, True, 1e-12, 1)
+    got = f64(out)
+    rows = row_errors(got, ref)
+    kept = np.abs(ref).max(-1) > 0
+    print(f"f16 one-key rows D{D} s={scale}: kept {int(kept.sum())} of {kept.size}, worst row {rows.max():.3e}, "
+          f"rows the exact oracle keeps {int((np.abs(exact).max(-1) > 0).sum())}", flush=True)
+    assert kept.sum() > 0 and (~kept).sum() > 0, "the rows must span the flush threshold"
+    assert rows.max() <= 2e-3, rows.max()
 
 
 @pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 80, 96, 112, 128, 160, 192, 256, 20, 3])
@@ -279,11 +337,14 @@ def test_fwd_d128_documents(cuda_device, dtype, is_causal):
     _check_fwd(1, 2, 600, 128, dtype, cuda_device, is_causal=is_causal, doc=doc, scale=0.2, std=0.7, seed=7)
 
 
-# (A one-key window leaves each row a single weight: fp16 rounds the weights
-# of tiny overlaps to zero, as the reference's kernel does, and the row's
-# output with them, while the float64 oracle keeps them; so bf16 only there.)
-@pytest.mark.parametrize("dtype,window", [(torch.bfloat16, 1)] + [(d, w) for d in (torch.bfloat16, torch.float16)
-                                                                  for w in (33, 100, 300, 2000)])
+# A one-key window leaves each row a single weight, which fp16 rounds for
+# P.V as the reference's kernel does (a tiny overlap's row drops to 0 with
+# it): the fp16 rows are held, row by row, to the oracle that rounds the
+# weights likewise (_check_fwd's fp16 default).
+WINDOW_DOC_CASES = [(d, w) for d in (torch.bfloat16, torch.float16) for w in (1, 33, 100, 300, 2000)]
+
+
+@pytest.mark.parametrize("dtype,window", WINDOW_DOC_CASES)
 def test_fwd_documents_and_window_fast(cuda_device, dtype, window):
     """D = 64 with document ids and a causal sliding window: the document
     kernel's window mode (candidates from the block's first window, window
@@ -297,11 +358,7 @@ def test_fwd_documents_and_window_fast(cuda_device, dtype, window):
                scale=0.5, std=0.7, seed=window + 3)
 
 
-# (A one-key window leaves each row a single weight: fp16 rounds the weights
-# of tiny overlaps to zero, as the reference's kernel does, and the row's
-# output with them, while the float64 oracle keeps them; so bf16 only there.)
-@pytest.mark.parametrize("dtype,window", [(torch.bfloat16, 1)] + [(d, w) for d in (torch.bfloat16, torch.float16)
-                                                                  for w in (33, 100, 300, 2000)])
+@pytest.mark.parametrize("dtype,window", WINDOW_DOC_CASES)
 def test_fwd_d128_documents_and_window(cuda_device, dtype, window):
     """D = 128 with document ids and a causal sliding window: the document
     mode's window bounds (candidate tiles from the block's first window,
@@ -455,6 +512,25 @@ def test_fwd_config_c2(cuda_device):
     q, k = l2_normalize(q), l2_normalize(k)
     q, k, v = (x.to(cuda_device, torch.bfloat16) for x in (q, k, v))
     _check_fwd(B, H, T, D, torch.bfloat16, cuda_device, heads="all", inputs=(q, k, v))
+
+
+def test_fwd_config_c2_f16_rows(cuda_device):
+    """C2's shape and recipe in fp16 (L2-normalised Q and K, scale 8: many
+    overlaps are small, so many weights are fp16 subnormals): every head;
+    every row of O within 2e-2 of the oracle that rounds the weights as the
+    reference's kernel does, Z within its bound from the reference's fp32
+    weights; the worst row against the exact oracle is printed too."""
+    from quantumdlblocks_amd import l2_normalize
+
+    B, H, T, D = 32, 4, 1024, 64
+    q, k, v = seeded_inputs((B, H, T, D), seed=0)
+    q, k = l2_normalize(q), l2_normalize(k)
+    q, k, v = (x.to(cuda_device, torch.float16) for x in (q, k, v))
+    out = _check_fwd(B, H, T, D, torch.float16, cuda_device, heads="all", inputs=(q, k, v), weight_dtype="f16",
+                     row_tol=2e-2)
+    exact, _ = orc.forward(f64(q[:2]), f64(k[:2]), f64(v[:2]), 8.0)
+    print(f"C2 fp16, batch rows 0-1 against the exact oracle: worst row {row_errors(f64(out[:2]), exact).max():.3e}, "
+          f"normwise {rel_err(f64(out[:2]), exact):.3e}", flush=True)
 
 
 def test_fwd_config_c3(cuda_device):

@@ -233,6 +233,56 @@ def test_document_special_cases():
     np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-15)
 
 
+def test_weight_rounding_one_key_rows_by_hand():
+    """forward(weight_dtype="f16") on one-key rows (window 1), r = q . k exact:
+    the weight p = (s r)^2 enters O as fp16(p), so O_i = v_i fp16(p)/(p + eps).
+    Chosen so fp16(p) is known exactly: 2^-22 and 2^-24 (subnormals, kept
+    exactly), 2^-26 (below half the smallest subnormal: 0), 9 2^-28 (rounds up
+    to 2^-24), 2^-10 (normal).  Z keeps the unrounded p."""
+    s = 8.0
+    p = np.array([2.0 ** -22, 2.0 ** -24, 2.0 ** -26, 9 * 2.0 ** -28, 2.0 ** -10])
+    fp16p = np.array([2.0 ** -22, 2.0 ** -24, 0.0, 2.0 ** -24, 2.0 ** -10])
+    r = np.sqrt(p) / s
+    T = p.size
+    q = np.zeros((1, 1, T, 4))
+    k = np.zeros((1, 1, T, 4))
+    q[..., 0] = r
+    k[..., 0] = 1.0
+    v = np.arange(1.0, 4 * T + 1).reshape(1, 1, T, 4)
+    O, Z = orc.forward(q, k, v, s, True, 1e-12, 1, weight_dtype="f16")
+    np.testing.assert_allclose(Z[0, 0], p + 1e-12, rtol=1e-14)
+    np.testing.assert_allclose(O[0, 0], v[0, 0] * (fp16p / (p + 1e-12))[:, None], rtol=1e-12, atol=0)
+    O_exact, _ = orc.forward(q, k, v, s, True, 1e-12, 1)
+    np.testing.assert_allclose(O_exact[0, 0], v[0, 0] * (p / (p + 1e-12))[:, None], rtol=1e-12)
+
+
+@pytest.mark.parametrize("wd,tdtype", [("f16", torch.float16), ("bf16", torch.bfloat16)])
+def test_weight_rounding_matches_torch_kernel_arithmetic(wd, tdtype):
+    """forward(weight_dtype=...) against torch evaluating the reference
+    kernel's arithmetic op by op in fp32 (s = (q k^T) scale, a = relu(s) M,
+    p = a a, z = sum p + eps, O = (p.to(dtype) @ v) / z; flash_born.py:166-186),
+    on fp16-representable inputs with a wide spread of overlap magnitudes."""
+    g = torch.Generator().manual_seed(3)
+    q = (torch.randn(1, 2, 48, 16, generator=g) * torch.logspace(-4, 0, 48).view(1, 1, 48, 1)).to(tdtype)
+    k = torch.randn(1, 2, 48, 16, generator=g).to(tdtype)
+    v = torch.randn(1, 2, 48, 16, generator=g).to(tdtype)
+    scale = 6.0
+    qf, kf, vf = q.float(), k.float(), v.float()
+    for causal, window in ((True, 0), (True, 1), (False, 5)):
+        mask = torch.from_numpy(orc.visible_mask(48, causal, window)).float()
+        sc = (qf @ kf.transpose(-1, -2)) * scale
+        a = sc.clamp_min(0) * mask
+        pt = a * a
+        zt = pt.sum(-1) + 1e-12
+        ot = (pt.to(tdtype).float() @ vf) / zt[..., None]
+        O, Z = orc.forward(qf.double().numpy(), kf.double().numpy(), vf.double().numpy(), scale, causal, 1e-12,
+                           window, weight_dtype=wd)
+        np.testing.assert_allclose(Z, zt.double().numpy(), rtol=1e-5)
+        err = np.abs(O - ot.double().numpy()).max() / np.abs(ot.double().numpy()).max()
+        assert err <= 2e-3, (causal, window, err)
+        assert np.array_equal(O == 0, ot.double().numpy() == 0), "flushed rows differ"
+
+
 def test_permutation_equivariance():
     B, H, T, D = 3, 4, 16, 8
     q, k, v = _rand((B, H, T, D), seed=5)

@@ -64,11 +64,12 @@ def abi_forward(q, k, v, scale, is_causal=True, eps=1e-12, window_size=0, doc=No
     return out, z
 
 
-# Relative rounding of one weight p' as the kernels store it before it is
-# summed into Z: bf16 / fp16 round p' to the dtype (unit roundoff 2^-8 /
-# 2^-11: the row sums are formed from the 16-bit weights that feed the P.V
-# product), fp32 keeps p in fp32.
-_Z_UNIT = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24}
+# Relative rounding of one weight p' as the kernels form it before it is
+# summed into Z.  bf16 rounds p' to bf16 (unit roundoff 2^-8: the row sums are
+# formed from the 16-bit weights that feed the P.V product).  fp16 keeps the
+# reference's fp32 weight p = (s r)^2 (two fp32 roundings: the scale times the
+# overlap, the square), as does fp32.
+_Z_UNIT = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -22, torch.float32: 2.0 ** -24}
 
 
 def z_row_bound(q, k, scale, z_ref, eps, dtype, mask):
@@ -76,13 +77,16 @@ def z_row_bound(q, k, scale, z_ref, eps, dtype, mask):
 
     Z_ref = sum_j p_ij + eps in exact arithmetic on the dtype-rounded inputs;
     the kernel computes r_ij = q_i . k_j in fp32 (exact products of 16-bit or
-    fp32 inputs, D-term fp32 sums: |dr| <= D 2^-24 sum_a |q_ia k_ja|), squares
-    it, rounds the weight to the dtype (relative u, plus 2^-25 (s/c)^2
-    absolute below fp16's normal range, c = min(|s|, 1)), and sums the
-    n_i visible weights in fp32 (relative n_i 2^-23), then scales by s^2 and
-    adds eps (two more roundings).  Hence
+    fp32 inputs, D-term fp32 sums: |dr| <= D 2^-24 sum_a |q_ia k_ja|), forms
+    the weight (bf16: r|r| rounded to bf16, relative u = 2^-8, and 2^-126 s^2
+    absolute below bf16's normal range; fp16 and fp32: the fp32 weight, u a
+    few fp32 roundings), and sums the n_i visible weights in fp32 (relative
+    n_i 2^-23), then scales by s^2 (bf16; 1 for fp16) and adds eps (two more
+    roundings).  Hence
       |dZ_i| <= (u + n_i 2^-23 + 2^-22) sum_j p_ij
                 + s^2 sum_j m_ij (2|r_ij| + dr_ij) dr_ij + n_i a + 2^-23 eps.
+    For fp16 this is the reference's own arithmetic (Z from the fp32 weights,
+    flash_born.py:180-182) up to the fp32 summation order.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -98,15 +102,19 @@ def z_row_bound(q, k, scale, z_ref, eps, dtype, mask):
     u = _Z_UNIT[dtype]
     s2 = (s * s)[..., 0]
     term_r = (s * s * m * (2.0 * np.abs(r) + dr) * dr).sum(-1)
-    if dtype == torch.float16:
-        c = np.minimum(np.abs(s), 1.0)[..., 0]
-        with np.errstate(divide="ignore", invalid="ignore"):
-            absolute = np.where(c > 0, 2.0 ** -25 * s2 / np.where(c > 0, c * c, 1.0), 0.0)
-    elif dtype == torch.bfloat16:
-        absolute = 2.0 ** -126 * s2
-    else:
-        absolute = 2.0 ** -149 * s2
+    absolute = (2.0 ** -126 if dtype == torch.bfloat16 else 2.0 ** -149) * s2
     return (u + n * 2.0 ** -23 + 2.0 ** -22) * np.abs(psum) + term_r + n * absolute + 2.0 ** -23 * abs(eps)
+
+
+def row_errors(got, ref, floor=0.0):
+    """Per-row normwise relative error of O: max_d |got - ref| / max_d |ref|
+    for each row (last axis D), with rows whose reference is 0 judged by their
+    absolute error against ``floor``."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    num = np.abs(got - ref).max(-1)
+    den = np.abs(ref).max(-1)
+    return np.where(den > 0, num / np.where(den > 0, den, 1.0), np.where(num <= floor, 0.0, np.inf))
 
 
 def doc_spans(row):
@@ -122,7 +130,8 @@ def doc_spans(row):
     return list(zip(starts.tolist(), stops.tolist()))
 
 
-def oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, dtype, chunk=16):
+def oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, dtype, chunk=16,
+                         weight_dtype=None):
     """Oracle O and Z for the selected (b, h) heads, and the per-row bound on
     the kernel's Z (util.z_row_bound).  Heads of one batch row are stacked
     into one (1, n, T, D) call.  Causal rows of documents that form
@@ -144,13 +153,13 @@ def oracle_forward_heads(qn, kn, vn, sc, sel, is_causal, eps, window_size, doc, 
                 bd = np.empty((1, len(hh), T))
                 for a, e in doc_spans(doc[b]):
                     qs, ks, vs = (x[b : b + 1, hh, a:e] for x in (qn, kn, vn))
-                    o[..., a:e, :], z[..., a:e] = orc.forward(qs, ks, vs, s_h, True, eps)
+                    o[..., a:e, :], z[..., a:e] = orc.forward(qs, ks, vs, s_h, True, eps, weight_dtype=weight_dtype)
                     bd[..., a:e] = z_row_bound(qs, ks, s_h, z[..., a:e], eps, dtype,
                                                orc.visible_mask(e - a, True, 0))
             else:
                 dd = None if doc is None else doc[b : b + 1]
                 qs, ks, vs = (x[b : b + 1, hh] for x in (qn, kn, vn))
-                o, z = orc.forward(qs, ks, vs, s_h, is_causal, eps, window_size, dd)
+                o, z = orc.forward(qs, ks, vs, s_h, is_causal, eps, window_size, dd, weight_dtype=weight_dtype)
                 bd = z_row_bound(qs, ks, s_h, z, eps, dtype, orc.visible_mask(T, is_causal, window_size, dd))
             refs.append(o)
             zrefs.append(z)
