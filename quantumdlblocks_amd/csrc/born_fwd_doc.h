@@ -4,8 +4,9 @@
 // Same arithmetic, row layout and four-phase tile as born_fwd16_fast_kernel
 // (born_fwd_fast.h).  What differs is the set of key tiles a query block
 // visits, which depends on the document ids:
-//   * One 256-row query block per workgroup (two workgroups per CU), the
-//     blocks of the longest key ranges launched first.  Q goes straight from
+//   * One 256-row query block per workgroup (two workgroups per CU), or
+//     128 rows (four per CU: the Born launch, see NW below), the blocks of
+//     the longest key ranges launched first.  Q goes straight from
 //     HBM into registers, so LDS holds only the K/V ring (three stages of a
 //     K tile, a V tile and the tile's 64 key document ids) and the tile list.
 //   * Candidate key tiles (up to the block's last row under causality) are
@@ -43,25 +44,34 @@ namespace qdl {
 // candidate tiles start at the block's first row's window, tiles that start
 // before the block's last row's window are tested per element, and the test
 // also drops keys before the row's window.
-template <class E, int DP, bool PUR = false, bool WIN = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+//
+// NW: waves per workgroup, 4 (256-row blocks, two workgroups per CU, a ring
+// of three stages) or 2 (128-row blocks, four workgroups per CU, a ring of
+// two stages: 40 KiB of LDS each).  Every wave holds two 32-row column blocks
+// either way; 128-row blocks straddle fewer document edges and cut the
+// causal diagonal finer (C4's documents: 1.28x the visible pairs executed
+// against 1.53x for 256-row blocks).
+template <class E, int DP, bool PUR = false, bool WIN = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
-    constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = 256;
+    static_assert(NW == 4 || NW == 2, "256- or 128-row blocks");
+    constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = 64 * NW;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
-    constexpr int CAP = 256;               // candidate tiles screened per pass (one per thread)
-    // Loads per wave per tile: K, V and a 64-byte slice of the key document ids.
+    constexpr int CAP = 64 * NW;           // candidate tiles screened per pass (one per thread)
+    constexpr int KDW = BN / NW;           // key document ids loaded per wave per tile
+    // Loads per wave per tile: K, V and a slice of the key document ids.
     constexpr int kTileLoads = 2 * LPW + 1;
-    static_assert(TB % (1024 * NW) == 0 && BN == 64 && BM == 4 * BN, "tile split");
+    static_assert(TB % (1024 * NW) == 0 && BN == 64 && KDW % 4 == 0, "tile split");
 
     // One buffer: the K/V ring during the tile loop, the output staging
-    // (256 rows x 128 bytes) once the loop is done.
+    // (BM rows x 128 bytes) once the loop is done.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
     __shared__ __attribute__((aligned(16))) int32_t kd_lds[NST * BN];  // key document ids per stage
     __shared__ int32_t t_list[CAP];                                   // kept tiles, ascending
@@ -109,13 +119,14 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
     const i32x4 rd = buffer_rsrc(docb, (uint32_t)T * 4u);
 
-    // Rows: column c of block qb -> row R + 128 qb + 64 (c / 16) + 16 wave + c % 16.
-    const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
+    // Rows: column c of block qb -> row R + (BM/2) qb + (BM/4) (c / 16) +
+    // 16 wave + c % 16: every wave has 16-row pieces of each quarter.
+    const int lrow = (BM / 4) * (c >> 4) + 16 * wave + (c & 15);
     int qrow[NQB], qdoc[NQB];
     u32x4 qr[NQB][KS];
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-        qrow[qb] = R + 128 * qb + lrow;
+        qrow[qb] = R + (BM / 2) * qb + lrow;
         const bool ok = qrow[qb] < T;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -238,7 +249,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off + ((pc ^ (row & 7)) << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off + ((pc ^ ((row & 3) << 1)) << 4));
         }
-        if (lane < 4) dma_load16(rd, lds_addr(kd_lds + st * BN + wave * 16), (key0 + wave * 16 + lane * 4) * 4);
+        if (lane < KDW / 4) dma_load16(rd, lds_addr(kd_lds + st * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
 
     f32x16 oacc[DB][NQB];
@@ -485,21 +496,22 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // Pipeline over the kept tiles of each screened chunk: tiles 0 and 1
-    // issued up front, tile u+2 right after the barrier that starts step u;
-    // at that barrier each wave has waited for its share of tile u (loads
-    // return in order: only tile u+1's may still be in flight).
+    // Pipeline over the kept tiles of each screened chunk: tiles 0 .. NST-2
+    // issued up front, tile u+NST-1 right after the barrier that starts step
+    // u (the stage of tile u-1, which every wave has left by then); at that
+    // barrier each wave has waited for its share of tile u (loads return in
+    // order: only the later tiles' may still be in flight).
     for (int c0 = 0; c0 < ncand; c0 += CAP) {
         const int n = screen(c0, min(CAP, ncand - c0));
         if (n > 0) issue(0);
-        if (n > 1) issue(1);
+        if (NST == 3 && n > 1) issue(1);
         for (int u = 0; u < n; ++u) {
-            if (u + 1 < n)
+            if (NST == 3 && u + 1 < n)
                 wait_vmcnt<kTileLoads>();
             else
                 wait_vmcnt<0>();
             __syncthreads();
-            if (u + 2 < n) issue(u + 2);
+            if (u + NST - 1 < n) issue(u + NST - 1);
             // Stage offset opaque to the optimiser (addresses formed per tile).
             int soff = (u % NST) * TB;
             asm volatile("" : "+s"(soff));
@@ -510,7 +522,8 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
             read_k(kop, kb, 0);
             // A column block needs the element test on the causal diagonal
-            // (tiles t0 .. t0+3: block 0 in all four, block 1 in the last two)
+            // (256-row blocks: tiles t0 .. t0+3, block 0 in all four, block 1
+            // in the last two; 128-row blocks: t0, t0+1 and t0+1)
             // and where the tile's keys span several documents.  Off the
             // diagonal, keys of one document are visible to the rows of that
             // document and to no other: unless all 32 rows are in it, a
@@ -523,7 +536,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             // Window: both blocks tested where a row's window starts.
             const bool cut = WIN && ti * BN < kwin;
             const bool m0 = rel >= 0 || mixed || tail || cut;
-            const bool m1 = rel >= 2 || mixed || tail || cut;
+            const bool m1 = rel >= BM / 128 || mixed || tail || cut;
             tile(kb, vb, kd, ti * BN, m0, m1, td != qsd[0], td != qsd[1], qdoc[0] == td, qdoc[1] == td, !mixed);
         }
         __syncthreads();  // the list and the ring are reused by the next chunk
@@ -537,7 +550,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
         for (int qb = 0; qb < NQB; ++qb) {
             const float zl = zacc[qb][0] + zacc[qb][1];
             const float zd = zl + __shfl_xor(zl, 32) + p.eps;
-            const int qi = R + 128 * qb + lrow;
+            const int qi = R + (BM / 2) * qb + lrow;
             if (qi < T) {
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
@@ -563,14 +576,14 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     // here rather than hoisted and kept live across the tile loop.)
     int ln = lane;
     asm volatile("" : "+v"(ln));
-    const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+    const int lr = (BM / 4) * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
     const int gg = ln >> 5;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const float zl = zacc[qb][0] + zacc[qb][1];
         const float zt = zl + __shfl_xor(zl, 32);
         const float rcp = 1.0f / (zt + eps_s);
-        const int row = 128 * qb + lr;
+        const int row = (BM / 2) * qb + lr;
         uint8_t* rb = smem + row * RB;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -588,17 +601,23 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     const int chunk = ln & 7;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
+        const int row = (BM / 4) * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
         const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
         const int qi = R + row;
         if (qi < T) __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * DP + chunk * 8));
     }
 }
 
+// Born with documents: 128-row blocks (the document ids live on the device,
+// so the host cannot look at their lengths).  Against 256-row blocks, on
+// B4 H16 T8192 bf16 (one box, best of 5 x 50 launches): geometric documents
+// of mean 128 / 512 / 2048 tokens 103.7 -> 83.7, 150.9 -> 142.9, 312.4 ->
+// 313.1 us; one document per row 519.5 -> 548.2 us.
 template <class E, int DP, bool WIN = false>
 hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
-    const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP, false, WIN>), grid, dim3(256), 0, st, a);
+    constexpr int NW = 2, BM = 64 * NW;
+    const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP, false, WIN, NW>), grid, dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 

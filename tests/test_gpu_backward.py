@@ -40,8 +40,11 @@ def _grads(q, k, v, do, scale, **kw):
 
 # A gradient passes if its normwise relative error is within TOL, or -- for
 # gradients that cancel to ~0 (a row that sees one key, a window of 1) -- if
-# its error is within FLOOR of the scale of the terms it sums
-# (oracle.backward_magnitudes): the rounding floor of the computation.
+# its error is within FLOOR of the largest magnitude of the terms it sums
+# (oracle.backward_magnitudes): the rounding floor of the computation (for
+# fp32, 1e-6 is ~17 ulps of the largest term).  C4's fp32 dQ passes by the
+# floor: its document rows that see a few keys cancel terms of ~10^3-10^4 to
+# results of ~10^-5, each row's error within ~2 ulps of its own terms.
 FLOOR = {torch.float32: 1e-6, torch.bfloat16: 1e-4, torch.float16: 1e-4}
 
 
