@@ -622,11 +622,13 @@ hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
 }
 
 // Purified-Born forward with document ids (bf16, D = 64; WIN: with a causal
-// sliding window).
+// sliding window), 128-row blocks as the Born launch (p4b 220 -> 227,
+// pwc4b 155 -> 166 TFLOP/s for the step on one box, 4 VGPRs spilled).
 template <bool WIN = false>
 hipError_t launch_purified_fwd_doc(const PurArgs& a, hipStream_t st) {
-    const dim3 grid((unsigned)((a.T + 255) / 256) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true, WIN>), grid, dim3(256), 0, st, a);
+    constexpr int NW = 2, BM = 64 * NW;
+    const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true, WIN, NW>), grid, dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 
