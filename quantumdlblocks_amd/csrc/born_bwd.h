@@ -1136,7 +1136,7 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
                                 : launch_bwd16_dkdv_fast<E, 64, kDense, true>(a, st);
             }
             if (e != hipSuccess) return e;
-            const int nwg = ((a.T + 255) / 256) * a.B * a.H;
+            const int nwg = bwd16_dq_fast_groups(a.B, a.H, a.T, true);
             hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),
                                0, st, a, nwg);
             return hipGetLastError();

@@ -83,13 +83,13 @@ __device__ __forceinline__ void doc_rows_range(const int32_t* __restrict__ docb,
     }
 }
 
-// Screens candidate tiles c0 .. c0+nc-1 (nc <= 256; tile t holds rows
+// Screens candidate tiles c0 .. c0+nc-1 (nc <= block size; tile t holds rows
 // row0 + TS t .. row0 + TS t + TS - 1, clipped to T) of one batch row's ids:
 // a tile is kept when its [min, max] id range meets [lo, hi] (exact for
 // sorted ids, a superset for any others, whose tiles keep the per-element
 // test).  Writes the kept tiles in ascending order to list (index | kDocOne
 // when the tile is one document) and that document to ldoc; returns how many.
-// Every thread of the 256-thread block calls it; keep / tdoc are nc-entry
+// Every thread of the block calls it; keep / tdoc are nc-entry
 // scratch arrays, list / ldoc nc entries, count one int, all in LDS.
 template <int TS>
 __device__ int screen_doc_tiles(const int32_t* __restrict__ docb, int T, int row0, int c0, int nc, int lo, int hi,
@@ -131,32 +131,37 @@ __device__ int screen_doc_tiles(const int32_t* __restrict__ docb, int T, int row
 // kernel.
 // PAD (purified only): a head dim D < 64 (a multiple of 8), as in the
 // forward: chunks past D load as zeros and are not stored.
-template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW (documents only): 2 waves over 128-row blocks, four workgroups per CU
+// and a two-stage ring, as the document forward (fewer blocks straddle a
+// document edge); otherwise 4 waves over 256-row blocks.
+template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
     static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
-    constexpr int NW = 4, NQB = 2, BN = 64, NST = 3, BM = NW * 32 * NQB;
+    static_assert(NW == 4 || (NW == 2 && DOC), "128-row blocks: the document variant");
+    constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
-    constexpr int CAP = 256;               // documents: candidate tiles screened per pass
-    // Loads per wave per tile: K, V (and a 16-key slice of the key document ids).
+    constexpr int CAP = 64 * NW;           // documents: candidate tiles screened per pass
+    constexpr int KDW = BN / NW;           // documents: key ids loaded per wave per tile
+    // Loads per wave per tile: K, V (and a slice of the key document ids).
     constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB, "tile split / staging fits the ring");
-    static_assert(BM == 4 * BN, "four 64-row slices per block");
+    static_assert(BM == NW * BN, "NW 64-row slices per block");
     // kWindow: causal, row i sees keys i - window + 1 .. i (flash_born.py:394,
     // 415-416): the block visits the key tiles from its window's first key on.
     constexpr bool kWin = (MODE == kWindow);
     constexpr bool kCaus = (MODE == kCausal) || kWin;
 
     // One buffer: the K/V ring during the tile loop, the output staging
-    // (256 rows x 128 bytes) once the loop is done.
+    // (BM rows x 128 bytes) once the loop is done.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
     // Documents: key document ids per stage, the kept-tile list and screening scratch.
     __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
@@ -179,8 +184,9 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, g = lane >> 5;
-    // Rows: column c of block qb -> row R + 128 qb + 64 (c / 16) + 16 wave + c % 16.
-    const int lrow = 64 * (c >> 4) + 16 * wave + (c & 15);
+    // Rows: column c of block qb -> row R + (BM/2) qb + (BM/4) (c / 16) +
+    // 16 wave + c % 16.
+    const int lrow = (BM / 4) * (c >> 4) + 16 * wave + (c & 15);
 
     // Head dim in HBM: DP, or (PAD) D < DP with CG 16-byte chunks per row.
     const int D = PAD ? p.D : DP;
@@ -226,12 +232,12 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             Og = reinterpret_cast<const uint16_t*>(p.o) + base;
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
-            qrow[qb] = R + 128 * qb + lrow;
+            qrow[qb] = R + (BM / 2) * qb + lrow;
             const int qi = qrow[qb];
             const bool ok = qi < T;
             if constexpr (DOC) {
                 qdoc[qb] = ok ? docb[qi] : INT_MIN;
-                if (g == 0) r_doc[128 * qb + lrow] = qdoc[qb];
+                if (g == 0) r_doc[(BM / 2) * qb + lrow] = qdoc[qb];
             }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -319,8 +325,8 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 
     // Tile u (documents: kept tile u of the list) -> stage u % NST:
     // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane,
-    // slot = row * CPR + chunk'; documents: also this wave's 16 key document
-    // ids (lanes 0-3, 16 bytes each).
+    // slot = row * CPR + chunk'; documents: also this wave's KDW key document
+    // ids (lanes 0 .. KDW/4 - 1, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
         int key0 = (tb + u) * BN;
@@ -337,7 +343,8 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
         if constexpr (DOC)
-            if (lane < 4) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 16), (key0 + wave * 16 + lane * 4) * 4);
+            if (lane < KDW / 4)
+                dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
 
     // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, dP^T);
@@ -416,7 +423,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 // Documents: the row's id (read only where the tile is tested).
                 int rd = 0;
                 if constexpr (DOC)
-                    if (dm[qb]) rd = r_doc[128 * qb + 64 * (c >> 4) + 16 * wave + (c & 15)];
+                    if (dm[qb]) rd = r_doc[(BM / 2) * qb + (BM / 4) * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float w[2];
@@ -452,7 +459,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 if (dm[qb]) {
                     const int lim = kCaus ? qrow[qb] - kbase : INT_MAX;
                     const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
-                    const int rd = r_doc[128 * qb + 64 * (c >> 4) + 16 * wave + (c & 15)];
+                    const int rd = r_doc[(BM / 2) * qb + (BM / 4) * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
@@ -556,15 +563,17 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
             const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
+            // Tiles 0 .. NST-2 up front, tile u+NST-1 after the barrier of
+            // step u (into the stage of tile u-1).
             if (n > 0) issue(0);
-            if (n > 1) issue(1);
+            if (NST == 3 && n > 1) issue(1);
             for (int u = 0; u < n; ++u) {
-                if (u + 1 < n)
+                if (NST == 3 && u + 1 < n)
                     wait_vmcnt<kTileLoads>();
                 else
                     wait_vmcnt<0>();
                 __syncthreads();
-                if (u + 2 < n) issue(u + 2);
+                if (u + NST - 1 < n) issue(u + NST - 1);
                 int soff = (u % NST) * TB;
                 asm volatile("" : "+s"(soff));
                 const uint8_t* kb = k_lds + soff;
@@ -575,11 +584,12 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 const int ti = e & ~kDocOne;
                 const bool one = (e & kDocOne) != 0;
                 // A column block is tested per element on the causal diagonal
-                // (as in the plain loop below; window: block 1 on every
+                // (block 1 from tile t0 + BM/128 on; window: block 1 on every
                 // diagonal tile, both on the tiles before te) and unless the
                 // tile's keys and all of its rows are one and the same
                 // document.
-                const bool mk[NQB] = {ti >= t0 || (kWin && ti < te), ti >= t0 + 2 || (kWin && (ti < te || ti >= t0))};
+                const bool mk[NQB] = {ti >= t0 || (kWin && ti < te),
+                                      ti >= t0 + BM / 128 || (kWin && (ti < te || ti >= t0))};
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) dm[qb] = mk[qb] || !(one && qone[qb] && td == qsd[qb]);
                 tile(kb, vb, (tb + ti) * BN, mk, NoSkip{});
@@ -643,10 +653,10 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const float f = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
     int ln = lane;
     asm volatile("" : "+v"(ln));
-    const int lr = 64 * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
+    const int lr = (BM / 4) * ((ln & 31) >> 4) + 16 * wave + (ln & 15);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-        const int row = 128 * qb + lr;
+        const int row = (BM / 2) * qb + lr;
         uint8_t* rb = smem + row * RB;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -663,7 +673,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const int chunk = ln & 7;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int row = 64 * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
+        const int row = (BM / 4) * (i >> 1) + 16 * wave + 8 * (i & 1) + (ln >> 3);
         const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 7)) << 4));
         const int q = R + row;
         if (q < T && (!PAD || chunk < CG))
@@ -705,11 +715,18 @@ __global__ __launch_bounds__(256) void born_bwd_dscale_groups_kernel(BwdArgs p, 
     }
 }
 
+// Workgroups of the D = 64 dQ launch (each writes one dscale partial):
+// 256-row blocks, 128-row blocks with documents.
+inline int bwd16_dq_fast_groups(int B, int H, int T, bool doc) {
+    const int BM = doc ? 128 : 256;
+    return ((T + BM - 1) / BM) * B * H;
+}
+
 template <class E, int DP, int MODE, bool DOC = false>
 hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
-    constexpr int BM = 256;
-    const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, DP, MODE, false, DOC>), grid, dim3(256), 0, st, a);
+    constexpr int NW = DOC ? 2 : 4;
+    const dim3 grid((unsigned)bwd16_dq_fast_groups(a.B, a.H, a.T, DOC));
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, DP, MODE, false, DOC, false, NW>), grid, dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 

@@ -54,13 +54,14 @@ namespace qdl {
 //   delta_z = dO . O / Z      (B*H*T fp32)
 //   zinv    = 1 / Z           (B*H*T fp32)
 //   dscale partial sums       (fp64: H * DSCALE_CHUNKS, or one per workgroup of
-//                              the D = 64 dQ kernel, whichever is more)
+//                              the D = 64 dQ kernel -- 128-row blocks with
+//                              documents -- whichever is more)
 inline int64_t bwd_region_bytes(int64_t B, int64_t H, int64_t T) {
     return ((B * H * T * 4) + 255) / 256 * 256;
 }
 inline int64_t bwd_partial_bytes(int64_t B, int64_t H, int64_t T) {
     const int64_t chunks = (H > 1 ? H : 1) * DSCALE_CHUNKS;
-    const int64_t groups = B * H * ((T + 255) / 256);
+    const int64_t groups = B * H * ((T + 127) / 128);
     const int64_t n = (chunks > groups ? chunks : groups) * 8;
     return (n + 255) / 256 * 256;
 }

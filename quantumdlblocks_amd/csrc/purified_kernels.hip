@@ -86,9 +86,10 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
 // partials), then the fixed-order reduction.
 template <int MODE, bool DOC = false, bool PAD = false>
 static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
-    const unsigned BH = (unsigned)(a.B * a.H);
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC, PAD>),
-                       dim3((unsigned)((a.T + 255) / 256) * BH), dim3(256), 0, s, a);
+    // dQ: 256-row blocks of 4 waves, 128-row blocks of 2 with documents.
+    constexpr int NW = DOC ? 2 : 4;
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC, PAD, NW>),
+                       dim3((unsigned)bwd16_dq_fast_groups(a.B, a.H, a.T, DOC)), dim3(64 * NW), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 64);
