@@ -1108,12 +1108,17 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     // (born_bwd_fast.h).
     const bool addr32 = ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
     const bool fast = DP == 64 && a.D == 64 && MODE != kGeneral && addr32;
-    // Causal sliding window without documents: the two fast kernels' window
-    // mode.
+    // Sliding window without documents: the two fast kernels' window modes
+    // (kWindow causal, kWindowNC not).
     if constexpr (DP == 64 && MODE == kGeneral) {
-        if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32) {
-            if ((e = launch_bwd16_dq_fast<E, 64, kWindow>(a, st)) != hipSuccess) return e;
-            if ((e = launch_bwd16_dkdv_fast<E, 64, kWindow>(a, st)) != hipSuccess) return e;
+        if (a.D == 64 && a.doc == nullptr && a.window > 0 && addr32) {
+            if (a.is_causal) {
+                if ((e = launch_bwd16_dq_fast<E, 64, kWindow>(a, st)) != hipSuccess) return e;
+                if ((e = launch_bwd16_dkdv_fast<E, 64, kWindow>(a, st)) != hipSuccess) return e;
+            } else {
+                if ((e = launch_bwd16_dq_fast<E, 64, kWindowNC>(a, st)) != hipSuccess) return e;
+                if ((e = launch_bwd16_dkdv_fast<E, 64, kWindowNC>(a, st)) != hipSuccess) return e;
+            }
             const int nwg = ((a.T + 255) / 256) * a.B * a.H;
             hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256),
                                0, st, a, nwg);

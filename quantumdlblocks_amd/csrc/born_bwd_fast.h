@@ -140,7 +140,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(NW == 4 || (NW == 2 && DOC), "128-row blocks: the document variant");
     constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = NW * 32 * NQB;
     constexpr int KS = DP / 16;
@@ -155,10 +155,11 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB, "tile split / staging fits the ring");
     static_assert(BM == NW * BN, "NW 64-row slices per block");
-    // kWindow: causal, row i sees keys i - window + 1 .. i (flash_born.py:394,
+    // kWindow: causal, row i sees keys i - window + 1 .. i (kWindowNC: up to
+    // T - 1) (flash_born.py:394,
     // 415-416): the block visits the key tiles from its window's first key on.
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     // One buffer: the K/V ring during the tile loop, the output staging
     // (BM rows x 128 bytes) once the loop is done.
@@ -443,7 +444,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                                            kdp[nb * 32 + 4 * g + off] != rd))
                                 dr_ = 0.f;
                         } else {
-                            if (mk[qb] && (off > lim || (kWin && off < lim - W + 1))) dr_ = 0.f;
+                            if (mk[qb] && ((kCaus && off > lim) || (kWin && off < lim - W + 1))) dr_ = 0.f;
                         }
                         w[e] = dr_;
                     }
@@ -458,7 +459,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 // the lane's row (causal) or in another document.
                 if (dm[qb]) {
                     const int lim = kCaus ? qrow[qb] - kbase : INT_MAX;
-                    const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
+                    const int wlo = kWin ? qrow[qb] - kbase - W + 1 : 0;  // window: first visible key
                     const int rd = r_doc[(BM / 2) * qb + (BM / 4) * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -476,7 +477,7 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int off = 8 * (r >> 2) + (r & 3);
-                    if (off > lim || (kWin && off < wlo)) s[qb][r] = 0.f;
+                    if ((kCaus && off > lim) || (kWin && off < wlo)) s[qb][r] = 0.f;
                 }
             }
 #pragma unroll
@@ -756,13 +757,13 @@ hipError_t launch_bwd16_dq_fast(const BwdArgs& a, hipStream_t st) {
 // relu(-gamma tau) when tau < 0); queries past T have 1/Z = 0 from the
 // workspace read, so they add nothing.
 template <class E, int DP, int MODE, bool PUR = false, bool DOC = false, bool PAD = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && (DOC || MODE == kWindow)) ? 2 : 3,
-                                                                     (PUR && (DOC || MODE == kWindow)) ? 2 : 3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && (DOC || mode_window(MODE))) ? 2 : 3,
+                                                                     (PUR && (DOC || mode_window(MODE))) ? 2 : 3)))
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DB = DP / 32;
@@ -777,10 +778,11 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     // leave room for 128-entry lists).
     constexpr int CAP = 128;
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && 2 * BK * RB <= NST * SB, "tile split / staging");
-    // kWindow: causal, key j is seen by queries j .. j + window - 1: the
-    // block visits the query tiles up to its last key's window.
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    // kWindow: causal, key j is seen by queries j .. j + window - 1 (kWindowNC:
+    // queries 0 .. j + window - 1): the block visits the query tiles up to
+    // its last key's window.
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
     __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
@@ -790,8 +792,9 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const int BH = p.B * p.H;
     const int bid = blockIdx.x;
     const int bh = bid % BH;
-    // Key blocks in ascending order: under causality the first sees the most queries.
-    const int kblk = bid / BH;
+    // Key blocks in ascending order: under causality the first sees the most
+    // queries; kWindowNC: descending, the last sees the most.
+    const int kblk = MODE == kWindowNC ? (T + BK - 1) / BK - 1 - bid / BH : bid / BH;
     const int h = bh % p.H;
     const int K0 = kblk * BK;
 
@@ -963,7 +966,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                                        qd[nb * 32 + 4 * g + off] != kdoc))
                                 u = bb = 0.f;
                         } else {
-                            if (mk && (off + lim < 0 || (kWin && off + lim >= W))) u = bb = 0.f;
+                            if (mk && ((kCaus && off + lim < 0) || (kWin && off + lim >= W))) u = bb = 0.f;
                         }
                         const float u2_ = u * u;
                         const float dpz = dp[r] * z4[k + e];
@@ -983,6 +986,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             // the lane's key (causal) or in another document.
             if (xm) {
                 const int lim = kCaus ? qbase - key : INT_MAX / 2;
+                const int wl = qbase - key;  // window: query - key >= W is masked
                 const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -990,7 +994,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + wl >= W) || dq[k] != kdoc)
                             s[4 * i + k] = 0.f;
                 }
             }
@@ -1001,7 +1005,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if (off + lim < 0 || (kWin && off + lim >= W)) s[r] = 0.f;
+                if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) s[r] = 0.f;
             }
         }
 #pragma unroll

@@ -230,8 +230,14 @@ enum MaskMode : int {
     kDense = 0,    // non-causal, no window, no documents
     kCausal = 1,   // causal only
     kGeneral = 2,  // runtime causal flag + window + document ids
-    kWindow = 3,   // causal with a sliding window (the D = 64 fast kernels only)
+    kWindow = 3,   // causal with a sliding window (the tuned kernels)
+    kWindowNC = 4, // sliding window without causality (the D = 64 fast kernels)
 };
+
+// Row i sees keys j with i - j < window (flash_born.py:173-174), and j <= i
+// under causality: kWindowNC keeps every key after the row as well.
+constexpr bool mode_window(int m) { return m == kWindow || m == kWindowNC; }
+constexpr bool mode_causal(int m) { return m == kCausal || m == kWindow; }
 
 // Document ids: the span of candidate tiles a block has to visit.  The
 // block's stationary rows r0 .. r1-1 hold ids in [dlo, dhi]; candidate tile t

@@ -21,6 +21,9 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
     // Causal sliding window (no documents): the fast kernel's window mode.
     if (a.D == 64 && a.doc == nullptr && a.window > 0 && a.is_causal && addr32)
         return launch_fwd16_fast<F16, 64, kWindow>(a, s);
+    // Sliding window without causality (no documents): its kWindowNC mode.
+    if (a.D == 64 && a.doc == nullptr && a.window > 0 && !a.is_causal && addr32)
+        return launch_fwd16_fast<F16, 64, kWindowNC>(a, s);
     // D == 128 with document ids (and a causal window): the D == 128 kernel's
     // document mode.
     if (a.D == 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {

@@ -137,10 +137,10 @@ template <class E, int DP, int MODE, bool PUR = false, bool PRO = false, bool PA
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_fast_kernel(
     typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "no document masks here");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "no document masks here");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
     static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
-    static_assert(MODE != kWindow || !PRO, "sliding windows: no fused prologue");
+    static_assert(!mode_window(MODE) || !PRO, "sliding windows: no fused prologue");
     static_assert(!PAD || PUR, "narrow head dims: purified");
     using C = FastFwdCfg<DP>;
     constexpr int NW = C::NW, NQB = C::NQB, BN = C::BN, NST = C::NST, BM = C::BM;
@@ -156,11 +156,11 @@ void born_fwd16_fast_kernel(
     static_assert(TB % (1024 * NW) == 0 && QB % (1024 * NW) == 0, "tile split");
     static_assert(NST == 3, "vmcnt bookkeeping below assumes a three-stage ring");
     // kWindow: causal, and row i sees keys i - window + 1 .. i
-    // (flash_born.py:152, 173-174).  Launched unpaired (one block per
-    // workgroup: blocks carry about equal work); each block visits the key
-    // tiles from its window's first key on.
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    // (flash_born.py:152, 173-174); kWindowNC: not causal, row i sees keys
+    // i - window + 1 .. T - 1.  Launched unpaired (one block per workgroup);
+    // each block visits the key tiles from its window's first key on.
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     // The DMA loads are issued as inline asm, so the compiler never waits on
     // them; their completion is tracked by the pipeline's own vmcnt waits and
@@ -187,7 +187,8 @@ void born_fwd16_fast_kernel(
     const int bh = item % BH;
     const int pr = item / BH;
     const int h = bh % p.H;
-    const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
+    // kWindowNC: the first blocks see the most keys, so they go first.
+    const int mb_a = MODE == kWindowNC ? pr : nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
     const int W = kWin ? p.window : 0;
     // First key tile of a block (its window's first key), and its tile count.
@@ -316,7 +317,7 @@ void born_fwd16_fast_kernel(
             for (int qb = 0; qb < NQB; ++qb) {
                 if (M[qb] == kSkip) continue;
                 const int lim = mlim[qb] - kbase;
-                const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
+                const int wlo = kWin ? qrow[qb] - kbase - W + 1 : 0;  // window: first visible key
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float w[2];
@@ -348,13 +349,13 @@ void born_fwd16_fast_kernel(
             if (M[qb] == kSkip) continue;
             if (M[qb] == kMasked) {
                 // Key kbase + 8 (r / 4) + r % 4 of register r: masked past the
-                // lane's row, and (window) before the row's first key.
+                // lane's row (causal), and (window) before the row's first key.
                 const int lim = qrow[qb] - kbase;
                 const int wlo = kWin ? lim - W + 1 : 0;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int off = 8 * (r >> 2) + (r & 3);
-                    if (off > lim || (kWin && off < wlo)) s[qb][r] = 0.f;
+                    if ((kCaus && off > lim) || (kWin && off < wlo)) s[qb][r] = 0.f;
                 }
             }
 #pragma unroll
@@ -882,13 +883,15 @@ void born_fwd16_fast_kernel(
                 }
             }
         } else if constexpr (PUR) {
+            // Not causal: the last tile holds the keys past T (tile counted
+            // from tb, the window's first key tile).
             for (; t < nt; ++t, ++u) {
                 if (!at_top) top(u);
                 at_top = false;
                 const uint8_t *kb, *vb;
                 stage(u, kb, vb);
                 read_k(kop, kb, 0);
-                tile(kb, vb, t * BN, Masked{}, Masked{});
+                tile(kb, vb, (tb + t) * BN, Masked{}, Masked{});
             }
         }
     }

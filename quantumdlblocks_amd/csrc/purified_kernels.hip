@@ -14,17 +14,18 @@ inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <
 // The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
 // offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
 // kernels, as the Born dispatch does.
-// D = 64 (and below) also takes a causal sliding window (the wavelet models'
+// Sliding windows: D <= 64 without documents takes any window (kWindow causal,
+// kWindowNC not); D = 128 and documents a causal one (the wavelet models'
 // purified layers run causal with a window and document ids).
 inline bool purified_window_ok(const PurArgs& a) { return a.window == 0 || a.is_causal; }
 
 inline bool purified_fast_ok(const PurArgs& a) {
-    return a.D == 64 && purified_window_ok(a) && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D == 64 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 // D < 64 (a multiple of 8) on the D = 64 kernels with the columns past D zero.
 inline bool purified_narrow_ok(const PurArgs& a) {
-    return a.D < 64 && purified_window_ok(a) && a.doc == nullptr && ((int64_t)a.T + 256) * 64 * 2 < ((int64_t)1 << 31);
+    return a.D < 64 && a.doc == nullptr && ((int64_t)a.T + 256) * 64 * 2 < ((int64_t)1 << 31);
 }
 
 // D == 128, and 64 < D < 128 with the columns past D zero.
@@ -47,11 +48,14 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // bf16, D = 64 (and below, zero columns), dense, causal or causal
     // window: the bf16-MFMA kernel with split weights.
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
-        if (a.window > 0) return launch_purified_fwd_fast<kWindow>(a, s);
+        if (a.window > 0)
+            return a.is_causal ? launch_purified_fwd_fast<kWindow>(a, s) : launch_purified_fwd_fast<kWindowNC>(a, s);
         return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
     }
     if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
-        if (a.window > 0) return launch_purified_fwd_fast<kWindow, true>(a, s);
+        if (a.window > 0)
+            return a.is_causal ? launch_purified_fwd_fast<kWindow, true>(a, s)
+                               : launch_purified_fwd_fast<kWindowNC, true>(a, s);
         return a.is_causal ? launch_purified_fwd_fast<kCausal, true>(a, s) : launch_purified_fwd_fast<kDense, true>(a, s);
     }
     // bf16, 64 < D <= 128, dense, causal or causal window: the D = 128
@@ -118,11 +122,13 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
-        if (a.window > 0) return purified_bwd_fast<kWindow>(a, s);
+        if (a.window > 0) return a.is_causal ? purified_bwd_fast<kWindow>(a, s) : purified_bwd_fast<kWindowNC>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
     }
     if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
-        if (a.window > 0) return purified_bwd_fast<kWindow, false, true>(a, s);
+        if (a.window > 0)
+            return a.is_causal ? purified_bwd_fast<kWindow, false, true>(a, s)
+                               : purified_bwd_fast<kWindowNC, false, true>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
     }
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {

@@ -192,6 +192,18 @@ def test_bwd_sliding_window_fast_kernels(cuda_device, dtype, window):
                check_dscale=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 63, 64, 65, 127, 128, 129, 255, 256, 300, 700, 2000])
+def test_bwd_sliding_window_noncausal_fast_kernels(cuda_device, dtype, window):
+    """Windows without causality at D = 64 run the fast dQ and dK/dV
+    kernels' kWindowNC mode (key j is seen by queries 0 .. j + W - 1; the
+    dK/dV launch takes the last key blocks first): windows on and beside the
+    64-row tile, 128-key and 256-row block edges, longer than T, a partial
+    last block; per-head scales and dscale."""
+    _check_bwd(2, 2, 1100, 64, dtype, cuda_device, is_causal=False, window_size=window, seed=window + 5,
+               scale=[8.0, -0.7], check_dscale=True)
+
+
 @pytest.mark.parametrize("T", [1, 37, 64, 200, 256, 300, 513, 1100])
 @pytest.mark.parametrize("is_causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -216,6 +216,17 @@ def test_fwd_sliding_window_fast_kernel(cuda_device, dtype, window):
     _check_fwd(2, 2, 1100, 64, dtype, cuda_device, window_size=window, seed=window + 7)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 63, 64, 65, 100, 255, 256, 257, 320, 512, 900, 2000])
+def test_fwd_sliding_window_noncausal_fast_kernel(cuda_device, dtype, window):
+    """Windows without causality at D = 64 (row i sees keys i - W + 1 ..
+    T - 1, flash_born.py:173-174) run the fast kernel's kWindowNC mode: one
+    block per workgroup, the first blocks first; windows starting inside, on
+    and beside the 64-key tile and 256-row block edges, longer than T, a
+    partial last tile and block."""
+    _check_fwd(2, 2, 1100, 64, dtype, cuda_device, is_causal=False, window_size=window, seed=window + 9)
+
+
 @pytest.mark.parametrize("T", [1, 37, 64, 255, 256, 300, 513, 777, 1100])
 @pytest.mark.parametrize("is_causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

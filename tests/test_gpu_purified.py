@@ -370,6 +370,41 @@ def test_purified_window_fast(cuda_device, D, window, docs):
         assert ok.all(), (name, got, want, m)
 
 
+@pytest.mark.parametrize("D", [64, 32])
+@pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
+def test_purified_window_noncausal_fast(cuda_device, D, window):
+    """bf16 purified attention with a sliding window and no causality: the
+    D = 64 kernels' kWindowNC mode (D = 32 with zero columns); tau < 0 (a
+    masked pair with a zero overlap still weighs relu(-gamma tau)^4, so the
+    window's edge and the keys past T are zeroed per weight), per-head gamma
+    and tau, T not a multiple of the tile.  Forward (fp32 output) against the
+    oracle to 1e-4; gradients, dgamma and dtau to the bf16 bars."""
+    B, H, T = 2, 2, 700
+    print(f"purified non-causal window D{D} W{window}", flush=True)
+    q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=window + D + 3, std=0.25, n=4,
+                                                              dtype=torch.bfloat16))
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    o32, z32 = _pur_fwd_abi(q, k, v, scale, tau, 0.05, False, 1e-8, window=window)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, False,
+                                        1e-8, window)
+    assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
+    assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
+    sc = torch.tensor(np.asarray(scale, dtype=np.float32), device=cuda_device)
+    ta = torch.tensor(np.asarray(tau, dtype=np.float32), device=cuda_device)
+    fast = _run(q, k, v, do, sc, ta, eps_base=0.05, is_causal=False, eps=1e-8, window_size=window)
+    okw = dict(eps_base=0.05, is_causal=False, eps=1e-8, window_size=window)
+    ref = orc.purified_backward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do), **okw)
+    mag = orc.purified_backward_magnitudes(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), f64(do),
+                                           **okw)
+    for i, name in enumerate(("dq", "dk", "dv")):
+        got, want, m = f64(fast[1 + i]), ref[i], mag[i]
+        assert rel_err(got, want) <= 2e-2 or max_abs(got, want) / m.max() <= 1e-4, (name, rel_err(got, want))
+    for name, got, want, m in (("dscale", fast[4], ref[3], mag[3]), ("dtau", fast[5], ref[4], mag[4])):
+        got = np.atleast_1d(f64(got))
+        ok = (np.abs(got - want) <= 2e-2 * np.abs(want)) | (np.abs(got - want) <= 1e-4 * m)
+        assert ok.all(), (name, got, want, m)
+
+
 def test_purified_d128_window_paired_launch(cuda_device):
     """Head dim 128 with a causal window on a grid of 256 block pairs
     (B4 H16 T2048, window 384: the launch pairs blocks nmb-1-mb and mb);
