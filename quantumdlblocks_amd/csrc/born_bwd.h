@@ -1147,12 +1147,13 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
             return hipGetLastError();
         }
     }
-    // D == 128, dense, causal or causal sliding window (no documents): the
-    // D == 128 kernels (born_bwd_d128.h); 64 < D < 128 on the same kernels
-    // with the columns past D zero.
+    // D == 128, dense, causal or a sliding window with or without causality
+    // (no documents): the D == 128 kernels (born_bwd_d128.h); 64 < D < 128 on
+    // the same kernels with the columns past D zero.
     if constexpr (DP == 128) {
         if (a.D == 128 && a.doc == nullptr && addr32) {
             if (MODE == kGeneral && a.window > 0 && a.is_causal) return launch_bwd16_d128<E, kWindow>(a, st);
+            if (MODE == kGeneral && a.window > 0 && !a.is_causal) return launch_bwd16_d128<E, kWindowNC>(a, st);
             if (MODE == kDense || MODE == kCausal) return launch_bwd16_d128<E, MODE == kCausal ? kCausal : kDense>(a, st);
         }
     }
@@ -1168,6 +1169,7 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     if constexpr (DP == 96 || DP == 128) {
         if (a.D > 64 && a.D < 128 && a.doc == nullptr && addr32) {
             if (MODE == kGeneral && a.window > 0 && a.is_causal) return launch_bwd16_d128<E, kWindow, true>(a, st);
+            if (MODE == kGeneral && a.window > 0 && !a.is_causal) return launch_bwd16_d128<E, kWindowNC, true>(a, st);
             if (MODE == kDense || MODE == kCausal)
                 return launch_bwd16_d128<E, MODE == kCausal ? kCausal : kDense, true>(a, st);
         }

@@ -50,7 +50,8 @@ struct BwdD128Cfg {
 template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
 
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
@@ -63,8 +64,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // Loads per wave per tile: K, V (documents: and 8 of the key document ids).
     constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB && BM == 32 * NW, "tile split / staging");
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     // The K/V ring during the tile loop, the output staging afterwards.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
@@ -311,7 +312,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     float d = f * fmaf(t[r], zinv, nd);
                     if constexpr (decltype(m)::value == kMasked) {
                         const int off = 8 * (r >> 2) + (r & 3);
-                        if (off > lim || (kWin && off < wlo)) d = 0.f;
+                        if ((kCaus && off > lim) || (kWin && off < wlo)) d = 0.f;
                     }
                     if constexpr (decltype(m)::value == kDocm)
                         if ((dmask >> r) & 1u) d = 0.f;
@@ -328,7 +329,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
+                if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
             }
         }
         if constexpr (decltype(m)::value == kDocm) {
@@ -503,7 +504,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
 
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
@@ -517,8 +519,8 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     constexpr int CAP = 256;               // documents: candidate tiles screened per pass
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && BK * RB <= NST * SB && BK == 32 * NW,
                   "tile split / staging");
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
     __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
@@ -528,8 +530,9 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const int BH = p.B * p.H;
     const int bid = blockIdx.x;
     const int bh = bid % BH;
-    // Key blocks in ascending order: under causality the first sees the most queries.
-    const int kblk = bid / BH;
+    // Key blocks in ascending order: under causality the first sees the most
+    // queries; kWindowNC: descending, the last sees the most.
+    const int kblk = MODE == kWindowNC ? (T + BK - 1) / BK - 1 - bid / BH : bid / BH;
     const int h = bh % p.H;
     const int K0 = kblk * BK;
 
@@ -762,7 +765,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         float bb = __int_as_float(max(__float_as_int(x), 0));
                         if constexpr (decltype(m)::value == kMasked) {
                             const int off = 8 * (r >> 2) + (r & 3);
-                            if (off + lim < 0 || (kWin && off + lim >= W)) u = bb = 0.f;
+                            if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) u = bb = 0.f;
                         }
                         if constexpr (decltype(m)::value == kDocm)
                             if ((dmask >> r) & 1u) u = bb = 0.f;
@@ -802,7 +805,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if (off + lim < 0 || (kWin && off + lim >= W)) s[r] = 0.f;
+                if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) s[r] = 0.f;
             }
         }
 #pragma unroll

@@ -30,9 +30,11 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
         if (a.window > 0) return launch_fwd16_d128_doc<BF16, kWindow>(a, s);
         return a.is_causal ? launch_fwd16_d128_doc<BF16, kCausal>(a, s) : launch_fwd16_d128_doc<BF16, kDense>(a, s);
     }
-    // D == 128: dense, causal or causal sliding window (no documents).
-    if (a.D == 128 && a.doc == nullptr && addr32 && (a.window == 0 || a.is_causal)) {
-        if (a.window > 0) return launch_fwd16_d128<BF16, kWindow>(a, s);
+    // D == 128: dense, causal or a sliding window with or without causality
+    // (no documents).
+    if (a.D == 128 && a.doc == nullptr && addr32) {
+        if (a.window > 0)
+            return a.is_causal ? launch_fwd16_d128<BF16, kWindow>(a, s) : launch_fwd16_d128<BF16, kWindowNC>(a, s);
         return a.is_causal ? launch_fwd16_d128<BF16, kCausal>(a, s) : launch_fwd16_d128<BF16, kDense>(a, s);
     }
     if (a.D == 64 && mode != kGeneral && addr32)

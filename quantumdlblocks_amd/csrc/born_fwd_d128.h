@@ -73,7 +73,8 @@ struct FwdD128Cfg {
 template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
-    static_assert(MODE == kDense || MODE == kCausal || MODE == kWindow, "mask modes");
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
     static_assert(!DOC || !PAD, "documents: D == 128");
     using C = FwdD128Cfg;
@@ -88,8 +89,10 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     constexpr int LQW = QB / (1024 * NW);  // 1-KiB loads per wave per Q block
     static_assert(TB % (1024 * NW) == 0 && QB % (1024 * NW) == 0, "tile split");
     static_assert(LQW * 1024 == 32 * RB, "each wave's Q loads land on its own 32 rows");
-    constexpr bool kWin = (MODE == kWindow);
-    constexpr bool kCaus = (MODE == kCausal) || kWin;
+    // kWindow: causal with a window; kWindowNC: a window without causality
+    // (row i sees keys i - W + 1 .. T - 1).
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
 
     __shared__ __attribute__((aligned(1024))) uint8_t k_lds[NST * TB];
     __shared__ __attribute__((aligned(1024))) uint8_t v_lds[NST * TB];
@@ -106,12 +109,12 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const int bid = blockIdx.x;
     // Paired launch: item 0 is query block nmb-1-pr, item 1 block pr when
     // that is a different block.  Unpaired: one block per workgroup, the
-    // longest key ranges first.
+    // longest key ranges first (kWindowNC: the first blocks).
     const bool paired = gridDim.x < (unsigned)(nmb * BH);
     const int bh = bid % BH;
     const int pr = bid / BH;
     const int h = bh % p.H;
-    const int mb_a = nmb - 1 - pr, mb_b = paired ? pr : mb_a;
+    const int mb_a = (MODE == kWindowNC && !paired) ? pr : nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
     const int W = kWin ? p.window : 0;
     // First key tile of a block (its first row's window start) and its tile count.
@@ -237,7 +240,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             // the row's window, and (documents) in another document: bit r of
             // dmask for register r.
             const int lim = (kCaus ? qrow : T - 1) - kbase;
-            const int wlo = kWin ? lim - W + 1 : 0;
+            const int wlo = kWin ? qrow - kbase - W + 1 : 0;
             uint32_t dmask = 0;
             if constexpr (decltype(m)::value == kDocm) {
                 if (dmw) {
@@ -285,7 +288,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if (off > lim || (kWin && off < wlo)) s[r] = 0.f;
+                if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
             }
         }
         if constexpr (decltype(m)::value == kDocm) {
@@ -748,7 +751,7 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
-    const bool pair = MODE != kWindow && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
+    const bool pair = !mode_window(MODE) && d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
     const dim3 grid(pair ? npair : nsingle);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
@@ -777,8 +780,8 @@ hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     constexpr unsigned kCUs = 256;
-    const bool pair = MODE == kWindow ? 2 * ((npair + kCUs - 1) / kCUs) <= (nsingle + kCUs - 1) / kCUs
-                                      : d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
+    const bool pair = mode_window(MODE) ? 2 * ((npair + kCUs - 1) / kCUs) <= (nsingle + kCUs - 1) / kCUs
+                                        : d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
     const dim3 grid(pair ? npair : nsingle);
     hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();

@@ -188,7 +188,7 @@ void born_fwd16_fast_kernel(
     const int pr = item / BH;
     const int h = bh % p.H;
     // kWindowNC: the first blocks see the most keys, so they go first.
-    const int mb_a = MODE == kWindowNC ? pr : nmb - 1 - pr, mb_b = paired ? pr : mb_a;
+    const int mb_a = (MODE == kWindowNC && !paired) ? pr : nmb - 1 - pr, mb_b = paired ? pr : mb_a;
     const int nitems = (mb_a != mb_b) ? 2 : 1;
     const int W = kWin ? p.window : 0;
     // First key tile of a block (its window's first key), and its tile count.

@@ -14,9 +14,9 @@ inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <
 // The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
 // offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
 // kernels, as the Born dispatch does.
-// Sliding windows: D <= 64 without documents takes any window (kWindow causal,
-// kWindowNC not); D = 128 and documents a causal one (the wavelet models'
-// purified layers run causal with a window and document ids).
+// Sliding windows: without documents any window (kWindow causal, kWindowNC
+// not); with documents a causal one (the wavelet models' purified layers run
+// causal with a window and document ids).
 inline bool purified_window_ok(const PurArgs& a) { return a.window == 0 || a.is_causal; }
 
 inline bool purified_fast_ok(const PurArgs& a) {
@@ -30,8 +30,7 @@ inline bool purified_narrow_ok(const PurArgs& a) {
 
 // D == 128, and 64 < D < 128 with the columns past D zero.
 inline bool purified_d128_ok(const PurArgs& a) {
-    return a.D > 64 && a.D <= 128 && purified_window_ok(a) && a.doc == nullptr &&
-           ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D > 64 && a.D <= 128 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 // D == 128 with document ids: the D = 128 kernels' document mode.
@@ -62,10 +61,13 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // kernel's purified mode.
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
         if (a.D == 128) {
-            if (a.window > 0) return launch_purified_fwd_d128<kWindow>(a, s);
+            if (a.window > 0)
+                return a.is_causal ? launch_purified_fwd_d128<kWindow>(a, s) : launch_purified_fwd_d128<kWindowNC>(a, s);
             return a.is_causal ? launch_purified_fwd_d128<kCausal>(a, s) : launch_purified_fwd_d128<kDense>(a, s);
         }
-        if (a.window > 0) return launch_purified_fwd_d128<kWindow, true>(a, s);
+        if (a.window > 0)
+            return a.is_causal ? launch_purified_fwd_d128<kWindow, true>(a, s)
+                               : launch_purified_fwd_d128<kWindowNC, true>(a, s);
         return a.is_causal ? launch_purified_fwd_d128<kCausal, true>(a, s) : launch_purified_fwd_d128<kDense, true>(a, s);
     }
     // bf16, D = 128, document ids (with or without a causal window): its
@@ -132,7 +134,7 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
     }
     if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
-        if (a.window > 0) return purified_bwd_d128<kWindow>(a, s);
+        if (a.window > 0) return a.is_causal ? purified_bwd_d128<kWindow>(a, s) : purified_bwd_d128<kWindowNC>(a, s);
         return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
     }
     if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a)) {

@@ -224,6 +224,17 @@ def test_bwd_d128_sliding_window(cuda_device, dtype, window):
                std=0.7, check_dscale=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D, window", [(128, 1), (128, 31), (128, 33), (128, 64), (128, 127), (128, 129),
+                                       (128, 256), (128, 700), (128, 2000), (96, 100), (96, 257)])
+def test_bwd_d128_sliding_window_noncausal(cuda_device, dtype, D, window):
+    """Windows without causality at D = 128 (and D = 96 with the columns
+    past D zero): the D = 128 dQ and dK/dV kernels' kWindowNC mode (dK/dV
+    takes the last key blocks first); per-head scales and dscale."""
+    _check_bwd(2, 2, 1100, D, dtype, cuda_device, is_causal=False, window_size=window, seed=window + 17,
+               scale=[0.09, -0.3], std=0.7, check_dscale=True)
+
+
 @pytest.mark.parametrize("D", [72, 96, 120])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mode", ["causal", "dense", "window"])

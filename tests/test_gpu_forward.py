@@ -261,6 +261,16 @@ def test_fwd_d128_sliding_window(cuda_device, dtype, window):
     _check_fwd(2, 2, 1100, 128, dtype, cuda_device, window_size=window, scale=0.09, seed=window + 11)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("window", [1, 31, 32, 33, 64, 100, 255, 256, 257, 900, 2000])
+def test_fwd_d128_sliding_window_noncausal(cuda_device, dtype, window):
+    """Windows without causality at D = 128: the D = 128 kernel's kWindowNC
+    mode (per-wave runs from the window's first key to T, one block per
+    workgroup, the first blocks first)."""
+    _check_fwd(2, 2, 1100, 128, dtype, cuda_device, is_causal=False, window_size=window, scale=0.09,
+               seed=window + 15)
+
+
 @pytest.mark.parametrize("D", [104, 112, 120])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mode", ["causal", "dense", "window"])

@@ -370,11 +370,12 @@ def test_purified_window_fast(cuda_device, D, window, docs):
         assert ok.all(), (name, got, want, m)
 
 
-@pytest.mark.parametrize("D", [64, 32])
+@pytest.mark.parametrize("D", [64, 32, 128, 96])
 @pytest.mark.parametrize("window", [1, 33, 100, 300, 2000])
 def test_purified_window_noncausal_fast(cuda_device, D, window):
     """bf16 purified attention with a sliding window and no causality: the
-    D = 64 kernels' kWindowNC mode (D = 32 with zero columns); tau < 0 (a
+    D = 64 and D = 128 kernels' kWindowNC mode (D = 32 and 96 with zero
+    columns); tau < 0 (a
     masked pair with a zero overlap still weighs relu(-gamma tau)^4, so the
     window's edge and the keys past T are zeroed per weight), per-head gamma
     and tau, T not a multiple of the tile.  Forward (fp32 output) against the
