@@ -52,7 +52,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
 
     constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
 
     constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
@@ -1068,19 +1068,19 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// The purified D == 128 backward (bf16, dense or causal): dQ (and the
-// workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
-// partials (one per dK/dV workgroup).
-template <int MODE, bool PAD = false, bool DOC = false>
+// The purified D == 128 backward (bf16 or fp16): dQ (and the workspace),
+// dK/dV (and the dgamma / dtau partials); the caller reduces the partials (one
+// per dK/dV workgroup).
+template <int MODE, bool PAD = false, bool DOC = false, class E = BF16>
 hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<BF16, MODE, true, PAD, DOC>), dim3(nq * BH),
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, true, PAD, DOC>), dim3(nq * BH),
                        dim3(BwdD128Cfg::NW * 64), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<BF16, MODE, true, PAD, DOC>), dim3(nk * BH),
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, true, PAD, DOC>), dim3(nk * BH),
                        dim3(BwdD128Cfg::NWK * 64), 0, st, a);
     return hipGetLastError();
 }

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(NW == 4 || (NW == 2 && DOC), "128-row blocks: the document variant");
     constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = NW * 32 * NQB;
@@ -762,7 +762,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((PUR && (DO
 void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PAD || (PUR && !DOC), "narrow head dims: purified");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified gradients: bf16");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     constexpr int NW = 4, BQ = 64, NST = 3, BK = NW * 32;
     constexpr int KS = DP / 16;

@@ -87,19 +87,20 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
         default: return launch_purified_fwd<IN, 256>(a, s);
     }
 }
-// bf16, D = 64, dense or causal: the bf16-MFMA dQ kernel (which also writes
-// -delta and 1/Z) before the dK/dV kernel (which writes the dgamma / dtau
-// partials), then the fixed-order reduction.
-template <int MODE, bool DOC = false, bool PAD = false>
+// 16-bit, D = 64: the 16-bit-MFMA dQ kernel (which also writes -delta and
+// 1/Z) before the dK/dV kernel (which writes the dgamma / dtau partials), then
+// the fixed-order reduction.  E: the input dtype, to which the reference
+// rounds p/Z and dR before their contractions (flash_born.py:926, 939, 1058).
+template <int MODE, bool DOC = false, bool PAD = false, class E = BF16>
 static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     // dQ: 256-row blocks of 4 waves, 128-row blocks of 2 with documents.
     constexpr int NW = DOC ? 2 : 4;
-    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<BF16, 64, MODE, true, DOC, PAD, NW>),
+    hipLaunchKernelGGL((born_bwd16_dq_fast_kernel<E, 64, MODE, true, DOC, PAD, NW>),
                        dim3((unsigned)bwd16_dq_fast_groups(a.B, a.H, a.T, DOC)), dim3(64 * NW), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 64);
-    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<BF16, 64, MODE, true, DOC, PAD>), dim3((unsigned)nwg), dim3(256), 0,
+    hipLaunchKernelGGL((born_bwd16_dkdv_fast_kernel<E, 64, MODE, true, DOC, PAD>), dim3((unsigned)nwg), dim3(256), 0,
                        s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
@@ -107,13 +108,13 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// bf16, 64 < D <= 128, dense, causal or causal window: the D = 128 dQ and
-// dK/dV kernels' purified mode, then the same reduction.
-template <int MODE, bool DOC = false>
+// 16-bit, 64 < D <= 128: the D = 128 dQ and dK/dV kernels' purified mode,
+// then the same reduction.
+template <int MODE, bool DOC = false, class E = BF16>
 static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
-    hipError_t e = DOC           ? launch_purified_bwd_d128<MODE, false, DOC>(a, s)
-                   : a.D == 128 ? launch_purified_bwd_d128<MODE>(a, s)
-                                : launch_purified_bwd_d128<MODE, true>(a, s);
+    hipError_t e = DOC           ? launch_purified_bwd_d128<MODE, false, DOC, E>(a, s)
+                   : a.D == 128 ? launch_purified_bwd_d128<MODE, false, false, E>(a, s)
+                                : launch_purified_bwd_d128<MODE, true, false, E>(a, s);
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 128);
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
@@ -123,29 +124,41 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
 
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
-    if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
-        if (a.window > 0) return a.is_causal ? purified_bwd_fast<kWindow>(a, s) : purified_bwd_fast<kWindowNC>(a, s);
-        return a.is_causal ? purified_bwd_fast<kCausal>(a, s) : purified_bwd_fast<kDense>(a, s);
-    }
-    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
+    // 16-bit inputs: the 16-bit-MFMA backward kernels (bf16 and fp16 alike:
+    // the reference rounds p/Z and dR to the input dtype before its dots);
+    // the forward they follow may be either kind (fp16 forwards run the
+    // fp32-MFMA kernel), as both store O and Z in fp32.
+    using E = typename std::conditional<std::is_same<IN, F16>::value, F16, BF16>::type;
+    constexpr bool k16 = !std::is_same<IN, float>::value;
+    if (k16 && purified_fast_ok(a)) {
         if (a.window > 0)
-            return a.is_causal ? purified_bwd_fast<kWindow, false, true>(a, s)
-                               : purified_bwd_fast<kWindowNC, false, true>(a, s);
-        return a.is_causal ? purified_bwd_fast<kCausal, false, true>(a, s) : purified_bwd_fast<kDense, false, true>(a, s);
+            return a.is_causal ? purified_bwd_fast<kWindow, false, false, E>(a, s)
+                               : purified_bwd_fast<kWindowNC, false, false, E>(a, s);
+        return a.is_causal ? purified_bwd_fast<kCausal, false, false, E>(a, s)
+                           : purified_bwd_fast<kDense, false, false, E>(a, s);
     }
-    if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
-        if (a.window > 0) return a.is_causal ? purified_bwd_d128<kWindow>(a, s) : purified_bwd_d128<kWindowNC>(a, s);
-        return a.is_causal ? purified_bwd_d128<kCausal>(a, s) : purified_bwd_d128<kDense>(a, s);
+    if (k16 && purified_narrow_ok(a)) {
+        if (a.window > 0)
+            return a.is_causal ? purified_bwd_fast<kWindow, false, true, E>(a, s)
+                               : purified_bwd_fast<kWindowNC, false, true, E>(a, s);
+        return a.is_causal ? purified_bwd_fast<kCausal, false, true, E>(a, s)
+                           : purified_bwd_fast<kDense, false, true, E>(a, s);
     }
-    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a)) {
-        if (a.window > 0) return purified_bwd_d128<kWindow, true>(a, s);
-        return a.is_causal ? purified_bwd_d128<kCausal, true>(a, s) : purified_bwd_d128<kDense, true>(a, s);
+    if (k16 && purified_d128_ok(a)) {
+        if (a.window > 0)
+            return a.is_causal ? purified_bwd_d128<kWindow, false, E>(a, s) : purified_bwd_d128<kWindowNC, false, E>(a, s);
+        return a.is_causal ? purified_bwd_d128<kCausal, false, E>(a, s) : purified_bwd_d128<kDense, false, E>(a, s);
     }
-    // bf16, D = 64, document ids (with or without a causal window): the same
+    if (k16 && purified_d128_doc_ok(a)) {
+        if (a.window > 0) return purified_bwd_d128<kWindow, true, E>(a, s);
+        return a.is_causal ? purified_bwd_d128<kCausal, true, E>(a, s) : purified_bwd_d128<kDense, true, E>(a, s);
+    }
+    // D = 64, document ids (with or without a causal window): the same
     // kernels' document variants.
-    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a)) {
-        if (a.window > 0) return purified_bwd_fast<kWindow, true>(a, s);
-        return a.is_causal ? purified_bwd_fast<kCausal, true>(a, s) : purified_bwd_fast<kDense, true>(a, s);
+    if (k16 && purified_doc_fast_ok(a)) {
+        if (a.window > 0) return purified_bwd_fast<kWindow, true, false, E>(a, s);
+        return a.is_causal ? purified_bwd_fast<kCausal, true, false, E>(a, s)
+                           : purified_bwd_fast<kDense, true, false, E>(a, s);
     }
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);

@@ -87,7 +87,33 @@ def test_purified_forward_backward(cuda_device, case):
     _check_pur(case, cuda_device)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+F16_MODES = [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=100),
+             dict(is_causal=False, window_size=100)]
+
+
+@pytest.mark.parametrize("D", [64, 32, 128, 96])
+@pytest.mark.parametrize("kw", F16_MODES, ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
+def test_purified_f16_backward_fast(cuda_device, D, kw):
+    """fp16 purified gradients on the 16-bit-MFMA backward kernels (the
+    reference rounds p/Z and dR to fp16 before its dots, flash_born.py:926,
+    939, 1058, as these kernels do); the forward before them runs the
+    fp32-MFMA kernel.  D = 64 and 128, and 32 / 96 with zero columns; dense,
+    causal and windows with and without causality; tau < 0, per-head gamma
+    and tau, T not a multiple of the tile."""
+    _check_pur((2, 2, 700, D, torch.float16, kw, [8.0, 5.0], [-0.05, 0.1], 0.25), cuda_device)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kw", [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=150)],
+                         ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
+def test_purified_f16_documents_backward_fast(cuda_device, D, kw):
+    """fp16 purified gradients with document ids on the document variants of
+    the 16-bit-MFMA backward kernels."""
+    doc = orc.geometric_doc_ids(2, 700, 90.0, seed=D)
+    _check_pur((2, 2, 700, D, torch.float16, kw, [8.0, 5.0], [-0.05, 0.1], 0.25), cuda_device, doc)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
@@ -100,7 +126,7 @@ def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
     _check_pur((2, 2, 500, D, dtype, dict(is_causal=is_causal), 8.0, -0.05, 0.3), cuda_device, doc)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_purified_document_tile_edges(cuda_device, dtype, D, is_causal):
