@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include <climits>
+#include <type_traits>
 
 namespace qdl {
 
@@ -125,6 +126,42 @@ __device__ __forceinline__ uint32_t born_weight_pair(float x0, float x1, float c
         const uint32_t u = relu_pk16(E::pack(x0 * fabsf(x0), x1 * fabsf(x1)));
         z = E::sum2(u, z);
         return u;
+    }
+}
+
+// An fp16 pair as two bf16 pairs that sum to it exactly (the purified
+// forward's fp16 V operand, whose products with the split fp32 weights run on
+// the bf16 MFMA): hi = each value's fp32 form truncated to bf16, lo = the
+// remainder, which holds at most the 3 low bits of fp16's 11-bit significand
+// (or of a subnormal's 10) and so is exact in bf16 and truncates exactly.
+__device__ __forceinline__ void f16_pair_to_bf16_hi_lo(uint32_t u, uint32_t& hi, uint32_t& lo) {
+    const float a = F16::lo(u), b = F16::hi(u);
+    const uint32_t ab = __float_as_uint(a) & 0xffff0000u, bb = __float_as_uint(b) & 0xffff0000u;
+    hi = (ab >> 16) | bb;
+    const float ra = a - __uint_as_float(ab), rb = b - __uint_as_float(bb);
+    lo = (__float_as_uint(ra) >> 16) | (__float_as_uint(rb) & 0xffff0000u);
+}
+
+// O^T += V^T P for the purified forward: bf16 V times the split weights
+// (hi, lo: two bf16 MFMAs), or fp16 V split exactly into bf16 hi + lo times
+// them (three: the lo x lo term, below 2^-17 of the product, is left out).
+template <class E>
+__device__ __forceinline__ f32x16 pur_pv(u32x4 v, u32x4 ph, u32x4 pl, f32x16 acc) {
+    if constexpr (std::is_same<E, F16>::value) {
+        u32x4 vh, vl;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t h, l;
+            f16_pair_to_bf16_hi_lo(v[w], h, l);
+            vh[w] = h;
+            vl[w] = l;
+        }
+        acc = BF16::mfma(vh, ph, acc);
+        acc = BF16::mfma(vh, pl, acc);
+        return BF16::mfma(vl, ph, acc);
+    } else {
+        acc = BF16::mfma(v, ph, acc);
+        return BF16::mfma(v, pl, acc);
     }
 }
 

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified: bf16");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     static_assert(!DOC || !PAD, "documents: D == 128");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
@@ -276,9 +276,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                     w[e] = pw;
                 }
                 zacc[0] += w[0] + w[1];
-                const uint32_t hi = E::pack(w[0], w[1]);
+                const uint32_t hi = BF16::pack(w[0], w[1]);
                 pk[j] = hi;
-                pl[j % PW] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+                pl[j % PW] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
             }
             return;
         }
@@ -336,11 +336,12 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
-                oacc[db] = E::mfma(ops[hh][db], bq, oacc[db]);
                 if constexpr (PUR) {
                     const u32x4 bl = {pl[4 * hh % PW], pl[(4 * hh + 1) % PW], pl[(4 * hh + 2) % PW],
                                       pl[(4 * hh + 3) % PW]};
-                    oacc[db] = E::mfma(ops[hh][db], bl, oacc[db]);
+                    oacc[db] = pur_pv<E>(ops[hh][db], bq, bl, oacc[db]);
+                } else {
+                    oacc[db] = E::mfma(ops[hh][db], bq, oacc[db]);
                 }
             }
     };
@@ -380,7 +381,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         pv_op(vop0, pk0, pl0);
         elementwise(s1, pk1, pl1, m, key0 + 32 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < (PUR ? 4 : 2) * DB; ++i) {
+        for (int i = 0; i < (PUR ? (std::is_same<E, F16>::value ? 6 : 4) : 2) * DB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x002, V3, 1);
             if constexpr (!PUR) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
@@ -759,11 +760,11 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
 
 // Purified-Born forward with document ids (bf16, D == 128; with or without a
 // causal window).
-template <int MODE>
+template <int MODE, class E = BF16>
 hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     const dim3 grid((unsigned)fast_fwd_nmb(a.T, C::BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, false, true>), grid, dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, false, true>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -773,7 +774,7 @@ hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
 // pairs take no longer than the rounds of single blocks: the second block's
 // loads then overlap the first block's fp32 output stores (B16 H8 T2048,
 // window 384: step 632 -> 620 us; the Born window forward gains nothing).
-template <int MODE, bool PAD = false>
+template <int MODE, bool PAD = false, class E = BF16>
 hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
@@ -783,7 +784,7 @@ hipError_t launch_purified_fwd_d128(const PurArgs& a, hipStream_t st) {
     const bool pair = mode_window(MODE) ? 2 * ((npair + kCUs - 1) / kCUs) <= (nsingle + kCUs - 1) / kCUs
                                         : d128_fwd_paired(a.B, a.H, a.T, MODE == kCausal);
     const dim3 grid(pair ? npair : nsingle);
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<BF16, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

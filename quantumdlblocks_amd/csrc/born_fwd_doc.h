@@ -55,7 +55,7 @@ template <class E, int DP, bool PUR = false, bool WIN = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     static_assert(NW == 4 || NW == 2, "256- or 128-row blocks");
     constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = 64 * NW;
     constexpr int KS = DP / 16;
@@ -357,11 +357,12 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
-                    oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
                     if constexpr (PUR) {
                         const u32x4 bl = {pl[qb][4 * hh % PW], pl[qb][(4 * hh + 1) % PW], pl[qb][(4 * hh + 2) % PW],
                                           pl[qb][(4 * hh + 3) % PW]};
-                        oacc[db][qb] = E::mfma(ops[hh][db], bl, oacc[db][qb]);
+                        oacc[db][qb] = pur_pv<E>(ops[hh][db], bq, bl, oacc[db][qb]);
+                    } else {
+                        oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
                     }
                 }
     };
@@ -403,9 +404,9 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
                     w[e] = masked ? 0.f : pw;
                 }
                 zacc[qb][0] += w[0] + w[1];
-                const uint32_t hi = E::pack(w[0], w[1]);
+                const uint32_t hi = BF16::pack(w[0], w[1]);
                 pk[qb][j] = hi;
-                pl[qb][j % PW] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+                pl[qb][j % PW] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
             }
         }
     };
@@ -441,7 +442,7 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
             pv_op(vop0, pk0, pl0);
             elementwise_pur(s1, pk1, pl1, key0 + 32, kd + 32, m0, m1, l0, l1, v0, v1, single);
 #pragma unroll
-            for (int i = 0; i < 4 * DB * NQB; ++i) {
+            for (int i = 0; i < (std::is_same<E, F16>::value ? 6 : 4) * DB * NQB; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
                 __builtin_amdgcn_sched_group_barrier(0x002, 20, 1);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
@@ -624,11 +625,11 @@ hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
 // Purified-Born forward with document ids (bf16, D = 64; WIN: with a causal
 // sliding window), 128-row blocks as the Born launch (p4b 220 -> 227,
 // pwc4b 155 -> 166 TFLOP/s for the step on one box, 4 VGPRs spilled).
-template <bool WIN = false>
+template <bool WIN = false, class E = BF16>
 hipError_t launch_purified_fwd_doc(const PurArgs& a, hipStream_t st) {
     constexpr int NW = 2, BM = 64 * NW;
     const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, true, WIN, NW>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<E, 64, true, WIN, NW>), grid, dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 

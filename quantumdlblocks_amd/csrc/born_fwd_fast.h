@@ -138,7 +138,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_fast_kernel(
     typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "no document masks here");
-    static_assert(!PUR || std::is_same<E, BF16>::value, "purified weights need bf16's exponent range");
+    // Purified: the weights are split into bf16 terms (fp32's exponent range)
+    // whatever the input dtype; fp16 V is split exactly into two bf16 terms.
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
     static_assert(!mode_window(MODE) || !PRO, "sliding windows: no fused prologue");
     static_assert(!PAD || PUR, "narrow head dims: purified");
@@ -337,9 +339,9 @@ void born_fwd16_fast_kernel(
                         w[e] = pw;
                     }
                     zacc[qb][0] += w[0] + w[1];
-                    const uint32_t hi = E::pack(w[0], w[1]);
+                    const uint32_t hi = BF16::pack(w[0], w[1]);
                     pk[qb][j] = hi;
-                    pl[qb][j] = E::pack(w[0] - E::lo(hi), w[1] - E::hi(hi));
+                    pl[qb][j] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
                 }
             }
             return;
@@ -407,11 +409,12 @@ void born_fwd16_fast_kernel(
                 for (int qb = 0; qb < NQB; ++qb) {
                     if (M[qb] == kSkip) continue;
                     const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2], pk[qb][4 * hh + 3]};
-                    oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
                     if constexpr (PUR) {
                         const u32x4 bl = {pl[qb][4 * hh % PW], pl[qb][(4 * hh + 1) % PW], pl[qb][(4 * hh + 2) % PW],
                                           pl[qb][(4 * hh + 3) % PW]};
-                        oacc[db][qb] = E::mfma(ops[hh][db], bl, oacc[db][qb]);
+                        oacc[db][qb] = pur_pv<E>(ops[hh][db], bq, bl, oacc[db][qb]);
+                    } else {
+                        oacc[db][qb] = E::mfma(ops[hh][db], bq, oacc[db][qb]);
                     }
                 }
     };
@@ -450,7 +453,7 @@ void born_fwd16_fast_kernel(
         pv_op(vop0, pk0, pl0, m0, m1);
         elementwise(s1, pk1, pl1, m0, m1, key0 + 32 + 4 * g);
 #pragma unroll
-        for (int i = 0; i < (PUR ? 4 : 2) * DB * NA; ++i) {
+        for (int i = 0; i < (PUR ? (std::is_same<E, F16>::value ? 6 : 4) : 2) * DB * NA; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x002, V3, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
@@ -946,16 +949,16 @@ hipError_t launch_fwd16_fast_prologue(const FwdProArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Purified-Born forward through the same kernel (bf16, D == 64, dense,
-// causal or causal sliding window; no documents).
-template <int MODE, bool PAD = false>
+// Purified-Born forward through the same kernel (bf16 or fp16, D == 64,
+// dense, causal or a sliding window; no documents).
+template <int MODE, bool PAD = false, class E = BF16>
 hipError_t launch_purified_fwd_fast(const PurArgs& a, hipStream_t st) {
     using C = FastFwdCfg<64>;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned npair = (unsigned)fast_fwd_npair(a.T, C::BM) * BH;
     const unsigned nsingle = (unsigned)fast_fwd_nmb(a.T, C::BM) * BH;
     const dim3 grid((npair < 512u || MODE != kDense) ? nsingle : npair);
-    hipLaunchKernelGGL((born_fwd16_fast_kernel<BF16, 64, MODE, true, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_fast_kernel<E, 64, MODE, true, false, PAD>), grid, dim3(C::NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

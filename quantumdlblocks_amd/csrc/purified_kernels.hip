@@ -44,42 +44,53 @@ inline bool purified_doc_fast_ok(const PurArgs& a) {
 
 template <class IN>
 static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
-    // bf16, D = 64 (and below, zero columns), dense, causal or causal
-    // window: the bf16-MFMA kernel with split weights.
-    if (std::is_same<IN, BF16>::value && purified_fast_ok(a)) {
+    // 16-bit inputs, D <= 128: the 16-bit-MFMA kernels with each weight split
+    // into two bf16 terms for P.V (fp16: the overlap on the fp16 MFMA, V split
+    // exactly into two bf16 terms).
+    using E = typename std::conditional<std::is_same<IN, F16>::value, F16, BF16>::type;
+    constexpr bool k16 = !std::is_same<IN, float>::value;
+    // D = 64 (and below, zero columns), dense, causal or a window.
+    if (k16 && purified_fast_ok(a)) {
         if (a.window > 0)
-            return a.is_causal ? launch_purified_fwd_fast<kWindow>(a, s) : launch_purified_fwd_fast<kWindowNC>(a, s);
-        return a.is_causal ? launch_purified_fwd_fast<kCausal>(a, s) : launch_purified_fwd_fast<kDense>(a, s);
+            return a.is_causal ? launch_purified_fwd_fast<kWindow, false, E>(a, s)
+                               : launch_purified_fwd_fast<kWindowNC, false, E>(a, s);
+        return a.is_causal ? launch_purified_fwd_fast<kCausal, false, E>(a, s)
+                           : launch_purified_fwd_fast<kDense, false, E>(a, s);
     }
-    if (std::is_same<IN, BF16>::value && purified_narrow_ok(a)) {
+    if (k16 && purified_narrow_ok(a)) {
         if (a.window > 0)
-            return a.is_causal ? launch_purified_fwd_fast<kWindow, true>(a, s)
-                               : launch_purified_fwd_fast<kWindowNC, true>(a, s);
-        return a.is_causal ? launch_purified_fwd_fast<kCausal, true>(a, s) : launch_purified_fwd_fast<kDense, true>(a, s);
+            return a.is_causal ? launch_purified_fwd_fast<kWindow, true, E>(a, s)
+                               : launch_purified_fwd_fast<kWindowNC, true, E>(a, s);
+        return a.is_causal ? launch_purified_fwd_fast<kCausal, true, E>(a, s)
+                           : launch_purified_fwd_fast<kDense, true, E>(a, s);
     }
-    // bf16, 64 < D <= 128, dense, causal or causal window: the D = 128
-    // kernel's purified mode.
-    if (std::is_same<IN, BF16>::value && purified_d128_ok(a)) {
+    // 64 < D <= 128, dense, causal or a window: the D = 128 kernel's purified
+    // mode.
+    if (k16 && purified_d128_ok(a)) {
         if (a.D == 128) {
             if (a.window > 0)
-                return a.is_causal ? launch_purified_fwd_d128<kWindow>(a, s) : launch_purified_fwd_d128<kWindowNC>(a, s);
-            return a.is_causal ? launch_purified_fwd_d128<kCausal>(a, s) : launch_purified_fwd_d128<kDense>(a, s);
+                return a.is_causal ? launch_purified_fwd_d128<kWindow, false, E>(a, s)
+                                   : launch_purified_fwd_d128<kWindowNC, false, E>(a, s);
+            return a.is_causal ? launch_purified_fwd_d128<kCausal, false, E>(a, s)
+                               : launch_purified_fwd_d128<kDense, false, E>(a, s);
         }
         if (a.window > 0)
-            return a.is_causal ? launch_purified_fwd_d128<kWindow, true>(a, s)
-                               : launch_purified_fwd_d128<kWindowNC, true>(a, s);
-        return a.is_causal ? launch_purified_fwd_d128<kCausal, true>(a, s) : launch_purified_fwd_d128<kDense, true>(a, s);
+            return a.is_causal ? launch_purified_fwd_d128<kWindow, true, E>(a, s)
+                               : launch_purified_fwd_d128<kWindowNC, true, E>(a, s);
+        return a.is_causal ? launch_purified_fwd_d128<kCausal, true, E>(a, s)
+                           : launch_purified_fwd_d128<kDense, true, E>(a, s);
     }
-    // bf16, D = 128, document ids (with or without a causal window): its
-    // document mode.
-    if (std::is_same<IN, BF16>::value && purified_d128_doc_ok(a)) {
-        if (a.window > 0) return launch_purified_fwd_d128_doc<kWindow>(a, s);
-        return a.is_causal ? launch_purified_fwd_d128_doc<kCausal>(a, s) : launch_purified_fwd_d128_doc<kDense>(a, s);
+    // D = 128, document ids (with or without a causal window): its document
+    // mode.
+    if (k16 && purified_d128_doc_ok(a)) {
+        if (a.window > 0) return launch_purified_fwd_d128_doc<kWindow, E>(a, s);
+        return a.is_causal ? launch_purified_fwd_d128_doc<kCausal, E>(a, s)
+                           : launch_purified_fwd_d128_doc<kDense, E>(a, s);
     }
-    // bf16, D = 64, document ids (with or without a causal window): the
-    // document kernel's purified mode.
-    if (std::is_same<IN, BF16>::value && purified_doc_fast_ok(a))
-        return a.window > 0 ? launch_purified_fwd_doc<true>(a, s) : launch_purified_fwd_doc(a, s);
+    // D = 64, document ids (with or without a causal window): the document
+    // kernel's purified mode.
+    if (k16 && purified_doc_fast_ok(a))
+        return a.window > 0 ? launch_purified_fwd_doc<true, E>(a, s) : launch_purified_fwd_doc<false, E>(a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);
@@ -125,9 +136,7 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
 template <class IN>
 static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
     // 16-bit inputs: the 16-bit-MFMA backward kernels (bf16 and fp16 alike:
-    // the reference rounds p/Z and dR to the input dtype before its dots);
-    // the forward they follow may be either kind (fp16 forwards run the
-    // fp32-MFMA kernel), as both store O and Z in fp32.
+    // the reference rounds p/Z and dR to the input dtype before its dots).
     using E = typename std::conditional<std::is_same<IN, F16>::value, F16, BF16>::type;
     constexpr bool k16 = !std::is_same<IN, float>::value;
     if (k16 && purified_fast_ok(a)) {

@@ -96,11 +96,41 @@ F16_MODES = [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, w
 def test_purified_f16_backward_fast(cuda_device, D, kw):
     """fp16 purified gradients on the 16-bit-MFMA backward kernels (the
     reference rounds p/Z and dR to fp16 before its dots, flash_born.py:926,
-    939, 1058, as these kernels do); the forward before them runs the
-    fp32-MFMA kernel.  D = 64 and 128, and 32 / 96 with zero columns; dense,
+    939, 1058, as these kernels do), after the 16-bit-MFMA forward.  D = 64
+    and 128, and 32 / 96 with zero columns; dense,
     causal and windows with and without causality; tau < 0, per-head gamma
     and tau, T not a multiple of the tile."""
     _check_pur((2, 2, 700, D, torch.float16, kw, [8.0, 5.0], [-0.05, 0.1], 0.25), cuda_device)
+
+
+@pytest.mark.parametrize("D", [64, 32, 128, 96])
+@pytest.mark.parametrize("mode", ["causal", "dense", "window", "window_nc", "docs", "docs_window", "v_subnormal"])
+def test_purified_f16_forward_fast(cuda_device, D, mode):
+    """fp16 purified forward on the 16-bit-MFMA kernels: the overlap on the
+    fp16 MFMA (exact products, fp32 sums, as the reference's fp16 dot), the
+    fp32 weights split into two bf16 terms and V split exactly into two bf16
+    terms, so P.V keeps ~16 bits of each product (the reference's is an fp32
+    dot): O and Z held to the float64 oracle to 1e-4.  Documents on the D =
+    64 document kernel and the D = 128 kernel's document mode; V scaled into
+    fp16's subnormal range for the split's low end."""
+    if mode.startswith("docs") and D not in (64, 128):
+        pytest.skip("documents at other head dims run the fp32-MFMA kernels")
+    B, H, T = 2, 2, 700
+    print(f"purified f16 forward D{D} {mode}", flush=True)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 41, std=0.25, n=3,
+                                                       dtype=torch.float16))
+    if mode == "v_subnormal":
+        v = (v.float() * 2.0 ** -18).to(torch.float16)
+    causal = mode not in ("dense", "window_nc")
+    window = {"window": 100, "window_nc": 100, "docs_window": 150}.get(mode, 0)
+    doc = orc.geometric_doc_ids(B, T, 90.0, seed=D) if mode.startswith("docs") else None
+    doc_t = None if doc is None else torch.tensor(doc, dtype=torch.int32, device=cuda_device)
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    o32, z32 = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8, doc=doc_t, window=window)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, causal,
+                                        1e-8, window, doc)
+    assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
+    assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
 
 
 @pytest.mark.parametrize("D", [64, 128])
@@ -198,6 +228,7 @@ FAST_CASES = [
 
 def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None, window=0):
     from quantumdlblocks_amd import _native
+    from quantumdlblocks_amd.kernels.flash_born import _DTYPE_CODE
 
     lib = _native.load()
     B, H, T, D = q.shape
@@ -206,7 +237,7 @@ def _pur_fwd_abi(q, k, v, scale, tau, eps_base, causal, eps, doc=None, window=0)
     sc = torch.tensor(np.atleast_1d(np.asarray(scale, dtype=np.float32)), device=q.device)
     ta = torch.tensor(np.atleast_1d(np.asarray(tau, dtype=np.float32)), device=q.device)
     rc = lib.qdl_flash_purified_born_fwd(
-        _native.DTYPE_BF16, B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), z.data_ptr(),
+        _DTYPE_CODE[q.dtype], B, H, T, D, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), z.data_ptr(),
         sc.data_ptr(), sc.numel(), ta.data_ptr(), ta.numel(), float(eps_base),
         doc.data_ptr() if doc is not None else None, int(causal), int(window), float(eps),
         torch.cuda.current_stream(q.device).cuda_stream)
