@@ -94,10 +94,14 @@ __device__ __forceinline__ bool visible(int i, int j, bool causal, int window, b
 //   u    = relu(S^T) * (dP^T / Z_i - delta'_i)   one query per lane
 //   dQ^T += K^T u          (A = K^T from the transposed LDS copy, B = u from
 //                           the accumulator registers, as P in the forward)
+// PUR: the purified gradient (flash_born.py:1035-1058) in place of u:
+// dR = (4 gamma u^3 + 2 eps_base b) dP / Z with u = relu(gamma (r - tau)),
+// b = relu(r), zero where masked, rounded to the input dtype as the
+// reference's .to(k.dtype); -delta and 1/Z come from the workspace.
 // ---------------------------------------------------------------------------
-template <class E, int DP, int NQB, int NW, int BN, int MODE, int WPE>
+template <class E, int DP, int NQB, int NW, int BN, int MODE, int WPE, bool PUR = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void born_bwd_dq16_kernel(BwdArgs p) {
+void born_bwd_dq16_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     constexpr int QW = 32 * NQB;
     constexpr int BM = NW * QW;
     constexpr int KS = DP / 16;
@@ -138,12 +142,10 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     const uint16_t* __restrict__ K = reinterpret_cast<const uint16_t*>(p.k) + base;
     const uint16_t* __restrict__ V = reinterpret_cast<const uint16_t*>(p.v) + base;
     const uint16_t* __restrict__ dO = reinterpret_cast<const uint16_t*>(p.dout) + base;
-    const float* __restrict__ Zr = p.z + (size_t)bh * T;
-    const float* __restrict__ Dl = p.delta_z + (size_t)bh * T;
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     // fp16 scales the overlap by c = 2|s|, so the dS operand is the
     // reference's 2 a dP (see E::kScaleInSquare); the epilogue divides c out.
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
@@ -151,6 +153,13 @@ void born_bwd_dq16_kernel(BwdArgs p) {
         if constexpr (E::kScaleInSquare) return x * sq_pre;
         else return x;
     };
+    float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+    }
 
     u32x4 qr[NQB][KS], dr[NQB][KS];
     float zinv[NQB], nd[NQB];
@@ -170,8 +179,13 @@ void born_bwd_dq16_kernel(BwdArgs p) {
             qr[qb][ks] = x ^ flip;
             dr[qb][ks] = y;
         }
-        zinv[qb] = ok ? 1.0f / Zr[row] : 0.f;
-        nd[qb] = ok ? -Dl[row] : 0.f;
+        if constexpr (PUR) {
+            zinv[qb] = ok ? p.zinv[(size_t)bh * T + row] : 0.f;
+            nd[qb] = ok ? p.ndelta[(size_t)bh * T + row] * zinv[qb] : 0.f;
+        } else {
+            zinv[qb] = ok ? 1.0f / p.z[(size_t)bh * T + row] : 0.f;
+            nd[qb] = ok ? -p.delta_z[(size_t)bh * T + row] : 0.f;
+        }
         qdoc[qb] = (has_doc && ok) ? docb[row] : -1;
     }
 
@@ -269,17 +283,26 @@ void born_bwd_dq16_kernel(BwdArgs p) {
                         tt[qb] = E::mfma(av, dr[qb][ks], tt[qb]);
                     }
                 }
+                uint32_t vis_bits[NQB];  // purified: bit r set for a visible register r
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) vis_bits[qb] = 0xffffu;
                 if (need_mask) {
                     const int kbase = key0 + nb * 32 + 4 * g;
 #pragma unroll
                     for (int qb = 0; qb < NQB; ++qb) {
                         const int qi = q0 + qb * 32 + c;
+                        uint32_t bits = 0;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int key = kbase + 8 * (r >> 2) + (r & 3);
                             const int kd = (kDoc && has_doc) ? doc_lds[buf][key - key0] : 0;
-                            if (!visible<MODE>(qi, key, causal, window, has_doc, qdoc[qb], kd)) s[qb][r] = 0.f;
+                            const bool vis = visible<MODE>(qi, key, causal, window, has_doc, qdoc[qb], kd);
+                            if constexpr (PUR)
+                                bits |= vis ? (1u << r) : 0u;
+                            else if (!vis)
+                                s[qb][r] = 0.f;
                         }
+                        vis_bits[qb] = bits;
                     }
                 }
                 uint32_t pk[NQB][8];
@@ -287,10 +310,25 @@ void born_bwd_dq16_kernel(BwdArgs p) {
                 for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const float u0 = fmaxf(pre(s[qb][2 * j]), 0.f) * fmaf(tt[qb][2 * j], zinv[qb], nd[qb]);
-                        const float u1 =
-                            fmaxf(pre(s[qb][2 * j + 1]), 0.f) * fmaf(tt[qb][2 * j + 1], zinv[qb], nd[qb]);
-                        pk[qb][j] = E::pack(u0, u1);
+                        if constexpr (PUR) {
+                            // A masked pair weighs zero even where its overlap is zero.
+                            float w[2];
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                const int r = 2 * j + e;
+                                const float x = s[qb][r];
+                                const float u = relu_f32(fmaf(x, pg, pgt));
+                                const float f = fmaf(p4g, u * u * u, p2e * relu_f32(x));
+                                const float d = f * fmaf(tt[qb][r], zinv[qb], nd[qb]);
+                                w[e] = ((vis_bits[qb] >> r) & 1u) ? d : 0.f;
+                            }
+                            pk[qb][j] = E::pack(w[0], w[1]);
+                        } else {
+                            const float u0 = fmaxf(pre(s[qb][2 * j]), 0.f) * fmaf(tt[qb][2 * j], zinv[qb], nd[qb]);
+                            const float u1 =
+                                fmaxf(pre(s[qb][2 * j + 1]), 0.f) * fmaf(tt[qb][2 * j + 1], zinv[qb], nd[qb]);
+                            pk[qb][j] = E::pack(u0, u1);
+                        }
                     }
                 }
 #pragma unroll
@@ -317,7 +355,7 @@ void born_bwd_dq16_kernel(BwdArgs p) {
     }
 
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+    const float f = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const int qi = q0 + qb * 32 + c;
@@ -352,10 +390,16 @@ void born_bwd_dq16_kernel(BwdArgs p) {
 // forming S and dPz over the whole head dim but accumulating dK, dV for half
 // of its columns (the wide head dims' full accumulators and stationary rows
 // exceed even one wave's 512 registers).
+// PUR: the purified gradients (flash_born.py:896-947): W = p / Z and
+// dR = (4 gamma u^3 + 2 eps_base b) dP / Z, each rounded to the input dtype
+// as the reference does, zero where masked; each key block's first column
+// split also writes its partial sums of dgamma = 4 sum u^3 dP (r - tau) and
+// dtau = -4 gamma sum u^3 dP (keys past T left out), reduced per output in a
+// fixed order afterwards.
 // ---------------------------------------------------------------------------
-template <class E, int DP, int NW, int BQ, int MODE, int WPE, int CS = 1>
+template <class E, int DP, int NW, int BQ, int MODE, int WPE, int CS = 1, bool PUR = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void born_bwd_dkdv16_kernel(BwdArgs p) {
+void born_bwd_dkdv16_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     constexpr int BK = NW * 32;
     constexpr int KS = DP / 16;
     constexpr int DBF = DP / 32;                // column blocks of the head dim
@@ -402,12 +446,11 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
     const uint16_t* __restrict__ K = reinterpret_cast<const uint16_t*>(p.k) + base;
     const uint16_t* __restrict__ V = reinterpret_cast<const uint16_t*>(p.v) + base;
     const uint16_t* __restrict__ dO = reinterpret_cast<const uint16_t*>(p.dout) + base;
-    const float* __restrict__ Zr = p.z + (size_t)bh * T;
     const float* __restrict__ NDl = p.ndelta + (size_t)bh * T;
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     // fp16 scales the overlap by c = 2|s|, so the dS operand is the
     // reference's 2 a dP (see E::kScaleInSquare); the epilogue divides c out.
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
@@ -415,6 +458,16 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         if constexpr (E::kScaleInSquare) return x * sq_pre;
         else return x;
     };
+    float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
+    if constexpr (PUR) {
+        ptau = p.tau[p.per_head_tau ? h : 0];
+        pg = sc;
+        pgt = -sc * ptau;
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+        pe = p.eps_base;
+    }
+    float dg_acc = 0.f, dt_acc = 0.f;  // purified: sum u^3 dP (r - tau), sum u^3 dP
 
     u32x4 kr[KS], vr[KS];
 #pragma unroll
@@ -446,7 +499,10 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         if (tid < BQ) {
             const int i = i0 + tid;
             ndreg = i < T ? NDl[i] : 0.f;
-            zireg = i < T ? 1.0f / Zr[i] : 0.f;
+            if constexpr (PUR)
+                zireg = i < T ? p.zinv[(size_t)bh * T + i] : 0.f;
+            else
+                zireg = i < T ? 1.0f / p.z[(size_t)bh * T + i] : 0.f;
             if (kDoc && has_doc) dreg = i < T ? docb[i] : -1;
         }
     };
@@ -537,22 +593,51 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
                     s = E::mfma(aq, kr[ks], s);
                     dp = E::mfma(ad, vr[ks], dp);
                 }
+                uint32_t vis_bits = 0xffffu;  // purified: bit r set for a visible register r
                 if (need_mask) {
                     const int ibase = i0 + qs * 32 + 4 * g;
+                    uint32_t bits = 0;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int qi = ibase + 8 * (r >> 2) + (r & 3);
                         const int qd = (kDoc && has_doc) ? doc_lds[buf][qi - i0] : 0;
-                        if (!visible<MODE>(qi, key, causal, window, has_doc, qd, kdoc)) s[r] = 0.f;
+                        const bool vis = visible<MODE>(qi, key, causal, window, has_doc, qd, kdoc);
+                        if constexpr (PUR)
+                            bits |= vis ? (1u << r) : 0u;
+                        else if (!vis)
+                            s[r] = 0.f;
                     }
+                    vis_bits = bits;
                 }
                 uint32_t w2[8], u2[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float a0 = fmaxf(pre(s[2 * j]), 0.f), a1 = fmaxf(pre(s[2 * j + 1]), 0.f);
-                    const float t0 = a0 * zi[2 * j], t1 = a1 * zi[2 * j + 1];
-                    w2[j] = E::pack(t0 * a0, t1 * a1);
-                    u2[j] = E::pack(t0 * dp[2 * j], t1 * dp[2 * j + 1]);
+                    if constexpr (PUR) {
+                        // Masked pairs weigh zero; queries past T have 1/Z = 0.
+                        float ww[2], uu[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int r = 2 * j + e;
+                            const float x = s[r];
+                            float u = relu_f32(fmaf(x, pg, pgt));
+                            float bb = relu_f32(x);
+                            if (!((vis_bits >> r) & 1u)) u = bb = 0.f;
+                            const float u2_ = u * u;
+                            const float dpz = dp[r] * zi[r];
+                            const float a = u2_ * u * dpz;
+                            dg_acc = fmaf(a, x - ptau, dg_acc);
+                            dt_acc += a;
+                            ww[e] = fmaf(u2_, u2_, pe * bb * bb) * zi[r];
+                            uu[e] = fmaf(p4g, u2_ * u, p2e * bb) * dpz;
+                        }
+                        w2[j] = E::pack(ww[0], ww[1]);
+                        u2[j] = E::pack(uu[0], uu[1]);
+                    } else {
+                        const float a0 = fmaxf(pre(s[2 * j]), 0.f), a1 = fmaxf(pre(s[2 * j + 1]), 0.f);
+                        const float t0 = a0 * zi[2 * j], t1 = a1 * zi[2 * j + 1];
+                        w2[j] = E::pack(t0 * a0, t1 * a1);
+                        u2[j] = E::pack(t0 * dp[2 * j], t1 * dp[2 * j + 1]);
+                    }
                 }
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
@@ -578,11 +663,33 @@ void born_bwd_dkdv16_kernel(BwdArgs p) {
         __syncthreads();
     }
 
+    if constexpr (PUR) {
+        // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
+        // waves), from the first column split of the key block only (the
+        // others form the same sums); keys past T excluded.
+        __shared__ float red[2 * NW];
+        float a = key < T ? 4.f * dg_acc : 0.f;
+        float t2 = key < T ? -4.f * sc * dt_acc : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off);
+            t2 += __shfl_xor(t2, off);
+        }
+        if (lane == 0) red[wave] = a, red[NW + wave] = t2;
+        __syncthreads();
+        if (cs == 0 && tid == 0) {
+            float sa = 0.f, st = 0.f;
+            for (int w = 0; w < NW; ++w) sa += red[w], st += red[NW + w];
+            const int nwg = (int)(gridDim.x / CS);
+            p.part[bid] = sa;
+            p.part[nwg + bid] = st;
+        }
+    }
     if (key < T) {
         uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
         uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
-        const float fk = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
-        const float fv = E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
+        const float fk = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+        const float fv = PUR ? 1.f : E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll

@@ -25,18 +25,28 @@
 // rows a 16-lane transpose read touches fall in distinct banks).
 // At the end each lane owns one query: z is completed with one cross-half
 // shuffle, O = O^T / (z + eps / s^2), Z = s^2 z + eps.
+//
+// PUR: the purified-Born forward (flash_born.py:696-811) on the same tiles,
+// as the fast kernels run it: p = relu(gamma (r - tau))^4 + eps_base relu(r)^2
+// in fp32, Z = sum p + eps in fp32, masked pairs and keys past T weighing
+// zero, each weight split into two bf16 terms for P.V (fp16 V split exactly
+// into two bf16 terms, pur_pv), O = sum p v / Z written in fp32.  Used for the
+// head dims above 128.
 #pragma once
 
+#include <type_traits>
+
 #include "born_common.h"
+#include "purified_args.h"
 
 namespace qdl {
 
 // ---------------------------------------------------------------------------
 // 16-bit (bf16 / fp16) forward.
 // ---------------------------------------------------------------------------
-template <class E, int DP, int NQB, int NW, int BN, int MODE, int WPE>
+template <class E, int DP, int NQB, int NW, int BN, int MODE, int WPE, bool PUR = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-void born_fwd16_kernel(FwdArgs p) {
+void born_fwd16_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(DP % 32 == 0 && DP <= 256, "padded head dim");
     static_assert(BN % 32 == 0, "key tile");
     constexpr int QW = 32 * NQB;
@@ -94,10 +104,17 @@ void born_fwd16_kernel(FwdArgs p) {
     const int32_t* __restrict__ docb = has_doc ? p.doc + (size_t)b * T : nullptr;
 
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = (sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     // fp16: the weights are the reference's relu(s r)^2 (c = |s| times the
     // sign-folded overlap; born_weight_pair); bf16: s^2 goes back in per row.
     const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
+    // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
+    float pg = 0.f, pgt = 0.f, pse = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        pse = sqrtf(p.eps_base);
+    }
 
     // Q^T operand, resident for the whole kernel.
     u32x4 qr[NQB][KS];
@@ -222,10 +239,15 @@ void born_fwd16_kernel(FwdArgs p) {
             active = active && (key0 + BN - 1 > q0 - window);
             need_mask = need_mask || (key0 <= q0 + QW - 1 - window);
         }
+        // Purified: a key past T (zero K row) still weighs relu(-gamma tau)^4.
+        if (PUR) need_mask = need_mask || (key0 + BN > T);
         if (!active) return;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             f32x16 s[NQB];
+            uint32_t vis_bits[NQB];  // purified: bit r set for a visible register r
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) vis_bits[qb] = 0xffffu;
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) s[qb] = zero16();
 #pragma unroll
@@ -254,23 +276,46 @@ void born_fwd16_kernel(FwdArgs p) {
                     // key = kbase + off(r); visible iff off(r) <= qi - kbase
                     // (causal) and off(r) > qi - kbase - window.
                     const int lim = q0 + qb * 32 + c - kbase;
-                    const int hi = causal ? lim : INT_MAX;
+                    const int hi = causal ? lim : (PUR ? T - 1 - kbase : INT_MAX);
                     const int lo = window > 0 ? lim - window : INT_MIN;
+                    uint32_t bits = 0;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int off = 8 * (r >> 2) + (r & 3);
                         bool vis = (off <= hi) && (off > lo);
                         if (kDoc && doc_mask) vis = vis && (kd[r] == qdoc[qb]);
-                        if (!vis) s[qb][r] = 0.f;
+                        if constexpr (PUR)
+                            bits |= vis ? (1u << r) : 0u;
+                        else if (!vis)
+                            s[qb][r] = 0.f;
                     }
+                    vis_bits[qb] = bits;
                 }
             }
             uint32_t pk[NQB][8];
+            uint32_t pl[NQB][PUR ? 8 : 1];
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    pk[qb][j] = born_weight_pair<E>(s[qb][2 * j], s[qb][2 * j + 1], sq_pre, zacc[qb][j & 1]);
+                    if constexpr (PUR) {
+                        float w[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const float x = s[qb][2 * j + e];
+                            const float u = relu_f32(fmaf(x, pg, pgt));
+                            const float bq = relu_f32(x * pse);
+                            const float u2 = u * u;
+                            const float pw = fmaf(u2, u2, bq * bq);
+                            w[e] = ((vis_bits[qb] >> (2 * j + e)) & 1u) ? pw : 0.f;
+                        }
+                        zacc[qb][0] += w[0] + w[1];
+                        const uint32_t hi = BF16::pack(w[0], w[1]);
+                        pk[qb][j] = hi;
+                        pl[qb][j] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
+                    } else {
+                        pk[qb][j] = born_weight_pair<E>(s[qb][2 * j], s[qb][2 * j + 1], sq_pre, zacc[qb][j & 1]);
+                    }
                 }
             }
             // V^T operand of the 16-key chunk (nb, hh): lane group G = lane / 16
@@ -290,7 +335,13 @@ void born_fwd16_kernel(FwdArgs p) {
                     for (int qb = 0; qb < NQB; ++qb) {
                         const u32x4 bq = {pk[qb][4 * hh], pk[qb][4 * hh + 1], pk[qb][4 * hh + 2],
                                           pk[qb][4 * hh + 3]};
-                        oacc[db][qb] = E::mfma(a, bq, oacc[db][qb]);
+                        if constexpr (PUR) {
+                            const u32x4 bl = {pl[qb][4 * hh], pl[qb][4 * hh + 1], pl[qb][4 * hh + 2],
+                                              pl[qb][4 * hh + 3]};
+                            oacc[db][qb] = pur_pv<E>(a, bq, bl, oacc[db][qb]);
+                        } else {
+                            oacc[db][qb] = E::mfma(a, bq, oacc[db][qb]);
+                        }
                     }
                 }
             }
@@ -377,8 +428,34 @@ void born_fwd16_kernel(FwdArgs p) {
     }
 
     // Epilogue: one query per lane.
-    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
     float* __restrict__ Zp = p.z + (size_t)bh * T;
+    if constexpr (PUR) {
+        // O = acc / (Z + eps) and Z + eps in fp32.
+        float* __restrict__ O32 = p.o + base;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float zl = zacc[qb][0] + zacc[qb][1];
+            const float zd = zl + __shfl_xor(zl, 32) + p.eps;
+            const int qi = q0 + qb * 32 + c;
+            if (qi < T) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int d = db * 32 + 8 * j + 4 * g;
+                        if (d < D) {
+                            const f32x16& o = oacc[db][qb];
+                            const f32x4 w = {o[4 * j] / zd, o[4 * j + 1] / zd, o[4 * j + 2] / zd, o[4 * j + 3] / zd};
+                            *reinterpret_cast<f32x4*>(O32 + (size_t)qi * D + d) = w;
+                        }
+                    }
+                }
+                if (g == 0) Zp[qi] = zd;
+            }
+        }
+        return;
+    }
+    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
 #pragma unroll

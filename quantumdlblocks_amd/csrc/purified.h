@@ -743,6 +743,8 @@ void purified_dq_kernel(PurArgs p) {
 
 // dgamma / dtau: output o sums, in a fixed order, the partials of the dK/dV
 // workgroups whose head it covers (all of them for a shared parameter).
+// (A template, so that several translation units can each hold it.)
+template <int kUnused = 0>
 __global__ __launch_bounds__(256) void purified_param_reduce_kernel(PurArgs p, int nwg, int n_scale) {
     __shared__ double red[256];
     const int out = blockIdx.x;
@@ -801,7 +803,7 @@ hipError_t launch_purified_bwd(const PurArgs& a, hipStream_t st) {
                        dim3(C::NW * 64), 0, st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
-    hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, st, a, nwg, n_scale);
+    hipLaunchKernelGGL(purified_param_reduce_kernel<0>, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, st, a, nwg, n_scale);
     return hipGetLastError();
 }
 

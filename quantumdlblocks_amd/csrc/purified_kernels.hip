@@ -11,6 +11,11 @@ namespace qdl {
 
 inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
+// 16-bit inputs above head dim 128: the generic 16-bit-MFMA kernels' purified
+// mode (purified_wide.hip).
+hipError_t purified_wide_fwd_launch(int dtype, const PurArgs& a, hipStream_t s);
+hipError_t purified_wide_bwd_launch(int dtype, const PurArgs& a, hipStream_t s);
+
 // The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
 // offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
 // kernels, as the Born dispatch does.
@@ -91,6 +96,8 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // kernel's purified mode.
     if (k16 && purified_doc_fast_ok(a))
         return a.window > 0 ? launch_purified_fwd_doc<true, E>(a, s) : launch_purified_fwd_doc<false, E>(a, s);
+    // Above D = 128: the generic 16-bit-MFMA kernels' purified mode.
+    if (k16 && a.D > 128) return purified_wide_fwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);
@@ -115,7 +122,7 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
                        s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
-    hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
+    hipLaunchKernelGGL(purified_param_reduce_kernel<0>, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
     return hipGetLastError();
 }
 
@@ -129,7 +136,7 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
     if (e != hipSuccess) return e;
     const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 128);
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
-    hipLaunchKernelGGL(purified_param_reduce_kernel, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
+    hipLaunchKernelGGL(purified_param_reduce_kernel<0>, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
     return hipGetLastError();
 }
 
@@ -169,6 +176,7 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         return a.is_causal ? purified_bwd_fast<kCausal, true, false, E>(a, s)
                            : purified_bwd_fast<kDense, true, false, E>(a, s);
     }
+    if (k16 && a.D > 128) return purified_wide_bwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);
         case 64: return launch_purified_bwd<IN, 64>(a, s);
