@@ -11,8 +11,9 @@ namespace qdl {
 
 inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
-// 16-bit inputs above head dim 128: the generic 16-bit-MFMA kernels' purified
-// mode (purified_wide.hip).
+// 16-bit inputs above head dim 128, and with document ids at head dims other
+// than 64 and 128: the generic 16-bit-MFMA kernels' purified mode
+// (purified_wide.hip).
 hipError_t purified_wide_fwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 hipError_t purified_wide_bwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 
@@ -96,8 +97,9 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // kernel's purified mode.
     if (k16 && purified_doc_fast_ok(a))
         return a.window > 0 ? launch_purified_fwd_doc<true, E>(a, s) : launch_purified_fwd_doc<false, E>(a, s);
-    // Above D = 128: the generic 16-bit-MFMA kernels' purified mode.
-    if (k16 && a.D > 128) return purified_wide_fwd_launch(E::kDtype, a, s);
+    // Above D = 128, and documents at other head dims: the generic
+    // 16-bit-MFMA kernels' purified mode.
+    if (k16 && (a.D > 128 || a.doc != nullptr)) return purified_wide_fwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
         case 64: return launch_purified_fwd<IN, 64>(a, s);
@@ -176,7 +178,7 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         return a.is_causal ? purified_bwd_fast<kCausal, true, false, E>(a, s)
                            : purified_bwd_fast<kDense, true, false, E>(a, s);
     }
-    if (k16 && a.D > 128) return purified_wide_bwd_launch(E::kDtype, a, s);
+    if (k16 && (a.D > 128 || a.doc != nullptr)) return purified_wide_bwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_bwd<IN, 32>(a, s);
         case 64: return launch_purified_bwd<IN, 64>(a, s);
