@@ -204,6 +204,18 @@ def test_bwd_sliding_window_noncausal_fast_kernels(cuda_device, dtype, window):
                scale=[8.0, -0.7], check_dscale=True)
 
 
+@pytest.mark.parametrize("T", [1, 37, 64, 129, 256, 300, 513])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("window", [1, 3, 100])
+def test_bwd_noncausal_window_ragged(cuda_device, T, D, window):
+    """kWindowNC dQ and dK/dV on ragged lengths: a single partial tile, T on
+    and beside the tile and key-block edges, windows shorter and longer than T
+    (the dK/dV launch walks the key blocks from the last)."""
+    _check_bwd(1, 2, T, D, torch.bfloat16, cuda_device, is_causal=False, window_size=window,
+               scale=[8.0, -0.7] if D == 64 else [0.09, -0.3], std=1.0 if D == 64 else 0.7, seed=T + window,
+               check_dscale=True)
+
+
 @pytest.mark.parametrize("T", [1, 37, 64, 200, 256, 300, 513, 1100])
 @pytest.mark.parametrize("is_causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

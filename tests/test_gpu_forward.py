@@ -227,6 +227,16 @@ def test_fwd_sliding_window_noncausal_fast_kernel(cuda_device, dtype, window):
     _check_fwd(2, 2, 1100, 64, dtype, cuda_device, is_causal=False, window_size=window, seed=window + 9)
 
 
+@pytest.mark.parametrize("T", [1, 37, 64, 255, 256, 300, 513])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("window", [1, 3, 100])
+def test_fwd_noncausal_window_ragged(cuda_device, T, D, window):
+    """kWindowNC on ragged lengths: a single partial tile, T on and beside
+    the tile and block edges, windows shorter and longer than T."""
+    _check_fwd(1, 2, T, D, torch.bfloat16, cuda_device, is_causal=False, window_size=window,
+               scale=8.0 if D == 64 else 0.09, seed=T + window)
+
+
 @pytest.mark.parametrize("T", [1, 37, 64, 255, 256, 300, 513, 777, 1100])
 @pytest.mark.parametrize("is_causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -132,6 +132,18 @@ def test_purified_f16_forward_fast(cuda_device, D, mode):
     assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
 
 
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 37, 129])
+@pytest.mark.parametrize("kw", [dict(is_causal=False), dict(is_causal=False, window_size=3)],
+                         ids=lambda kw: f"W{kw.get('window_size', 0)}")
+def test_purified_ragged_16bit(cuda_device, D, dtype, T, kw):
+    """16-bit purified attention on short and ragged lengths (one partial
+    tile; the keys past T weigh zero though their overlap is zero), dense and
+    with a non-causal window, on the D = 64, D = 128 and generic kernels."""
+    _check_pur((1, 2, T, D, dtype, kw, [8.0, 5.0], [-0.05, 0.1], 0.25), cuda_device)
+
+
 WIDE_MODES = ["causal", "dense", "window", "window_nc", "docs"]
 
 
