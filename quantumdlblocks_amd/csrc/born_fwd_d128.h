@@ -70,15 +70,21 @@ struct FwdD128Cfg {
     static constexpr int NST = 3;   // K/V ring stages
 };
 
-template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW (documents only): 4 waves over 128-row blocks, two workgroups per CU
+// and a two-stage ring (fewer blocks straddle a document edge, and two
+// workgroups per CU overlap one's start-up with the other's tiles);
+// otherwise 8 waves over 256-row blocks.
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false, int NW = 8>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     static_assert(!DOC || !PAD, "documents: D == 128");
+    static_assert(NW == 8 || (NW == 4 && DOC), "128-row blocks: the document mode");
     using C = FwdD128Cfg;
-    constexpr int DP = C::DP, NW = C::NW, BM = C::BM, BN = C::BN, NST = C::NST;
+    constexpr int DP = C::DP, BM = 32 * NW, BN = C::BN, NST = NW == 8 ? C::NST : 2;
+    constexpr int KDW = BN / NW;  // documents: key ids loaded per wave per tile
     constexpr int KS = DP / 16;            // 16-wide contraction steps of QK
     constexpr int DB = DP / 32;            // 32-column blocks of O
     constexpr int RB = DP * 2;             // bytes per row
@@ -173,9 +179,10 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), (PAD && kc >= CG) ? kBufOOB : off + (kc << 4));
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), (PAD && vc >= CG) ? kBufOOB : off + (vc << 4));
         }
-        // Documents: this wave's 8 of the tile's key ids (lanes 0-1).
+        // Documents: this wave's KDW of the tile's key ids (lanes 0 .. KDW/4 - 1).
         if constexpr (DOC)
-            if (lane < 2) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 8), (key0 + wave * 8 + lane * 4) * 4);
+            if (lane < KDW / 4)
+                dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
     auto issue_q = [&](int mb) __attribute__((always_inline)) {
 #pragma unroll
@@ -441,6 +448,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     };
     // Output staging: this wave's rows of the Q block (documents: its 32 rows
     // of the idle ring, waves 0-3 in the K ring, 4-7 in the V ring).
+    static_assert(!DOC || NST * BN >= 4 * 32, "documents: four waves' rows fit one ring");
     uint8_t* const stg = DOC ? (wave < 4 ? k_lds : v_lds) + 32 * (wave & 3) * RB : q_lds + 32 * wave * RB;
     auto put_lds = [&]() __attribute__((always_inline)) {
         int ln = lane;
@@ -577,21 +585,23 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             bq_lo = min(bq_lo, s_rng[2 * w]);
             bq_hi = max(bq_hi, s_rng[2 * w + 1]);
         }
-        constexpr int kDocTileLoads = 2 * LPW + 1;  // K, V and 8 key ids per wave
+        constexpr int kDocTileLoads = 2 * LPW + 1;  // K, V and the wave's key ids
         const int ncand = nt_a;
         for (int c0 = 0; c0 < ncand; c0 += CAP) {
             const int n = screen_doc_tiles<BN>(docb, T, tb_a * BN, c0, min(CAP, ncand - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
+            // Tiles 0 .. NST-2 up front, tile u+NST-1 after the barrier of
+            // step u (into the stage of tile u-1).
             if (n > 0) issue(0, 0);
-            if (n > 1) issue(1, 1);
+            if (NST == 3 && n > 1) issue(1, 1);
             if (c0 == 0) load_q_regs();
             for (int u = 0; u < n; ++u) {
-                if (u + 1 < n)
+                if (NST == 3 && u + 1 < n)
                     wait_vmcnt<kDocTileLoads>();
                 else
                     wait_vmcnt<0>();
                 __syncthreads();
-                if (u + 2 < n) issue(u + 2, (u + 2) % NST);
+                if (u + NST - 1 < n) issue(u + NST - 1, (u + NST - 1) % NST);
                 int soff = (u % NST) * TB;  // opaque: operand addresses formed per tile
                 asm volatile("" : "+s"(soff));
                 const uint8_t* kb = k_lds + soff;
@@ -740,8 +750,10 @@ inline bool d128_fwd_paired(int B, int H, int T, bool causal) {
 template <class E, int MODE>
 hipError_t launch_fwd16_d128_doc(const FwdArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
-    const dim3 grid((unsigned)fast_fwd_nmb(a.T, C::BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, false, true>), grid, dim3(C::NW * 64), 0, st, a);
+    // 128-row blocks of 4 waves, two workgroups per CU.
+    constexpr int NW = 4, BM = 32 * NW;
+    const dim3 grid((unsigned)fast_fwd_nmb(a.T, BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, false, true, NW>), grid, dim3(NW * 64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -763,8 +775,9 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
 template <int MODE, class E = BF16>
 hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
-    const dim3 grid((unsigned)fast_fwd_nmb(a.T, C::BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, false, true>), grid, dim3(C::NW * 64), 0, st, a);
+    constexpr int NW = 4, BM = 32 * NW;
+    const dim3 grid((unsigned)fast_fwd_nmb(a.T, BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, false, true, NW>), grid, dim3(NW * 64), 0, st, a);
     return hipGetLastError();
 }
 
