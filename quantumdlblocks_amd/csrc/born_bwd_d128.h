@@ -47,21 +47,26 @@ struct BwdD128Cfg {
     static constexpr int BK = 128;  // dK/dV: keys per block (32 per wave)
 };
 
-template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW (documents only): 4 waves over 128-row blocks, two workgroups per CU and
+// a two-stage ring, as the document forward; otherwise 8 waves over 256-row
+// blocks.
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false, int NW = 8>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
 
-    constexpr int DP = 128, NW = 8, BN = 64, NST = 3, BM = BwdD128Cfg::BM;
+    static_assert(NW == 8 || (NW == 4 && DOC), "128-row blocks: the document mode");
+    constexpr int DP = 128, BN = 64, NST = NW == 8 ? 3 : 2, BM = 32 * NW;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BN * RB;            // bytes per K or V tile
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
     constexpr int CAP = 256;               // documents: candidate tiles screened per pass
-    // Loads per wave per tile: K, V (documents: and 8 of the key document ids).
+    constexpr int KDW = BN / NW;           // documents: key ids loaded per wave per tile
+    // Loads per wave per tile: K, V (documents: and KDW of the key document ids).
     constexpr int kTileLoads = 2 * LPW + (DOC ? 1 : 0);
     static_assert(TB % (1024 * NW) == 0 && BM * RB <= 2 * NST * TB && BM == 32 * NW, "tile split / staging");
     constexpr bool kWin = mode_window(MODE);
@@ -205,8 +210,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 
     // Tile u (documents: kept tile u of the list) -> stage u % NST:
     // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane,
-    // slot = row * CPR + chunk'; documents: also this wave's 8 key document
-    // ids (lanes 0-1, 16 bytes each).
+    // slot = row * CPR + chunk'; documents: also this wave's KDW key document
+    // ids (lanes 0 .. KDW/4 - 1, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
         int key0 = (tb + u) * BN;
@@ -223,7 +228,8 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
         }
         if constexpr (DOC)
-            if (lane < 2) dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * 8), (key0 + wave * 8 + lane * 4) * 4);
+            if (lane < KDW / 4)
+                dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
 
     // Operand reads.  Rows: K/V row nb * 32 + c (A operands of S^T, T^T);
@@ -405,15 +411,17 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
             const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
+            // Tiles 0 .. NST-2 up front, tile u+NST-1 after the barrier of
+            // step u (into the stage of tile u-1).
             if (n > 0) issue(0);
-            if (n > 1) issue(1);
+            if (NST == 3 && n > 1) issue(1);
             for (int u = 0; u < n; ++u) {
-                if (u + 1 < n)
+                if (NST == 3 && u + 1 < n)
                     wait_vmcnt<kTileLoads>();
                 else
                     wait_vmcnt<0>();
                 __syncthreads();
-                if (u + 2 < n) issue(u + 2);
+                if (u + NST - 1 < n) issue(u + NST - 1);
                 int soff = (u % NST) * TB;
                 asm volatile("" : "+s"(soff));
                 const uint8_t* kb = k_lds + soff;
@@ -1054,10 +1062,13 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 template <class E, int MODE, bool PAD = false, bool DOC = false>
 hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
-    const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
+    // dQ: 256-row blocks of 8 waves, 128-row blocks of 4 with documents (one
+    // dscale partial per workgroup either way).
+    constexpr int NWQ = DOC ? 4 : BwdD128Cfg::NW, BMQ = 32 * NWQ;
+    const unsigned nq = (unsigned)((a.T + BMQ - 1) / BMQ);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD, DOC>), dim3(nq * BH),
-                       dim3(BwdD128Cfg::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD, DOC, NWQ>), dim3(nq * BH), dim3(NWQ * 64), 0,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD, DOC>), dim3(nk * BH),
@@ -1074,10 +1085,11 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
 template <int MODE, bool PAD = false, bool DOC = false, class E = BF16>
 hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
-    const unsigned nq = (unsigned)((a.T + BwdD128Cfg::BM - 1) / BwdD128Cfg::BM);
+    constexpr int NWQ = DOC ? 4 : BwdD128Cfg::NW, BMQ = 32 * NWQ;
+    const unsigned nq = (unsigned)((a.T + BMQ - 1) / BMQ);
     const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, true, PAD, DOC>), dim3(nq * BH),
-                       dim3(BwdD128Cfg::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, true, PAD, DOC, NWQ>), dim3(nq * BH), dim3(NWQ * 64), 0,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, true, PAD, DOC>), dim3(nk * BH),
