@@ -1204,6 +1204,11 @@ hipError_t launch_bwd_common_pre(const BwdArgs& a, hipStream_t st) {
 // dscale reduction (defined in born_bwd_common.hip).
 hipError_t launch_bwd_common_post(const BwdArgs& a, hipStream_t st);
 
+// 128 < D <= 256 without document ids, 16-bit inputs: the DMA-ring kernels of
+// born_bwd_d256.h (instantiated in born_bwd_d256.hip).
+template <class E>
+hipError_t launch_bwd16_wide(const BwdArgs& a, hipStream_t st);
+
 template <class E, int DP, int MODE>
 hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
     using C = Bwd16Cfg<DP>;
@@ -1272,6 +1277,11 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
             return a.is_causal ? launch_bwd16_d128<E, kCausal, false, true>(a, st)
                                : launch_bwd16_d128<E, kDense, false, true>(a, st);
         }
+    }
+    // 128 < D <= 256, dense, causal or a sliding window with or without
+    // causality (no documents): the DMA-ring kernels for wide rows.
+    if constexpr (DP > 128) {
+        if (a.D > 128 && a.doc == nullptr && addr32) return launch_bwd16_wide<E>(a, st);
     }
     if constexpr (DP == 96 || DP == 128) {
         if (a.D > 64 && a.D < 128 && a.doc == nullptr && addr32) {
