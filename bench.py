@@ -89,6 +89,9 @@ CONFIGS.update({
     "pw5": (16, 16, 2048, 64, 0.125, False, None, True),
     "pwc4b": (4, 16, 8192, 64, 0.125, False, 512.0, True),
     "pdw5": (16, 8, 2048, 128, 0.125, False, None, True),
+    # head dim 256 on the C3 / C5 work (a quarter of the heads, same flops)
+    "h3": (16, 4, 1024, 256, 0.125, False, None, False),
+    "h5": (16, 4, 2048, 256, 1.0, False, None, True),
 })
 PURIFIED |= {"pd3", "pd5", "pdc4b", "pw5", "pwc4b", "pdw5"}
 WINDOW = {"w3": 256, "w5": 512, "dw5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 384, "pwc4b": 384, "pdw5": 384}

@@ -40,17 +40,20 @@ struct BwdD256Cfg {
     static constexpr int LEAD = 4;  // operand reads in flight ahead of the MFMAs
 };
 
-// A lane's byte offsets into a 64-row tile of 512-byte rows (chunk c of row
-// r at chunk c ^ swz256(r)).  swz256 reads bits 0-3 of the row and changes
-// bits 0-3 of the chunk, so steps of 16 rows and of 16 chunks move every
-// offset by a constant: 8 offsets serve the row reads (row 32 nb + c, chunk
-// 2 ks + g: r[ks & 7] + 256 (ks >> 3) + 32 RB nb) and 8 the transposed reads
-// (rows 32 nb + 16 hh + 4 g + (lane & 15) / 4 + 8 e, columns 32 db + 16
-// ((lane >> 4) & 1) + 4 (lane & 3): t[db & 3][e] + 256 (db >> 2) + RB (32 nb
-// + 16 hh)), the rest being instruction immediates.
-struct LaneOffs512 {
+// A lane's LDS byte offsets into the two-stage ring of 64-row tiles of
+// 512-byte rows (chunk c of row r at chunk c ^ swz256(r)).  swz256 reads bits
+// 0-3 of the row and changes bits 0-3 of the chunk, so steps of 16 rows and
+// of 16 chunks move every offset by a constant: 8 offsets serve the row reads
+// (row 32 nb + c, chunk 2 ks + g: r[ks & 7] + 256 (ks >> 3) + 32 RB nb) and 8
+// the transposed reads (rows 32 nb + 16 hh + 4 g + (lane & 15) / 4 + 8 e,
+// columns 32 db + 16 ((lane >> 4) & 1) + 4 (lane & 3): t[db & 3][e] + 256
+// (db >> 2) + RB (32 nb + 16 hh)), the rest being instruction immediates
+// (below 64 KiB).  Stage st's two tiles start at 64 KiB st, so moving to the
+// other stage flips bit 16 of every offset in place (flip()): the 16 VGPRs are
+// the kernel's only LDS addresses.
+struct RingOffs512 {
     int r[8], t[4][2];
-    __device__ __forceinline__ LaneOffs512(int lane) {
+    __device__ __forceinline__ RingOffs512(int lane) {
         constexpr int RB = 512;
         const int c = lane & 31, g = lane >> 5;
         const int trow = 4 * g + ((lane & 15) >> 2);
@@ -65,6 +68,32 @@ struct LaneOffs512 {
                 t[j][e] = row * RB + (((4 * j + (tcol >> 3)) ^ swz256(row)) << 4) + (tcol & 7) * 2;
             }
     }
+    __device__ __forceinline__ void flip() {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r[j] ^= 0x10000;
+            asm volatile("" : "+v"(r[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                t[j][e] ^= 0x10000;
+                asm volatile("" : "+v"(t[j][e]));
+            }
+    }
+    // which: the first (0) or second (1) tile of the stage.
+    __device__ __forceinline__ u32x4 row(const uint8_t* lds, int which, int nb, int ks) const {
+        return *reinterpret_cast<const u32x4*>(lds + r[ks & 7] + which * 32768 + nb * 32 * RB_ + (ks >> 3) * 256);
+    }
+    __device__ __forceinline__ u32x4 tr(const uint8_t* lds, int which, int nb, int hh, int db) const {
+        const int k = which * 32768 + (nb * 32 + hh * 16) * RB_ + (db >> 2) * 256;
+        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(lds + t[db & 3][0] + k));
+        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(lds + t[db & 3][1] + k));
+        const u32x4 a = {x[0], x[1], y[0], y[1]};
+        return a;
+    }
+    static constexpr int RB_ = 512;
 };
 
 template <class E, int MODE, bool PAD = false>
@@ -194,30 +223,9 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
 
     // Operand reads (rows: A operands of S^T, T^T; K^T, transposed: A of
     // dQ^T, in the key order of the accumulator layout of U) through the
-    // stage's lane addresses; which = 0 (K) or 1 (V, one tile further).
-    const LaneOffs512 lo(lane);
-    struct Addr {
-        const uint8_t* r[8];
-        const uint8_t* t[4][2];
-    };
-    auto addr_of = [&](const uint8_t* sb) __attribute__((always_inline)) -> Addr {
-        Addr a;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a.r[j] = sb + lo.r[j];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a.t[j][0] = sb + lo.t[j][0], a.t[j][1] = sb + lo.t[j][1];
-        return a;
-    };
-    auto row_rd = [&](const Addr& a, int which, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
-        return *reinterpret_cast<const u32x4*>(a.r[ks & 7] + which * TB + nb * 32 * RB + (ks >> 3) * 256);
-    };
-    auto tr_rd = [&](const Addr& a, int which, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
-        const int k = which * TB + (nb * 32 + hh * 16) * RB + (db >> 2) * 256;
-        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(a.t[db & 3][0] + k));
-        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(a.t[db & 3][1] + k));
-        const u32x4 r = {x[0], x[1], y[0], y[1]};
-        return r;
-    };
+    // ring's lane offsets (current stage); which = 0 (K) or 1 (V).
+    static_assert(2 * TB == 0x10000, "stages 64 KiB apart");
+    RingOffs512 ro(lane);
     constexpr int LEAD = BwdD256Cfg::LEAD;
 
     f32x16 acc[DB];
@@ -235,12 +243,12 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
     //   U = relu(S^T) (T^T / Z - delta / Z), masked keys zeroed
     //   dQ^T += K^T U                    (A = K^T, B = U)
     // Each phase's operand reads run LEAD MFMAs ahead of their use.
-    auto half = [&](const Addr& ad, int nb, int kbase, auto m) __attribute__((always_inline)) {
+    auto half = [&](int nb, int kbase, auto m) __attribute__((always_inline)) {
         f32x16 s = zero16(), t = zero16();
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            s = E::mfma(row_rd(ad, 0, nb, ks), qr[ks], s);
-            t = E::mfma(row_rd(ad, 1, nb, ks), dr[ks], t);
+            s = E::mfma(ro.row(smem, 0, nb, ks), qr[ks], s);
+            t = E::mfma(ro.row(smem, 1, nb, ks), dr[ks], t);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);  // DS read
 #pragma unroll
@@ -276,7 +284,7 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
-                acc[db] = E::mfma(tr_rd(ad, 0, nb, hh, db), bq, acc[db]);
+                acc[db] = E::mfma(ro.tr(smem, 0, nb, hh, db), bq, acc[db]);
             }
         // Two transposed reads per operand.
         __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 1);
@@ -306,15 +314,17 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
     auto run = [&](int tend, auto m) __attribute__((always_inline)) {
         for (; u < tend; ++u) {
             step();
-            int soff = (u % NST) * 2 * TB;
-            asm volatile("" : "+s"(soff));
-            const Addr ad = addr_of(smem + soff);
             const int key0 = (tb + u) * BN;
-            half(ad, 0, key0 + 4 * g, m);
-            half(ad, 1, key0 + 32 + 4 * g, m);
+            half(0, key0 + 4 * g, m);
+            half(1, key0 + 32 + 4 * g, m);
+            ro.flip();
         }
     };
-    for (; u < runs.ta; ++u) step();
+    // (ro follows the stage of tile u: flipped after every tile, idle or not.)
+    for (; u < runs.ta; ++u) {
+        step();
+        ro.flip();
+    }
     run(runs.tf, Masked{});
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
@@ -353,6 +363,14 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
     }
 }
 
+// dK/dV (keys stationary).  Every MFMA here accumulates in AGPRs: a wave's
+// dK and dV accumulators for 32 keys fill all 256, so with the S and dPz
+// accumulators the compiler keeps two accumulator blocks in VGPRs and moves
+// them through the AGPRs around their MFMAs (about 110 register moves per 64
+// MFMAs of a 32-query half), with no scratch spills.  Splitting a key block
+// into a dV and a dK workgroup (each fits the AGPRs, but S is formed twice:
+// five contractions per pair instead of four) measured 15% slower for the
+// step (B16 H4 T2048 D256: 529 against 623 TFLOP/s).
 template <class E, int MODE, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
@@ -362,14 +380,15 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BQ * RB;            // bytes per Q or dO tile
-    constexpr int SB = 2 * TB + 2 * BQ * 4;  // bytes per stage: Q, dO, -delta, 1/Z
+    constexpr int RW = 2 * BQ * 4;         // -delta and 1/Z rows of a stage
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
-    static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && BK * RB <= NST * SB && BK == 32 * NW,
-                  "tile split / staging");
     constexpr bool kWin = mode_window(MODE);
     constexpr bool kCaus = mode_causal(MODE);
+    static_assert(2 * TB == 0x10000 && BK * RB <= 2 * NST * TB, "stages 64 KiB apart / staging");
 
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * SB];
+    // Stage st: Q and dO tiles at 2 TB st; -delta and 1/Z rows at
+    // 2 NST TB + RW st.  Afterwards the output staging.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB + NST * RW];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -430,10 +449,11 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
     const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
 
-    // Tile u -> stage u % NST.  Waves 0 and 1 also bring the tile's -delta and
-    // 1/Z (lanes 0-15, 16 bytes each).
+    // Tile u -> stage u % NST (Q and dO tiles at 2 TB st, -delta and 1/Z
+    // rows at 2 NST TB + RW st).  Waves 0 and 1 also bring the tile's -delta
+    // and 1/Z (lanes 0-15, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
-        uint8_t* sb = smem + (u % NST) * SB;
+        uint8_t* sb = smem + (u % NST) * 2 * TB;
         const int i0 = q_lo + u * BQ;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
@@ -445,7 +465,7 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
             dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
         }
         if (lane < 16) {
-            const uint32_t la = lds_addr(sb + 2 * TB + wave * BQ * 4);
+            const uint32_t la = lds_addr(smem + 2 * NST * TB + (u % NST) * RW + wave * BQ * 4);
             if (wave == 0)
                 dma_load16(rdl, la, (i0 + 4 * lane) * 4);
             else if (wave == 1)
@@ -454,39 +474,13 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     };
 
     // Operand reads (rows: A of S and dPz; transposed: A of dV^T, dK^T)
-    // through the stage's lane addresses; which = 0 (Q) or 1 (dO).
-    const LaneOffs512 lo(lane);
-    struct Addr {
-        const uint8_t* r[8];
-        const uint8_t* t[4][2];
-    };
-    auto addr_of = [&](const uint8_t* sb) __attribute__((always_inline)) -> Addr {
-        Addr a;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a.r[j] = sb + lo.r[j];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a.t[j][0] = sb + lo.t[j][0], a.t[j][1] = sb + lo.t[j][1];
-        return a;
-    };
-    auto row_rd = [&](const Addr& a, int which, int nb, int ks) __attribute__((always_inline)) -> u32x4 {
-        return *reinterpret_cast<const u32x4*>(a.r[ks & 7] + which * TB + nb * 32 * RB + (ks >> 3) * 256);
-    };
-    auto tr_rd = [&](const Addr& a, int which, int nb, int hh, int db) __attribute__((always_inline)) -> u32x4 {
-        const int k = which * TB + (nb * 32 + hh * 16) * RB + (db >> 2) * 256;
-        const u32x2 x = lds_read_tr16(reinterpret_cast<const uint16_t*>(a.t[db & 3][0] + k));
-        const u32x2 y = lds_read_tr16(reinterpret_cast<const uint16_t*>(a.t[db & 3][1] + k));
-        const u32x4 r = {x[0], x[1], y[0], y[1]};
-        return r;
-    };
-    constexpr int LEAD = 2;  // every register is taken: two reads ahead
+    // through the ring's lane offsets (current stage); which = 0 (Q) or 1 (dO).
+    RingOffs512 ro(lane);
+    constexpr int LEAD = BwdD256Cfg::LEAD;
 
     f32x16 acc_v[DB], acc_k[DB];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        acc_v[db] = zero16();
-        acc_k[db] = zero16();
-        asm volatile("" : "+a"(acc_v[db]), "+a"(acc_k[db]));
-    }
+    for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
 
     constexpr int kFull = 1, kMasked = 2;
     using Full = std::integral_constant<int, kFull>;
@@ -499,9 +493,9 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     //   t = relu(S) / Z_i, W = t relu(S), U = t dPz   (masked queries zeroed)
     //   dV^T += dO^T W,  dK^T += Q^T U   (A = dO^T, Q^T transposed reads)
     // Each phase's operand reads run LEAD MFMAs ahead of their use.
-    auto half = [&](const uint8_t* sb, const Addr& ad, int nb, int qbase, auto m) __attribute__((always_inline)) {
-        const float* dl = reinterpret_cast<const float*>(sb + 2 * TB);
-        const float* zl = reinterpret_cast<const float*>(sb + 2 * TB + BQ * 4);
+    auto half = [&](const uint8_t* rw, int nb, int qbase, auto m) __attribute__((always_inline)) {
+        const float* dl = reinterpret_cast<const float*>(rw);
+        const float* zl = reinterpret_cast<const float*>(rw + BQ * 4);
         f32x16 s = zero16(), dp;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -511,8 +505,8 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            s = E::mfma(row_rd(ad, 0, nb, ks), kr[ks], s);
-            dp = E::mfma(row_rd(ad, 1, nb, ks), vr[ks], dp);
+            s = E::mfma(ro.row(smem, 0, nb, ks), kr[ks], s);
+            dp = E::mfma(ro.row(smem, 1, nb, ks), vr[ks], dp);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, LEAD + 4, 0);  // DS read (and the -delta rows)
 #pragma unroll
@@ -555,8 +549,8 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
             const u32x4 bu = {u2[4 * hh], u2[4 * hh + 1], u2[4 * hh + 2], u2[4 * hh + 3]};
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                acc_v[db] = E::mfma(tr_rd(ad, 1, nb, hh, db), bw, acc_v[db]);
-                acc_k[db] = E::mfma(tr_rd(ad, 0, nb, hh, db), bu, acc_k[db]);
+                acc_v[db] = E::mfma(ro.tr(smem, 1, nb, hh, db), bw, acc_v[db]);
+                acc_k[db] = E::mfma(ro.tr(smem, 0, nb, hh, db), bu, acc_k[db]);
             }
         }
         // Two transposed reads per operand.
@@ -583,48 +577,49 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     auto run = [&](int tend, auto m) __attribute__((always_inline)) {
         for (; u < tend; ++u) {
             step();
-            int soff = (u % NST) * SB;
-            asm volatile("" : "+s"(soff));
-            const Addr ad = addr_of(smem + soff);
+            int roff = (u % NST) * RW;
+            asm volatile("" : "+s"(roff));
+            const uint8_t* rw = smem + 2 * NST * TB + roff;
             const int i0 = q_lo + u * BQ;
-            half(smem + soff, ad, 0, i0 + 4 * g, m);
-            half(smem + soff, ad, 1, i0 + 32 + 4 * g, m);
+            half(rw, 0, i0 + 4 * g, m);
+            half(rw, 1, i0 + 32 + 4 * g, m);
+            ro.flip();
         }
     };
-    for (; u < runs.ta; ++u) step();
+    // (ro follows the stage of tile u: flipped after every tile, idle or not.)
+    for (; u < runs.ta; ++u) {
+        step();
+        ro.flip();
+    }
     run(runs.tf, Masked{});
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
 
-    // Epilogue: dK = 2 s|s| / c acc_k, dV = (s / c)^2 acc_v (c = sq_pre: 1,
-    // or 2|s| for fp16, where the factors are s and 1/4), packed and staged,
-    // one output at a time, in this wave's own 32 rows of the idle ring (row
-    // r at smem + RB r, chunks XOR-swizzled by r & 15), then read back 16
-    // bytes per lane and stored 2 whole rows per instruction.
+    // Epilogue: dK = 2 s|s| / c acc, dV = (s / c)^2 acc (c = sq_pre: 1, or
+    // 2|s| for fp16, where the factors are s and 1/4), packed and staged in
+    // this wave's own 32 rows of the idle ring (row r at smem + RB r, chunks
+    // XOR-swizzled by r & 15), then read back 16 bytes per lane and stored 2
+    // whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
-    const float fk = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
-    const float fv = E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc;
-    uint16_t* __restrict__ dK = reinterpret_cast<uint16_t*>(p.dk) + base;
-    uint16_t* __restrict__ dV = reinterpret_cast<uint16_t*>(p.dv) + base;
     int ln = lane;
     asm volatile("" : "+v"(ln));
+    auto put = [&](const f32x16 (&acc)[DB], float f, void* dst) __attribute__((always_inline)) {
+        uint16_t* __restrict__ out = reinterpret_cast<uint16_t*>(dst) + base;
+        {
+            const int row = 32 * wave + (ln & 31);
+            uint8_t* rb = smem + row * RB;
 #pragma unroll
-    for (int which = 0; which < 2; ++which) {
-        const int row = 32 * wave + (ln & 31);
-        uint8_t* rb = smem + row * RB;
-        const float f = which ? fv : fk;
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x16& o = which ? acc_v[db] : acc_k[db];
-                u32x2 w;
-                w[0] = E::pack(o[4 * j] * f, o[4 * j + 1] * f);
-                w[1] = E::pack(o[4 * j + 2] * f, o[4 * j + 3] * f);
-                const int chunk = 4 * db + j;
-                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * (ln >> 5)) = w;
-            }
+                for (int j = 0; j < 4; ++j) {
+                    u32x2 w;
+                    w[0] = E::pack(acc[db][4 * j] * f, acc[db][4 * j + 1] * f);
+                    w[1] = E::pack(acc[db][4 * j + 2] * f, acc[db][4 * j + 3] * f);
+                    const int chunk = 4 * db + j;
+                    *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * (ln >> 5)) = w;
+                }
+        }
         const int chunk = ln & 31;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -632,9 +627,11 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
             const u32x4 x = *reinterpret_cast<const u32x4*>(smem + r2 * RB + ((chunk ^ (r2 & 15)) << 4));
             const int kk = K0 + r2;
             if (kk < T && (!PAD || chunk < CG))
-                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>((which ? dV : dK) + (size_t)kk * D + chunk * 8));
+                __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(out + (size_t)kk * D + chunk * 8));
         }
-    }
+    };
+    put(acc_k, E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc), p.dk);
+    put(acc_v, E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc, p.dv);
 }
 
 // The 128 < D <= 256 backward: dQ (and the workspace), dK/dV, then dscale

@@ -160,13 +160,33 @@ def test_bwd_head_dims(cuda_device, D, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mode", ["causal", "dense", "window", "documents"])
 def test_bwd_wide_head_dims_column_split(cuda_device, D, dtype, mode):
-    """Wide head dims (16-bit): D >= 192 runs two dK/dV workgroups per key
-    block, each holding half of the column blocks (seven split unevenly at
-    D = 224), D = 160 one; several key blocks and query tiles, every mask
-    mode, per-head scales, dscale."""
+    """Wide head dims (16-bit): without documents the DMA-ring kernels for
+    128 < D <= 256 (born_bwd_d256.h: D < 256 with zero columns); with
+    documents the generic kernels (D >= 192 in two dK/dV workgroups per key
+    block, each holding half of the column blocks, seven split unevenly at
+    D = 224); several key blocks and query tiles, every mask mode, per-head
+    scales, dscale."""
     kw = dict(is_causal=mode != "dense", window_size=90 if mode == "window" else 0,
               doc=orc.geometric_doc_ids(2, 300, 60.0, seed=D) if mode == "documents" else None)
     _check_bwd(2, 2, 300, D, dtype, cuda_device, scale=[0.2, -0.1], std=0.5, seed=D + 1, check_dscale=True, **kw)
+
+
+@pytest.mark.parametrize("D", [136, 200, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", [(True, 0, 1), (True, 0, 64), (True, 0, 129), (True, 0, 700), (False, 0, 300),
+                                  (True, 1, 300), (True, 63, 300), (True, 200, 700), (False, 1, 300),
+                                  (False, 64, 300), (False, 129, 700), (False, 1000, 300)])
+def test_bwd_wide_dma_kernels(cuda_device, D, dtype, case):
+    """128 < D <= 256 without documents: the dQ kernel (4 waves over 128
+    query rows, 64-key tiles through a two-stage ring) and the dK/dV kernel
+    (dV and dK of a 128-key block in two workgroups); padded head dims
+    (136, 200: zero columns past D), one and several key blocks, a partial
+    last tile and block, causal and dense, windows with and without
+    causality shorter and longer than T; per-head scales (one negative) and
+    dscale."""
+    is_causal, window, T = case
+    _check_bwd(1, 2, T, D, dtype, cuda_device, is_causal=is_causal, window_size=window, scale=[0.3, -0.15],
+               std=0.5, seed=D + T + window, check_dscale=True)
 
 
 def test_bwd_head_dim_above_256_takes_the_eager_path(cuda_device):
