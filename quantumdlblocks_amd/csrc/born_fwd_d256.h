@@ -1,0 +1,258 @@
+// Flash-Born forward for head dims 128 < D <= 256 (bf16 / fp16): dense,
+// causal, or a sliding window with or without causality; no document ids.
+// The arithmetic of the D == 64 and D == 128 forwards (born_fwd_fast.h,
+// born_fwd_d128.h: S^T = K Q^T on the 16-bit MFMA, p' = relu(x|x|) packed,
+// Z from the packed weights, O^T += V^T P, O = acc / (Z + eps / s^2)) with
+// the register split and load pipeline of the wide-row backward
+// (born_bwd_d256.h):
+//   * A wave's 32 query rows need 64 VGPRs of Q operands and 128 registers
+//     of O accumulators (which the MFMAs keep in AGPRs), so the kernel runs
+//     one wave per SIMD: 4 waves over a 128-row block, wave w owning rows
+//     32 w .. 32 w + 31, Q loaded straight from HBM into registers.
+//   * K/V tiles of 64 keys (32 KiB each) go global -> LDS with buffer_load
+//     ... lds through a ring of two stages 64 KiB apart, one workgroup per
+//     CU; chunks swizzled by swz256 (row reads of K, transposed reads of V,
+//     both conflict-free), the lane offsets flipped in place between stages.
+//   * Per 32-key half: S^T (16 MFMAs, K rows), the elementwise pass, O^T
+//     (16 MFMAs, V transposed), each phase's LDS operand reads issued a few
+//     MFMAs ahead.  Each MFMA takes one operand from LDS.
+//   * Each wave's tiles split into runs (nothing visible / cut by its
+//     diagonal or window edge / fully visible), one loop per run.
+// PAD: 128 < D < 256 (a multiple of 8): the loads of the chunks past D return
+// zeros, Q is zero there, and the output chunks past D are not stored.
+#pragma once
+
+#include "born_bwd_d256.h"
+
+namespace qdl {
+
+template <class E, int MODE, bool PAD = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void born_fwd16_d256_kernel(FwdArgs p) {
+    static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    constexpr int DP = 256, NW = 4, BN = 64, NST = 2, BM = 32 * NW;
+    constexpr int KS = DP / 16, DB = DP / 32;
+    constexpr int RB = DP * 2;             // bytes per row
+    constexpr int CPR = RB / 16;           // 16-byte chunks per row
+    constexpr int TB = BN * RB;            // bytes per K or V tile
+    constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of K, V)
+    static_assert(TB % (1024 * NW) == 0 && 2 * TB == 0x10000 && BM * RB <= 2 * NST * TB,
+                  "tile split / stages 64 KiB apart / staging");
+    constexpr bool kWin = mode_window(MODE);
+    constexpr bool kCaus = mode_causal(MODE);
+
+    // Stage st: K tile at 2 TB st, V tile right after it; afterwards the
+    // output staging.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+
+    const int T = p.T;
+    const int BH = p.B * p.H;
+    const int nmb = (T + BM - 1) / BM;
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    // The longest key ranges first (causal: the last blocks).
+    const int mb = kCaus ? (nmb - 1 - bid / BH) : (bid / BH);
+    const int h = bh % p.H;
+    const int R = mb * BM;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, g = lane >> 5;
+    const int qrow = R + 32 * wave + c;  // this lane's query row
+
+    const int D = PAD ? p.D : DP;
+    const int CG = D / 8;
+    const size_t base = (size_t)bh * T * D;
+    const float sc = p.scale[p.per_head_scale ? h : 0];
+    const uint32_t flip = sc < 0.f ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    // fp16: the reference's weights relu(s r)^2 (born_weight_pair).
+    const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
+
+    // Key tiles tb .. tb+ntiles-1 (tb: the window's first key tile, else 0).
+    const int W = kWin ? p.window : 0;
+    const int tb = kWin ? max(0, R - W + 1) / BN : 0;
+    const int ntiles = (kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN) - tb;
+    // This wave's rows rw .. rw + 31 see keys [rw - W + 1, rw + 31] (causal,
+    // window) and all of them see keys [rw + 32 - W, rw].
+    const int rw = R + 32 * wave;
+    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kRunsBig,
+                        kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kRunsBig);
+
+    const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
+    const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
+    const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+
+    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
+    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    auto issue = [&](int u) __attribute__((always_inline)) {
+        const int key0 = (tb + u) * BN;
+        uint8_t* kb = smem + (u % NST) * 2 * TB;
+        uint8_t* vb = kb + TB;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int slot = (wave * LPW + i) * 64 + lane;
+            const int row = slot / CPR, pc = slot % CPR;
+            const int ch = pc ^ swz256(row);
+            const int off = (PAD && ch >= CG) ? kBufOOB : (key0 + row) * (2 * D) + (ch << 4);
+            dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
+            dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
+        }
+    };
+
+    // Tile 0 goes out before the Q rows are loaded, so the two overlap.
+    issue(0);
+    // This lane's Q row chunks 2 ks + g (B operands of S^T), the sign of the
+    // scale folded in.
+    u32x4 qr[KS];
+    {
+        const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 x = {0u, 0u, 0u, 0u};
+            if (qrow < T && (!PAD || 2 * ks + g < CG)) x = ldg16(Qg + (size_t)qrow * D + (2 * ks + g) * 8);
+            qr[ks] = x ^ flip;
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
+    }
+
+    // Operand reads through the ring's lane offsets (current stage):
+    // which = 0 (K rows: A of S^T) or 1 (V transposed: A of O^T).
+    RingOffs512 ro(lane);
+    constexpr int LEAD = BwdD256Cfg::LEAD;
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float zacc[2] = {0.f, 0.f};
+
+    constexpr int kFull = 1, kMasked = 2;
+    using Full = std::integral_constant<int, kFull>;
+    using Masked = std::integral_constant<int, kMasked>;
+    // One 32-key half nb of a tile (lane: query c, keys kbase + 8 (r / 4) +
+    // r % 4 of register r):
+    //   S^T = K Q^T                 (A = K rows, B = Q^T)
+    //   p' = relu(x|x|) packed, z += p'   (masked keys zeroed first)
+    //   O^T += V^T P                (A = V^T, B = P)
+    auto half = [&](int nb, int kbase, auto m) __attribute__((always_inline)) {
+        f32x16 s = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s = E::mfma(ro.row(smem, 0, nb, ks), qr[ks], s);
+        __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);  // DS read
+#pragma unroll
+        for (int i = 0; i < KS - LEAD; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(m)::value == kMasked) {
+            // Masked past the lane's row (causal) and before its window.
+            const int lim = qrow - kbase;
+            const int wlo = kWin ? lim - W + 1 : 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
+            }
+        }
+        uint32_t pk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pk[j] = born_weight_pair<E>(s[2 * j], s[2 * j + 1], sq_pre, zacc[j & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] = E::mfma(ro.tr(smem, 1, nb, hh, db), bq, oacc[db]);
+        }
+        // Two transposed reads per operand.
+        __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 1);
+#pragma unroll
+        for (int i = 0; i < 2 * DB - LEAD / 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, LEAD / 2, 1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Pipeline: at the top of step u, once tile u has landed (each wave waits
+    // for its own share) and the barrier has made it visible and freed tile
+    // u-1's stage, tile u+1 goes out into that stage.
+    int u = 0;
+    auto step = [&]() __attribute__((always_inline)) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (u + 1 < ntiles) issue(u + 1);
+    };
+    auto run = [&](int tend, auto m) __attribute__((always_inline)) {
+        for (; u < tend; ++u) {
+            step();
+            const int key0 = (tb + u) * BN;
+            half(0, key0 + 4 * g, m);
+            half(1, key0 + 32 + 4 * g, m);
+            ro.flip();
+        }
+    };
+    // (ro follows the stage of tile u: flipped after every tile, idle or not.)
+    for (; u < runs.ta; ++u) {
+        step();
+        ro.flip();
+    }
+    run(runs.tf, Masked{});
+    run(runs.tg, Full{});
+    run(runs.tv, Masked{});
+    for (; u < ntiles; ++u) step();
+
+    // Epilogue: Z = s^2 z + eps and O = acc / (z + eps / s^2) (c = sq_pre
+    // folded into the weights), packed and staged in this wave's own 32 rows
+    // of the idle ring (row r at smem + RB r, chunks XOR-swizzled by r & 15),
+    // read back 16 bytes per lane and stored 2 whole rows per instruction.
+    __syncthreads();  // every wave is done with the ring
+    const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
+    const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
+    const float zl = zacc[0] + zacc[1];
+    const float ztot = zl + __shfl_xor(zl, 32);
+    const float rcp = 1.0f / (ztot + eps_s);
+    uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(p.o) + base;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    {
+        const int row = 32 * wave + (ln & 31);
+        uint8_t* rb = smem + row * RB;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                u32x2 w;
+                w[0] = E::pack(oacc[db][4 * j] * rcp, oacc[db][4 * j + 1] * rcp);
+                w[1] = E::pack(oacc[db][4 * j + 2] * rcp, oacc[db][4 * j + 3] * rcp);
+                const int chunk = 4 * db + j;  // columns 32 db + 8 j + 4 g .. +3
+                *reinterpret_cast<u32x2*>(rb + ((chunk ^ (row & 15)) << 4) + 8 * (ln >> 5)) = w;
+            }
+    }
+    if (g == 0 && qrow < T) __builtin_nontemporal_store(s2 * ztot + p.eps, p.z + (size_t)bh * T + qrow);
+    const int chunk = ln & 31;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = 32 * wave + 2 * i + (ln >> 5);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(smem + row * RB + ((chunk ^ (row & 15)) << 4));
+        const int qi = R + row;
+        if (qi < T && (!PAD || chunk < CG))
+            __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(O + (size_t)qi * D + chunk * 8));
+    }
+}
+
+// One 128-row block per workgroup, one workgroup per CU (128 KiB of LDS),
+// the longest key ranges first.
+template <class E, int MODE, bool PAD>
+hipError_t launch_fwd16_d256(const FwdArgs& a, hipStream_t st) {
+    const unsigned nmb = (unsigned)((a.T + 127) / 128);
+    hipLaunchKernelGGL((born_fwd16_d256_kernel<E, MODE, PAD>), dim3(nmb * (unsigned)(a.B * a.H)), dim3(256), 0, st,
+                       a);
+    return hipGetLastError();
+}
+
+}  // namespace qdl

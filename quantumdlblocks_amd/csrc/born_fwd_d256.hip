@@ -1,0 +1,29 @@
+// Forward kernels for head dims 128 < D <= 256 (bf16 and fp16 inputs, no
+// document ids): the DMA-ring kernel of born_fwd_d256.h, one instantiation
+// per mask mode, unpadded (D == 256) and padded.
+#include "born_fwd.h"
+#include "born_fwd_d256.h"
+
+namespace qdl {
+
+namespace {
+
+template <class E, bool PAD>
+hipError_t wide_modes(const FwdArgs& a, hipStream_t s) {
+    if (a.window > 0)
+        return a.is_causal ? launch_fwd16_d256<E, kWindow, PAD>(a, s) : launch_fwd16_d256<E, kWindowNC, PAD>(a, s);
+    return a.is_causal ? launch_fwd16_d256<E, kCausal, PAD>(a, s) : launch_fwd16_d256<E, kDense, PAD>(a, s);
+}
+
+}  // namespace
+
+template <class E>
+hipError_t launch_fwd16_wide(const FwdArgs& a, hipStream_t st) {
+    if (a.D <= 128 || a.D > 256 || a.D % 8 != 0 || a.doc != nullptr) return hipErrorInvalidValue;
+    return a.D == 256 ? wide_modes<E, false>(a, st) : wide_modes<E, true>(a, st);
+}
+
+template hipError_t launch_fwd16_wide<BF16>(const FwdArgs&, hipStream_t);
+template hipError_t launch_fwd16_wide<F16>(const FwdArgs&, hipStream_t);
+
+}  // namespace qdl

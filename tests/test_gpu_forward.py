@@ -191,6 +191,22 @@ def test_fwd_head_dims(cuda_device, D, dtype):
     _check_fwd(2, 2, 96, D, dtype, cuda_device, scale=1.0 / math.sqrt(D), seed=D)
 
 
+@pytest.mark.parametrize("D", [136, 200, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", [(True, 0, 1), (True, 0, 64), (True, 0, 129), (True, 0, 700), (False, 0, 300),
+                                  (True, 1, 300), (True, 63, 300), (True, 200, 700), (False, 1, 300),
+                                  (False, 64, 300), (False, 129, 700), (False, 1000, 300)])
+def test_fwd_wide_dma_kernel(cuda_device, D, dtype, case):
+    """128 < D <= 256 without documents: the DMA-ring forward (4 waves over
+    128 query rows, 64-key tiles through a two-stage ring); padded head dims
+    (136, 200: zero columns past D), one and several blocks, a partial last
+    tile and block, causal and dense, windows with and without causality
+    shorter and longer than T; per-head scales (one negative); O and Z."""
+    is_causal, window, T = case
+    _check_fwd(1, 2, T, D, dtype, cuda_device, is_causal=is_causal, window_size=window,
+               scale=np.array([0.3, -0.15], dtype=np.float32), std=0.5, seed=D + T + window)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("D", [272, 320])
 def test_fwd_head_dims_above_256_take_the_eager_path(cuda_device, D, dtype):
