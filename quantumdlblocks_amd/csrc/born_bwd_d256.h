@@ -26,6 +26,11 @@
 // PAD: 128 < D < 256 (a multiple of 8) on the same kernels: the loads of the
 // chunks past D return zeros, the stationary rows are zero there, and the
 // output chunks past D are not stored.
+// PUR: the purified-Born gradients (flash_born.py:812-1061) as in the D == 128
+// kernels' purified mode: dR = (4 gamma u^3 + 2 eps_base b) dP and W = p / Z
+// rounded to the input dtype before their contractions, O read in fp32, and
+// the dK/dV workgroups writing their partial sums of dgamma and dtau (reduced
+// per output afterwards in a fixed order).
 #pragma once
 
 #include "born_bwd_d128.h"
@@ -96,10 +101,11 @@ struct RingOffs512 {
     static constexpr int RB_ = 512;
 };
 
-template <class E, int MODE, bool PAD = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void born_bwd16_dq_d256_kernel(BwdArgs p) {
+void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
     constexpr int DP = 256, NW = BwdD256Cfg::NW, BN = 64, NST = 2, BM = BwdD256Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -135,47 +141,77 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
     const int CG = D / 8;
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = sc < 0.f ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
+    // Purified: t = gamma r - gamma tau; dR / dP = 4 gamma u^3 + 2 eps_base b.
+    float pg = 0.f, pgt = 0.f, p4g = 0.f, p2e = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+    }
 
     // Stationary operands (sign-flipped Q, dO: B operands of S^T and T^T),
     // delta = dO . O from the stored O (each lane holds half a row, the other
-    // half is in lane ^ 32), and the workspace rows -delta, 1/Z, delta/Z.
+    // half is in lane ^ 32; purified: the fp32 O), and the workspace rows
+    // -delta, 1/Z (Born: and delta/Z).
     u32x4 qr[KS], dr[KS];
     float zinv, nd;
     {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
         const uint16_t* __restrict__ dOg = reinterpret_cast<const uint16_t*>(p.dout) + base;
-        const uint16_t* __restrict__ Og = reinterpret_cast<const uint16_t*>(p.o) + base;
         const bool ok = qrow < T;
         float dl = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u}, o = {0u, 0u, 0u, 0u};
-            if (ok && (!PAD || 2 * ks + g < CG)) {
+            u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+            const bool in = ok && (!PAD || 2 * ks + g < CG);
+            if (in) {
                 x = ldg16(Qg + (size_t)qrow * D + (2 * ks + g) * 8);
                 y = ldg16(dOg + (size_t)qrow * D + (2 * ks + g) * 8);
-                o = ldg16(Og + (size_t)qrow * D + (2 * ks + g) * 8);
             }
             qr[ks] = x ^ flip;
             dr[ks] = y;
+            if constexpr (PUR) {
+                if (in) {
+                    const float* o32 = p.o_in + base + (size_t)qrow * D + (2 * ks + g) * 8;
+                    const f32x4 oa = *reinterpret_cast<const f32x4*>(o32);
+                    const f32x4 ob = *reinterpret_cast<const f32x4*>(o32 + 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dl += E::lo(o[j]) * E::lo(y[j]) + E::hi(o[j]) * E::hi(y[j]);
+                    for (int j = 0; j < 4; ++j) {
+                        const float o0 = j < 2 ? oa[2 * j] : ob[2 * j - 4];
+                        const float o1 = j < 2 ? oa[2 * j + 1] : ob[2 * j - 3];
+                        dl += o0 * E::lo(y[j]) + o1 * E::hi(y[j]);
+                    }
+                }
+            } else {
+                u32x4 o = {0u, 0u, 0u, 0u};
+                if (in) o = ldg16(reinterpret_cast<const uint16_t*>(p.o) + base + (size_t)qrow * D + (2 * ks + g) * 8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dl += E::lo(o[j]) * E::lo(y[j]) + E::hi(o[j]) * E::hi(y[j]);
+            }
         }
         dl += __shfl_xor(dl, 32);
         const size_t row = (size_t)bh * T + qrow;
-        const float zr = ok ? p.z[row] : 1.f;
+        float zr = 1.f;
+        if (ok) {
+            if constexpr (PUR)
+                zr = p.z_in[row];
+            else
+                zr = p.z[row];
+        }
         zinv = ok ? 1.0f / zr : 0.f;
         nd = ok ? -(dl / zr) : 0.f;
         if (ok && g == 0) {
             p.ndelta[row] = -dl;
             p.zinv[row] = zinv;
-            p.delta_z[row] = dl / zr;
+            if constexpr (!PUR) p.delta_z[row] = dl / zr;
         }
     }
     // This workgroup's part of dscale = (2/s) eps sum delta / Z (closed form):
     // its rows' sum in a fixed order (lanes, then waves), one double.
-    {
+    if constexpr (!PUR) {
         float dz = (g == 0) ? -nd : 0.f;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) dz += __shfl_xor(dz, off);
@@ -258,25 +294,52 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
         }
         __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (decltype(m)::value == kMasked) {
-            // Key kbase + 8 (r / 4) + r % 4 of register r: masked past the
-            // lane's row, and (window) before its first key.
+        uint32_t pk[8];
+        if constexpr (PUR) {
+            // A masked pair weighs zero even where its overlap is zero (u =
+            // relu(-gamma tau) > 0 for tau < 0).  Keys past T need no mask
+            // here: their K rows (zero) multiply U.
             const int lim = qrow - kbase;
             const int wlo = kWin ? lim - W + 1 : 0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int off = 8 * (r >> 2) + (r & 3);
-                if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
-            }
-        }
-        uint32_t pk[8];
+            for (int j = 0; j < 8; ++j) {
+                float w[2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float x0 = s[2 * j], x1 = s[2 * j + 1];
-            if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
-            const float a0 = __int_as_float(max(__float_as_int(x0), 0));
-            const float a1 = __int_as_float(max(__float_as_int(x1), 0));
-            pk[j] = E::pack(a0 * fmaf(t[2 * j], zinv, nd), a1 * fmaf(t[2 * j + 1], zinv, nd));
+                for (int e = 0; e < 2; ++e) {
+                    const int r = 2 * j + e;
+                    const float x = s[r];
+                    const float uu = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                    const float bb = __int_as_float(max(__float_as_int(x), 0));
+                    const float f = fmaf(p4g, uu * uu * uu, p2e * bb);
+                    float d = f * fmaf(t[r], zinv, nd);
+                    if constexpr (decltype(m)::value == kMasked) {
+                        const int off = 8 * (r >> 2) + (r & 3);
+                        if ((kCaus && off > lim) || (kWin && off < wlo)) d = 0.f;
+                    }
+                    w[e] = d;
+                }
+                pk[j] = E::pack(w[0], w[1]);
+            }
+        } else {
+            if constexpr (decltype(m)::value == kMasked) {
+                // Key kbase + 8 (r / 4) + r % 4 of register r: masked past
+                // the lane's row, and (window) before its first key.
+                const int lim = qrow - kbase;
+                const int wlo = kWin ? lim - W + 1 : 0;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int off = 8 * (r >> 2) + (r & 3);
+                    if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float x0 = s[2 * j], x1 = s[2 * j + 1];
+                if constexpr (E::kScaleInSquare) x0 *= sq_pre, x1 *= sq_pre;
+                const float a0 = __int_as_float(max(__float_as_int(x0), 0));
+                const float a1 = __int_as_float(max(__float_as_int(x1), 0));
+                pk[j] = E::pack(a0 * fmaf(t[2 * j], zinv, nd), a1 * fmaf(t[2 * j + 1], zinv, nd));
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -335,7 +398,7 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
     // bytes per lane and store 2 whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
     uint16_t* __restrict__ dQ = reinterpret_cast<uint16_t*>(p.dq) + base;
-    const float f = E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
+    const float f = PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     {
@@ -371,10 +434,11 @@ void born_bwd16_dq_d256_kernel(BwdArgs p) {
 // into a dV and a dK workgroup (each fits the AGPRs, but S is formed twice:
 // five contractions per pair instead of four) measured 15% slower for the
 // step (B16 H4 T2048 D256: 529 against 623 TFLOP/s).
-template <class E, int MODE, bool PAD = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
+void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
     constexpr int DP = 256, NW = BwdD256Cfg::NW, BQ = 64, NST = 2, BK = BwdD256Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -411,8 +475,18 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     const int CG = D / 8;
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = sc < 0.f ? 0x80008000u : 0u;
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;
     const float sq_pre = (E::kScaleInSquare && sc != 0.f) ? 2.f * fabsf(sc) : 1.f;
+    float pg = 0.f, pgt = 0.f, ptau = 0.f, p4g = 0.f, p2e = 0.f, pe = 0.f;
+    if constexpr (PUR) {
+        ptau = p.tau[p.per_head_tau ? h : 0];
+        pg = sc;
+        pgt = -sc * ptau;
+        p4g = 4.f * sc;
+        p2e = 2.f * p.eps_base;
+        pe = p.eps_base;
+    }
+    float dg_acc = 0.f, dt_acc = 0.f;  // purified: sum u^3 dP (r - tau), sum u^3 dP
 
     // Stationary operands: sign-flipped K and V rows of this lane's key.
     u32x4 kr[KS], vr[KS];
@@ -476,7 +550,7 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     // Operand reads (rows: A of S and dPz; transposed: A of dV^T, dK^T)
     // through the ring's lane offsets (current stage); which = 0 (Q) or 1 (dO).
     RingOffs512 ro(lane);
-    constexpr int LEAD = BwdD256Cfg::LEAD;
+    constexpr int LEAD = PUR ? 2 : BwdD256Cfg::LEAD;  // purified: more registers in the elementwise pass
 
     f32x16 acc_v[DB], acc_k[DB];
 #pragma unroll
@@ -516,7 +590,7 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
         }
         __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (decltype(m)::value == kMasked) {
+        if constexpr (!PUR && decltype(m)::value == kMasked) {
             // Register r (query qbase + off) is masked before the lane's key
             // (off + lim < 0) and (window) past its window (off + lim >= W).
             const int lim = qbase - key;
@@ -527,6 +601,39 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
             }
         }
         uint32_t w2[8], u2[8];
+        if constexpr (PUR) {
+            // Masked pairs (query before the lane's key, or past its window)
+            // weigh zero; queries past T have 1/Z = 0 from the workspace read.
+            const int lim = qbase - key;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    float ww[2], uv[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 4 * i + k + e;
+                        const float x = s[r];
+                        float uu = __int_as_float(max(__float_as_int(fmaf(x, pg, pgt)), 0));
+                        float bb = __int_as_float(max(__float_as_int(x), 0));
+                        if constexpr (decltype(m)::value == kMasked) {
+                            const int off = 8 * (r >> 2) + (r & 3);
+                            if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) uu = bb = 0.f;
+                        }
+                        const float u2_ = uu * uu;
+                        const float dpz = dp[r] * z4[k + e];
+                        const float a = u2_ * uu * dpz;
+                        dg_acc = fmaf(a, x - ptau, dg_acc);
+                        dt_acc += a;
+                        ww[e] = fmaf(u2_, u2_, pe * bb * bb) * z4[k + e];
+                        uv[e] = fmaf(p4g, u2_ * uu, p2e * bb) * dpz;
+                    }
+                    w2[(4 * i + k) >> 1] = E::pack(ww[0], ww[1]);
+                    u2[(4 * i + k) >> 1] = E::pack(uv[0], uv[1]);
+                }
+            }
+        } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
@@ -541,6 +648,7 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
                 w2[r >> 1] = E::pack(t0 * a0, t1 * a1);
                 u2[r >> 1] = E::pack(t0 * dp[r], t1 * dp[r + 1]);
             }
+        }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -602,6 +710,27 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
     // XOR-swizzled by r & 15), then read back 16 bytes per lane and stored 2
     // whole rows per instruction.
     __syncthreads();  // every wave is done with the ring
+    if constexpr (PUR) {
+        // Workgroup partials of dgamma and dtau in a fixed order (lanes, then
+        // waves), past the output staging; keys past T excluded (their zero
+        // K row still weighs relu(-gamma tau) when tau < 0).
+        float a = key < T ? 4.f * dg_acc : 0.f;
+        float t2 = key < T ? -4.f * sc * dt_acc : 0.f;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            a += __shfl_xor(a, off);
+            t2 += __shfl_xor(t2, off);
+        }
+        float* red = reinterpret_cast<float*>(smem + BK * RB);
+        if (lane == 0) red[wave] = a, red[NW + wave] = t2;
+        __syncthreads();
+        if (tid == 0) {
+            float sa = 0.f, st = 0.f;
+            for (int w = 0; w < NW; ++w) sa += red[w], st += red[NW + w];
+            p.part[bid] = sa;
+            p.part[gridDim.x + bid] = st;
+        }
+    }
     int ln = lane;
     asm volatile("" : "+v"(ln));
     auto put = [&](const f32x16 (&acc)[DB], float f, void* dst) __attribute__((always_inline)) {
@@ -630,8 +759,24 @@ void born_bwd16_dkdv_d256_kernel(BwdArgs p) {
                 __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(out + (size_t)kk * D + chunk * 8));
         }
     };
-    put(acc_k, E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc), p.dk);
-    put(acc_v, E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc, p.dv);
+    put(acc_k, PUR ? 1.f : E::kScaleInSquare ? sc : 2.f * sc * fabsf(sc), p.dk);
+    put(acc_v, PUR ? 1.f : E::kScaleInSquare ? (sc != 0.f ? 0.25f : 0.f) : sc * sc, p.dv);
+}
+
+// The purified backward at 128 < D <= 256 (bf16 or fp16): dQ (and the
+// workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
+// partials (one per dK/dV workgroup).
+template <class E, int MODE, bool PAD>
+hipError_t launch_purified_bwd_d256(const PurArgs& a, hipStream_t st) {
+    using C = BwdD256Cfg;
+    const unsigned BH = (unsigned)(a.B * a.H);
+    const unsigned nq = (unsigned)((a.T + C::BM - 1) / C::BM);
+    const unsigned nk = (unsigned)((a.T + C::BK - 1) / C::BK);
+    hipLaunchKernelGGL((born_bwd16_dq_d256_kernel<E, MODE, PAD, true>), dim3(nq * BH), dim3(C::NW * 64), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((born_bwd16_dkdv_d256_kernel<E, MODE, PAD, true>), dim3(nk * BH), dim3(C::NW * 64), 0, st, a);
+    return hipGetLastError();
 }
 
 // The 128 < D <= 256 backward: dQ (and the workspace), dK/dV, then dscale

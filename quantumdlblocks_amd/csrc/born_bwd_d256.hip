@@ -26,4 +26,26 @@ hipError_t launch_bwd16_wide(const BwdArgs& a, hipStream_t st) {
 template hipError_t launch_bwd16_wide<BF16>(const BwdArgs&, hipStream_t);
 template hipError_t launch_bwd16_wide<F16>(const BwdArgs&, hipStream_t);
 
+namespace {
+
+template <class E, bool PAD>
+hipError_t purified_modes(const PurArgs& a, hipStream_t s) {
+    if (a.window > 0)
+        return a.is_causal ? launch_purified_bwd_d256<E, kWindow, PAD>(a, s)
+                           : launch_purified_bwd_d256<E, kWindowNC, PAD>(a, s);
+    return a.is_causal ? launch_purified_bwd_d256<E, kCausal, PAD>(a, s)
+                       : launch_purified_bwd_d256<E, kDense, PAD>(a, s);
+}
+
+}  // namespace
+
+// Purified-Born dQ and dK/dV, 128 < D <= 256 without document ids (dtype
+// codes as in qdl_flash_born.h: 1 fp16, 2 bf16); the caller reduces the
+// dgamma / dtau partials of the B H ceil(T / 128) dK/dV workgroups.
+hipError_t purified_bwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s) {
+    if (a.D <= 128 || a.D > 256 || a.D % 8 != 0 || a.doc != nullptr) return hipErrorInvalidValue;
+    if (dtype == 1) return a.D == 256 ? purified_modes<F16, false>(a, s) : purified_modes<F16, true>(a, s);
+    return a.D == 256 ? purified_modes<BF16, false>(a, s) : purified_modes<BF16, true>(a, s);
+}
+
 }  // namespace qdl

@@ -20,16 +20,23 @@
 //     diagonal or window edge / fully visible), one loop per run.
 // PAD: 128 < D < 256 (a multiple of 8): the loads of the chunks past D return
 // zeros, Q is zero there, and the output chunks past D are not stored.
+// PUR: the purified-Born weights (flash_born.py:696-811) as in the D == 64 and
+// D == 128 forwards: p = relu(gamma (r - tau))^4 + eps_base relu(r)^2 in
+// fp32, each weight split into bf16 hi + lo terms for P V (fp16 V split
+// exactly into two bf16 terms: pur_pv), Z summed in fp32, O and Z stored in
+// fp32 straight from the accumulators; masks zero the weights, so without
+// causality the keys past T are masked in the last tile too.
 #pragma once
 
 #include "born_bwd_d256.h"
 
 namespace qdl {
 
-template <class E, int MODE, bool PAD = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void born_fwd16_d256_kernel(FwdArgs p) {
+void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     constexpr int DP = 256, NW = 4, BN = 64, NST = 2, BM = 32 * NW;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per row
@@ -65,19 +72,28 @@ void born_fwd16_d256_kernel(FwdArgs p) {
     const int CG = D / 8;
     const size_t base = (size_t)bh * T * D;
     const float sc = p.scale[p.per_head_scale ? h : 0];
-    const uint32_t flip = sc < 0.f ? 0x80008000u : 0u;  // sign of the scale folded into Q
+    const uint32_t flip = (!PUR && sc < 0.f) ? 0x80008000u : 0u;  // sign of the scale folded into Q
     // fp16: the reference's weights relu(s r)^2 (born_weight_pair).
     const float sq_pre = E::kScaleInSquare ? fabsf(sc) : 1.f;
+    // Purified weights: t = gamma r - gamma tau, b' = sqrt(eps_base) relu(r).
+    float pg = 0.f, pgt = 0.f, pse = 0.f;
+    if constexpr (PUR) {
+        pg = sc;
+        pgt = -sc * p.tau[p.per_head_tau ? h : 0];
+        pse = sqrtf(p.eps_base);
+    }
 
     // Key tiles tb .. tb+ntiles-1 (tb: the window's first key tile, else 0).
     const int W = kWin ? p.window : 0;
     const int tb = kWin ? max(0, R - W + 1) / BN : 0;
     const int ntiles = (kCaus ? (min(T, R + BM) + BN - 1) / BN : (T + BN - 1) / BN) - tb;
     // This wave's rows rw .. rw + 31 see keys [rw - W + 1, rw + 31] (causal,
-    // window) and all of them see keys [rw + 32 - W, rw].
+    // window) and all of them see keys [rw + 32 - W, rw]; purified without
+    // causality: keys up to T - 1, so a partial last tile is masked.
     const int rw = R + 32 * wave;
-    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, kCaus ? rw + 31 : kRunsBig,
-                        kWin ? max(0, rw + 32 - W) : 0, kCaus ? rw : kRunsBig);
+    const int vis_hi = kCaus ? rw + 31 : (PUR ? T - 1 : kRunsBig);
+    const int all_hi = kCaus ? rw : (PUR ? T - 1 : kRunsBig);
+    const WaveRuns runs(tb * BN, ntiles, kWin ? max(0, rw - W + 1) : 0, vis_hi, kWin ? max(0, rw + 32 - W) : 0, all_hi);
 
     const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
@@ -157,24 +173,63 @@ void born_fwd16_d256_kernel(FwdArgs p) {
                 if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
             }
         }
-        uint32_t pk[8];
+        constexpr int PW = PUR ? 8 : 1;  // packed low parts of the purified weights
+        uint32_t pk[8], pl[PW];
+        if constexpr (PUR) {
+            // Weights zeroed past the row (causal) or past T (dense), and
+            // before the row's window.
+            const int lim = (kCaus ? qrow : T - 1) - kbase;
+            const int wlo = kWin ? qrow - kbase - W + 1 : 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pk[j] = born_weight_pair<E>(s[2 * j], s[2 * j + 1], sq_pre, zacc[j & 1]);
+            for (int j = 0; j < 8; ++j) {
+                float w[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float x = s[2 * j + e];
+                    const float t = fmaf(x, pg, pgt);
+                    const float uu = __int_as_float(max(__float_as_int(t), 0));
+                    const float bq = __int_as_float(max(__float_as_int(x * pse), 0));
+                    const float u2 = uu * uu;
+                    float pw = fmaf(u2, u2, bq * bq);
+                    if constexpr (decltype(m)::value == kMasked) {
+                        const int r = 2 * j + e, off = 8 * (r >> 2) + (r & 3);
+                        if (off > lim || (kWin && off < wlo)) pw = 0.f;
+                    }
+                    w[e] = pw;
+                }
+                zacc[0] += w[0] + w[1];
+                const uint32_t hi = BF16::pack(w[0], w[1]);
+                pk[j] = hi;
+                pl[j % PW] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pk[j] = born_weight_pair<E>(s[2 * j], s[2 * j + 1], sq_pre, zacc[j & 1]);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const u32x4 bq = {pk[4 * hh], pk[4 * hh + 1], pk[4 * hh + 2], pk[4 * hh + 3]};
 #pragma unroll
-            for (int db = 0; db < DB; ++db) oacc[db] = E::mfma(ro.tr(smem, 1, nb, hh, db), bq, oacc[db]);
+            for (int db = 0; db < DB; ++db) {
+                if constexpr (PUR) {
+                    const u32x4 bl = {pl[4 * hh % PW], pl[(4 * hh + 1) % PW], pl[(4 * hh + 2) % PW],
+                                      pl[(4 * hh + 3) % PW]};
+                    oacc[db] = pur_pv<E>(ro.tr(smem, 1, nb, hh, db), bq, bl, oacc[db]);
+                } else {
+                    oacc[db] = E::mfma(ro.tr(smem, 1, nb, hh, db), bq, oacc[db]);
+                }
+            }
         }
-        // Two transposed reads per operand.
+        // Two transposed reads per operand (purified: two or three MFMAs).
+        constexpr int MPO = PUR ? (std::is_same<E, F16>::value ? 3 : 2) : 1;
         __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 1);
 #pragma unroll
         for (int i = 0; i < 2 * DB - LEAD / 2; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, MPO, 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, LEAD / 2, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, MPO * LEAD / 2, 1);
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -210,6 +265,27 @@ void born_fwd16_d256_kernel(FwdArgs p) {
     // folded into the weights), packed and staged in this wave's own 32 rows
     // of the idle ring (row r at smem + RB r, chunks XOR-swizzled by r & 15),
     // read back 16 bytes per lane and stored 2 whole rows per instruction.
+    if constexpr (PUR) {
+        // O = acc / (Z + eps) and Z + eps, fp32, straight from the
+        // accumulators (lane: one query row, 4 consecutive columns per store;
+        // plain stores, which L2 merges into whole lines).
+        const float zl = zacc[0] + zacc[1];
+        const float zd = zl + __shfl_xor(zl, 32) + p.eps;
+        if (qrow < T) {
+            float* __restrict__ O32 = p.o + base;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 w = {oacc[db][4 * j] / zd, oacc[db][4 * j + 1] / zd, oacc[db][4 * j + 2] / zd,
+                                     oacc[db][4 * j + 3] / zd};
+                    const int col = db * 32 + 8 * j + 4 * g;
+                    if (!PAD || col < D) *reinterpret_cast<f32x4*>(O32 + (size_t)qrow * D + col) = w;
+                }
+            if (g == 0) __builtin_nontemporal_store(zd, p.z + (size_t)bh * T + qrow);
+        }
+        return;
+    }
     __syncthreads();  // every wave is done with the ring
     const float s2 = (sq_pre > 0.f) ? (sc / sq_pre) * (sc / sq_pre) : 0.f;
     const float eps_s = (p.eps == 0.f) ? 0.f : p.eps / s2;
@@ -247,11 +323,11 @@ void born_fwd16_d256_kernel(FwdArgs p) {
 
 // One 128-row block per workgroup, one workgroup per CU (128 KiB of LDS),
 // the longest key ranges first.
-template <class E, int MODE, bool PAD>
-hipError_t launch_fwd16_d256(const FwdArgs& a, hipStream_t st) {
+template <class E, int MODE, bool PAD, bool PUR = false, class A>
+hipError_t launch_fwd16_d256(const A& a, hipStream_t st) {
     const unsigned nmb = (unsigned)((a.T + 127) / 128);
-    hipLaunchKernelGGL((born_fwd16_d256_kernel<E, MODE, PAD>), dim3(nmb * (unsigned)(a.B * a.H)), dim3(256), 0, st,
-                       a);
+    hipLaunchKernelGGL((born_fwd16_d256_kernel<E, MODE, PAD, PUR>), dim3(nmb * (unsigned)(a.B * a.H)), dim3(256), 0,
+                       st, a);
     return hipGetLastError();
 }
 

@@ -26,4 +26,24 @@ hipError_t launch_fwd16_wide(const FwdArgs& a, hipStream_t st) {
 template hipError_t launch_fwd16_wide<BF16>(const FwdArgs&, hipStream_t);
 template hipError_t launch_fwd16_wide<F16>(const FwdArgs&, hipStream_t);
 
+namespace {
+
+template <class E, bool PAD>
+hipError_t purified_modes(const PurArgs& a, hipStream_t s) {
+    if (a.window > 0)
+        return a.is_causal ? launch_fwd16_d256<E, kWindow, PAD, true>(a, s)
+                           : launch_fwd16_d256<E, kWindowNC, PAD, true>(a, s);
+    return a.is_causal ? launch_fwd16_d256<E, kCausal, PAD, true>(a, s) : launch_fwd16_d256<E, kDense, PAD, true>(a, s);
+}
+
+}  // namespace
+
+// Purified-Born forward, 128 < D <= 256 without document ids (dtype codes as
+// in qdl_flash_born.h: 1 fp16, 2 bf16).
+hipError_t purified_fwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s) {
+    if (a.D <= 128 || a.D > 256 || a.D % 8 != 0 || a.doc != nullptr) return hipErrorInvalidValue;
+    if (dtype == 1) return a.D == 256 ? purified_modes<F16, false>(a, s) : purified_modes<F16, true>(a, s);
+    return a.D == 256 ? purified_modes<BF16, false>(a, s) : purified_modes<BF16, true>(a, s);
+}
+
 }  // namespace qdl

@@ -16,6 +16,10 @@ inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <
 // (purified_wide.hip).
 hipError_t purified_wide_fwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 hipError_t purified_wide_bwd_launch(int dtype, const PurArgs& a, hipStream_t s);
+// 128 < D <= 256 without document ids: the wide-row DMA-ring kernels'
+// purified mode (born_fwd_d256.hip, born_bwd_d256.hip).
+hipError_t purified_fwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s);
+hipError_t purified_bwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s);
 
 // The bf16-MFMA kernels address one (batch, head) slice with 32-bit buffer
 // offsets (rows up to T + 256 of 2 D bytes); longer slices take the generic
@@ -42,6 +46,10 @@ inline bool purified_d128_ok(const PurArgs& a) {
 // D == 128 with document ids: the D = 128 kernels' document mode.
 inline bool purified_d128_doc_ok(const PurArgs& a) {
     return a.D == 128 && purified_window_ok(a) && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+}
+
+inline bool purified_d256_ok(const PurArgs& a) {
+    return a.D > 128 && a.D <= 256 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 inline bool purified_doc_fast_ok(const PurArgs& a) {
@@ -99,6 +107,7 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
         return a.window > 0 ? launch_purified_fwd_doc<true, E>(a, s) : launch_purified_fwd_doc<false, E>(a, s);
     // Above D = 128, and documents at other head dims: the generic
     // 16-bit-MFMA kernels' purified mode.
+    if (k16 && purified_d256_ok(a)) return purified_fwd_d256_launch(E::kDtype, a, s);
     if (k16 && (a.D > 128 || a.doc != nullptr)) return purified_wide_fwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {
         case 32: return launch_purified_fwd<IN, 32>(a, s);
@@ -177,6 +186,15 @@ static hipError_t purified_bwd_dispatch(const PurArgs& a, hipStream_t s) {
         if (a.window > 0) return purified_bwd_fast<kWindow, true, false, E>(a, s);
         return a.is_causal ? purified_bwd_fast<kCausal, true, false, E>(a, s)
                            : purified_bwd_fast<kDense, true, false, E>(a, s);
+    }
+    if (k16 && purified_d256_ok(a)) {
+        hipError_t e = purified_bwd_d256_launch(E::kDtype, a, s);
+        if (e != hipSuccess) return e;
+        const int nwg = ((a.T + 127) / 128) * a.B * a.H;
+        const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
+        hipLaunchKernelGGL(purified_param_reduce_kernel<0>, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg,
+                           n_scale);
+        return hipGetLastError();
     }
     if (k16 && (a.D > 128 || a.doc != nullptr)) return purified_wide_bwd_launch(E::kDtype, a, s);
     switch (purified_padded_dim(a.D)) {

@@ -151,13 +151,14 @@ WIDE_MODES = ["causal", "dense", "window", "window_nc", "docs"]
 @pytest.mark.parametrize("D", [136, 160, 192, 224, 256])
 @pytest.mark.parametrize("mode", WIDE_MODES)
 def test_purified_wide_head_dims(cuda_device, dtype, D, mode):
-    """16-bit purified attention above head dim 128 on the generic
-    16-bit-MFMA kernels' purified mode (padded head dims 160-256, masks as
-    runtime flags; the 192-256 dK/dV split in two column halves, of which the
-    first writes the dgamma / dtau partials): forward (fp32 output, split
-    weights) and Z against the oracle to 1e-4, gradients, dgamma and dtau to
-    the 16-bit bars; tau < 0, per-head gamma and tau, T not a multiple of the
-    tiles."""
+    """16-bit purified attention above head dim 128: without documents the
+    wide-row DMA-ring kernels' purified mode (born_fwd_d256.h,
+    born_bwd_d256.h; D < 256 with zero columns), with documents the generic
+    16-bit-MFMA kernels' purified mode (masks as runtime flags; the 192-256
+    dK/dV split in two column halves, of which the first writes the dgamma /
+    dtau partials): forward (fp32 output, split weights) and Z against the
+    oracle to 1e-4, gradients, dgamma and dtau to the 16-bit bars; tau < 0,
+    per-head gamma and tau, T not a multiple of the tiles."""
     B, H, T = 1, 2, 300
     print(f"purified wide D{D} {dtype} {mode}", flush=True)
     q, k, v, do = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 7, std=0.15, n=4, dtype=dtype))
@@ -172,6 +173,28 @@ def test_purified_wide_head_dims(cuda_device, dtype, D, mode):
     assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
     assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
     _check_pur((B, H, T, D, dtype, dict(is_causal=causal, window_size=window), scale, tau, 0.15), cuda_device, doc)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [200, 256])
+@pytest.mark.parametrize("kw", [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=200),
+                                dict(is_causal=False, window_size=129)],
+                         ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
+def test_purified_wide_dma_kernels_long(cuda_device, dtype, D, kw):
+    """The wide-row kernels' purified mode over several 128-row blocks and
+    64-key tiles (T = 700: a partial last tile and block), causal, dense and
+    windows with and without causality; per-head gamma and tau (one tau < 0),
+    forward against the oracle to 1e-4, gradients, dgamma and dtau."""
+    B, H, T = 1, 2, 700
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 11, std=0.15, dtype=dtype))
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    causal, window = kw["is_causal"], kw.get("window_size", 0)
+    o32, z32 = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8, window=window)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, causal,
+                                        1e-8, window, None)
+    assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
+    assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
+    _check_pur((B, H, T, D, dtype, kw, scale, tau, 0.15), cuda_device)
 
 
 @pytest.mark.parametrize("D", [64, 128])
