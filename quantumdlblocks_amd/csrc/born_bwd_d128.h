@@ -509,14 +509,18 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     }
 }
 
-template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// NW (documents only): 2 waves over 64-key blocks and a two-stage ring, so
+// that two workgroups share a CU (still one wave per SIMD) and one's
+// start-up overlaps the other's tiles; otherwise 4 waves over 128 keys.
+template <class E, int MODE, bool PUR = false, bool PAD = false, bool DOC = false, int NW = BwdD128Cfg::NWK>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
+    static_assert(NW == 4 || (NW == 2 && DOC), "64-key blocks: the document mode");
 
-    constexpr int DP = 128, NW = BwdD128Cfg::NWK, BQ = 64, NST = 3, BK = BwdD128Cfg::BK;
+    constexpr int DP = 128, BQ = 64, NST = NW == 4 ? 3 : 2, BK = 32 * NW;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
@@ -524,7 +528,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     // Bytes per stage: Q, dO, -delta, 1/Z (documents: and the query document ids).
     constexpr int SB = 2 * TB + (DOC ? 3 : 2) * BQ * 4;
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
-    constexpr int CAP = 256;               // documents: candidate tiles screened per pass
+    constexpr int CAP = 64 * NW;           // documents: candidate tiles screened per pass (one per thread)
     static_assert(TB % (1024 * NW) == 0 && BQ * 4 == 256 && BK * RB <= NST * SB && BK == 32 * NW,
                   "tile split / staging");
     constexpr bool kWin = mode_window(MODE);
@@ -607,9 +611,10 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
     const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
 
-    // Tile u (documents: kept tile u of the list) -> stage u % NST.  Waves 0
-    // and 1 also bring the tile's -delta and 1/Z, wave 2 (documents) its
-    // query document ids (lanes 0-15, 16 bytes each): one more load per tile.
+    // Tile u (documents: kept tile u of the list) -> stage u % NST.  The
+    // tile's -delta, 1/Z and (documents) query document ids (rows 0, 1, 2 of
+    // 64 values after the Q and dO tiles) come in one load each (lanes 0-15,
+    // 16 bytes each), row r from wave r % NW.
     constexpr int kRowLoaders = DOC ? 3 : 2;
     auto issue = [&](int u) __attribute__((always_inline)) {
         uint8_t* sb = smem + (u % NST) * SB;
@@ -625,13 +630,11 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             dma_load16(rd, lds_addr(sb + TB + (wave * LPW + i) * 1024), off);
         }
         if (lane < 16) {
-            const uint32_t la = lds_addr(sb + 2 * TB + wave * BQ * 4);
-            if (wave == 0)
-                dma_load16(rdl, la, (i0 + 4 * lane) * 4);
-            else if (wave == 1)
-                dma_load16(rzi, la, (i0 + 4 * lane) * 4);
-            else if (DOC && wave == 2)
-                dma_load16(rdoc, la, (i0 + 4 * lane) * 4);
+#pragma unroll
+            for (int r = 0; r < kRowLoaders; ++r)
+                if (wave == r % NW)
+                    dma_load16(r == 0 ? rdl : r == 1 ? rzi : rdoc, lds_addr(sb + 2 * TB + r * BQ * 4),
+                               (i0 + 4 * lane) * 4);
         }
     };
 
@@ -932,10 +935,12 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
             const int n = screen_doc_tiles<BQ>(docb, T, q_lo, c0, min(CAP, ntiles - c0), bk_lo, bk_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
+            // Tiles 0 .. NST-2 up front, tile u+NST-1 after the barrier of
+            // step u (into the stage of tile u-1).
             if (n > 0) issue(0);
-            if (n > 1) issue(1);
+            if (NST == 3 && n > 1) issue(1);
             for (int u = 0; u < n; ++u) {
-                if (u + 1 < n) {
+                if (NST == 3 && u + 1 < n) {
                     if (wave < kRowLoaders)
                         wait_vmcnt<2 * LPW + 1>();
                     else
@@ -944,7 +949,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     wait_vmcnt<0>();
                 }
                 __syncthreads();
-                if (u + 2 < n) issue(u + 2);
+                if (u + NST - 1 < n) issue(u + NST - 1);
                 int soff = (u % NST) * SB;
                 asm volatile("" : "+s"(soff));
                 const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
@@ -1065,14 +1070,16 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
     // dQ: 256-row blocks of 8 waves, 128-row blocks of 4 with documents (one
     // dscale partial per workgroup either way).
     constexpr int NWQ = DOC ? 4 : BwdD128Cfg::NW, BMQ = 32 * NWQ;
+    // dK/dV: 128-key blocks of 4 waves, 64-key blocks of 2 with documents.
+    constexpr int NWK = DOC ? 2 : BwdD128Cfg::NWK, BKK = 32 * NWK;
     const unsigned nq = (unsigned)((a.T + BMQ - 1) / BMQ);
-    const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
+    const unsigned nk = (unsigned)((a.T + BKK - 1) / BKK);
     hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, false, PAD, DOC, NWQ>), dim3(nq * BH), dim3(NWQ * 64), 0,
                        st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD, DOC>), dim3(nk * BH),
-                       dim3(BwdD128Cfg::NWK * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, false, PAD, DOC, NWK>), dim3(nk * BH), dim3(NWK * 64), 0,
+                       st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
                        st, a, (int)(nq * BH));
@@ -1081,19 +1088,20 @@ hipError_t launch_bwd16_d128(const BwdArgs& a, hipStream_t st) {
 
 // The purified D == 128 backward (bf16 or fp16): dQ (and the workspace),
 // dK/dV (and the dgamma / dtau partials); the caller reduces the partials (one
-// per dK/dV workgroup).
+// per dK/dV workgroup: B H ceil(T / 128), with documents B H ceil(T / 64)).
 template <int MODE, bool PAD = false, bool DOC = false, class E = BF16>
 hipError_t launch_purified_bwd_d128(const PurArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     constexpr int NWQ = DOC ? 4 : BwdD128Cfg::NW, BMQ = 32 * NWQ;
+    constexpr int NWK = DOC ? 2 : BwdD128Cfg::NWK, BKK = 32 * NWK;
     const unsigned nq = (unsigned)((a.T + BMQ - 1) / BMQ);
-    const unsigned nk = (unsigned)((a.T + BwdD128Cfg::BK - 1) / BwdD128Cfg::BK);
+    const unsigned nk = (unsigned)((a.T + BKK - 1) / BKK);
     hipLaunchKernelGGL((born_bwd16_dq_d128_kernel<E, MODE, true, PAD, DOC, NWQ>), dim3(nq * BH), dim3(NWQ * 64), 0,
                        st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, true, PAD, DOC>), dim3(nk * BH),
-                       dim3(BwdD128Cfg::NWK * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d128_kernel<E, MODE, true, PAD, DOC, NWK>), dim3(nk * BH), dim3(NWK * 64), 0,
+                       st, a);
     return hipGetLastError();
 }
 

@@ -771,6 +771,13 @@ inline int purified_dkdv_groups(int B, int H, int T, int DP) {
     return ((T + BK - 1) / BK) * B * H;
 }
 
+// Partial-sum slots the workspace holds for head dim DP: the most any dK/dV
+// launch at that head dim writes (D = 128 with documents: 64-key blocks).
+inline int purified_dkdv_groups_max(int B, int H, int T, int DP) {
+    const int g = purified_dkdv_groups(B, H, T, DP);
+    return DP == 128 ? max(g, ((T + 63) / 64) * B * H) : g;
+}
+
 template <class IN, int DP>
 hipError_t launch_purified_fwd(const PurArgs& a, hipStream_t st) {
     using C = PurCfg<DP>;

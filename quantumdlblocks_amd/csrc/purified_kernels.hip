@@ -11,9 +11,8 @@ namespace qdl {
 
 inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
-// 16-bit inputs above head dim 128, and with document ids at head dims other
-// than 64 and 128: the generic 16-bit-MFMA kernels' purified mode
-// (purified_wide.hip).
+// 16-bit inputs with document ids at head dims other than 64 and 128: the
+// generic 16-bit-MFMA kernels' purified mode (purified_wide.hip).
 hipError_t purified_wide_fwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 hipError_t purified_wide_bwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 // 128 < D <= 256 without document ids: the wide-row DMA-ring kernels'
@@ -145,7 +144,8 @@ static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
                    : a.D == 128 ? launch_purified_bwd_d128<MODE, false, false, E>(a, s)
                                 : launch_purified_bwd_d128<MODE, true, false, E>(a, s);
     if (e != hipSuccess) return e;
-    const int nwg = purified_dkdv_groups(a.B, a.H, a.T, 128);
+    // dK/dV workgroups: 128-key blocks, 64-key blocks with documents.
+    const int nwg = DOC ? ((a.T + 63) / 64) * a.B * a.H : purified_dkdv_groups(a.B, a.H, a.T, 128);
     const int n_scale = a.per_head_scale ? a.H : 1, n_tau = a.per_head_tau ? a.H : 1;
     hipLaunchKernelGGL(purified_param_reduce_kernel<0>, dim3((unsigned)(n_scale + n_tau)), dim3(256), 0, s, a, nwg, n_scale);
     return hipGetLastError();
@@ -218,7 +218,7 @@ hipError_t purified_bwd_launch(int dtype, const PurArgs& a, hipStream_t s) {
 }
 int64_t purified_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
     const int64_t region = (B * H * T * 4 + 255) / 256 * 256;
-    const int64_t nwg = purified_dkdv_groups((int)B, (int)H, (int)T, purified_padded_dim((int)D));
+    const int64_t nwg = purified_dkdv_groups_max((int)B, (int)H, (int)T, purified_padded_dim((int)D));
     return 2 * region + (2 * nwg * 4 + 255) / 256 * 256;
 }
 
