@@ -1204,8 +1204,8 @@ hipError_t launch_bwd_common_pre(const BwdArgs& a, hipStream_t st) {
 // dscale reduction (defined in born_bwd_common.hip).
 hipError_t launch_bwd_common_post(const BwdArgs& a, hipStream_t st);
 
-// 128 < D <= 256 without document ids, 16-bit inputs: the DMA-ring kernels of
-// born_bwd_d256.h (instantiated in born_bwd_d256.hip).
+// 128 < D <= 256 (documents with a causal window or none), 16-bit inputs:
+// the DMA-ring kernels of born_bwd_d256.h (instantiated in born_bwd_d256.hip).
 template <class E>
 hipError_t launch_bwd16_wide(const BwdArgs& a, hipStream_t st);
 
@@ -1279,9 +1279,11 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
         }
     }
     // 128 < D <= 256, dense, causal or a sliding window with or without
-    // causality (no documents): the DMA-ring kernels for wide rows.
+    // causality (documents: with a causal window or none): the DMA-ring
+    // kernels for wide rows.
     if constexpr (DP > 128) {
-        if (a.D > 128 && a.doc == nullptr && addr32) return launch_bwd16_wide<E>(a, st);
+        if (a.D > 128 && addr32 && (a.doc == nullptr || a.window == 0 || a.is_causal))
+            return launch_bwd16_wide<E>(a, st);
     }
     if constexpr (DP == 96 || DP == 128) {
         if (a.D > 64 && a.D < 128 && a.doc == nullptr && addr32) {

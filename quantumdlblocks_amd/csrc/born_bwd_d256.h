@@ -31,6 +31,13 @@
 // rounded to the input dtype before their contractions, O read in fp32, and
 // the dK/dV workgroups writing their partial sums of dgamma and dtau (reduced
 // per output afterwards in a fixed order).
+// DOC: document ids (with or without a causal window) as in the D == 128
+// kernels' document mode: each block screens its candidate tiles (key tiles
+// for dQ, query tiles for dK/dV) by document-id range into a list in LDS,
+// loads each kept tile's 64 ids with it, skips a tile per wave that lies on
+// the invisible side of its diagonal or window or is one document none of
+// its rows (keys) belongs to, and tests the rest per element unless document
+// and diagonal allow none.
 #pragma once
 
 #include "born_bwd_d128.h"
@@ -101,11 +108,12 @@ struct RingOffs512 {
     static constexpr int RB_ = 512;
 };
 
-template <class E, int MODE, bool PAD = false, bool PUR = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     constexpr int DP = 256, NW = BwdD256Cfg::NW, BN = 64, NST = 2, BM = BwdD256Cfg::BM;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
@@ -120,6 +128,12 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // V tile right after it), the output staging afterwards.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
     __shared__ float s_dz[NW];
+    // Documents: key document ids per stage, the kept-tile list and screening scratch.
+    constexpr int CAP = 64 * NW;  // candidate tiles screened per pass (one per thread)
+    constexpr int KDW = BN / NW;  // key ids loaded per wave per tile
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[DOC ? 2 * NW + 1 : 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -238,12 +252,18 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     const uint32_t nrec = (uint32_t)T * (uint32_t)(2 * D);
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
 
-    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
-    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    // Tile u (documents: kept tile u of the list) -> stage u % NST:
+    // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane, slot =
+    // row * CPR + chunk'; documents: also this wave's KDW of the tile's key
+    // ids (lanes 0 .. KDW/4 - 1, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         const int st = u % NST;
-        const int key0 = (tb + u) * BN;
+        int key0 = (tb + u) * BN;
+        if constexpr (DOC) key0 = (tb + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne)) * BN;
         uint8_t* kb = smem + st * 2 * TB;
         uint8_t* vb = kb + TB;
 #pragma unroll
@@ -255,6 +275,9 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
         }
+        if constexpr (DOC)
+            if (lane < KDW / 4)
+                dma_load16(rdoc, lds_addr(kd_lds + st * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
 
     // Operand reads (rows: A operands of S^T, T^T; K^T, transposed: A of
@@ -271,9 +294,15 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         asm volatile("" : "+a"(acc[db]));
     }
 
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the row's document id (INT_MIN past T); per tile, whether
+    // this wave tests it per element (dmw) and the stage's key ids (kdp).
+    const int qdoc = (DOC && qrow < T) ? docb[qrow] : INT_MIN;
+    bool dmw = true;
+    const int32_t* kdp = kd_lds;
     // One 32-key half nb of a tile:
     //   S^T = K Q^T, T^T = V dO^T      (A = K, V rows; B = Q^T, dO^T)
     //   U = relu(S^T) (T^T / Z - delta / Z), masked keys zeroed
@@ -301,6 +330,23 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             // here: their K rows (zero) multiply U.
             const int lim = qrow - kbase;
             const int wlo = kWin ? lim - W + 1 : 0;
+            // Documents: bit r set for a register masked by the diagonal
+            // (causal), the window or another document.
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int dlim = kCaus ? lim : INT_MAX;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > dlim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc)
+                                dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 float w[2];
@@ -316,11 +362,29 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                         const int off = 8 * (r >> 2) + (r & 3);
                         if ((kCaus && off > lim) || (kWin && off < wlo)) d = 0.f;
                     }
+                    if constexpr (decltype(m)::value == kDocm)
+                        if ((dmask >> r) & 1u) d = 0.f;
                     w[e] = d;
                 }
                 pk[j] = E::pack(w[0], w[1]);
             }
         } else {
+            if constexpr (decltype(m)::value == kDocm) {
+                // Masked past the lane's row (causal), before its window or
+                // in another document.
+                if (dmw) {
+                    const int lim = kCaus ? qrow - kbase : INT_MAX;
+                    const int wlo = kWin ? lim - W + 1 : 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                    }
+                }
+            }
             if constexpr (decltype(m)::value == kMasked) {
                 // Key kbase + 8 (r / 4) + r % 4 of register r: masked past
                 // the lane's row, and (window) before its first key.
@@ -364,16 +428,17 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     // step u, once tile u has landed (each wave waits for its own share) and
     // the barrier has made it visible and freed tile u-1's stage, tile u+1
     // goes out into that stage.
-    issue(0);
+    if constexpr (!DOC) issue(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]), "+v"(dr[ks]));
     asm volatile("" : "+v"(zinv), "+v"(nd));
     int u = 0;
-    auto step = [&]() __attribute__((always_inline)) {
+    auto step_n = [&](int n) __attribute__((always_inline)) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (u + 1 < ntiles) issue(u + 1);
+        if (u + 1 < n) issue(u + 1);
     };
+    auto step = [&]() __attribute__((always_inline)) { step_n(ntiles); };
     auto run = [&](int tend, auto m) __attribute__((always_inline)) {
         for (; u < tend; ++u) {
             step();
@@ -383,6 +448,58 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             ro.flip();
         }
     };
+    if constexpr (DOC) {
+        // Document range of this wave's valid rows (uniform; wone: one
+        // document) and of the whole block.
+        int wlo = qrow < T ? qdoc : INT_MAX, whi = qrow < T ? qdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            wlo = min(wlo, __shfl_xor(wlo, off));
+            whi = max(whi, __shfl_xor(whi, off));
+        }
+        wlo = __builtin_amdgcn_readfirstlane(wlo);
+        whi = __builtin_amdgcn_readfirstlane(whi);
+        const bool wone = wlo == whi;
+        if (lane == 0) {
+            s_rng[2 * wave] = wlo;
+            s_rng[2 * wave + 1] = whi;
+        }
+        __syncthreads();
+        int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_rng[2 * w]);
+            bq_hi = max(bq_hi, s_rng[2 * w + 1]);
+        }
+        // The kept tiles of each chunk of candidates through the ring.  Per
+        // tile and wave: nothing to do when the tile lies past the wave's
+        // rows (or before their windows) or is one document none of them
+        // belongs to; no per-element test when it is before the wave's first
+        // row and one document that all of them belong to.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            for (u = 0; u < n; ++u) {
+                step_n(n);
+                kdp = kd_lds + (u % NST) * BN;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int key0 = (tb + (e & ~kDocOne)) * BN;
+                const bool one = (e & kDocOne) != 0;
+                const bool vis = !(kCaus && key0 > rw + 31) && !(kWin && key0 + BN - 1 < rw - W + 1) &&
+                                 !(one && (td < wlo || td > whi));
+                dmw = (kCaus && key0 + BN - 1 > rw) || (kWin && key0 < rw + 32 - W) || !(one && wone && td == wlo);
+                if (vis) {
+                    half(0, key0 + 4 * g, Docm{});
+                    half(1, key0 + 32 + 4 * g, Docm{});
+                }
+                ro.flip();
+            }
+            if (n & 1) ro.flip();  // the next chunk starts on stage 0
+            __syncthreads();       // the list and the ring are reused by the next chunk (or the output)
+        }
+    } else {
     // (ro follows the stage of tile u: flipped after every tile, idle or not.)
     for (; u < runs.ta; ++u) {
         step();
@@ -392,6 +509,7 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
+    }
 
     // Epilogue: scale, pack, stage this wave's rows in the idle ring (row r
     // at smem + RB r, chunks XOR-swizzled by r & 15), read them back 16
@@ -434,25 +552,31 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
 // into a dV and a dK workgroup (each fits the AGPRs, but S is formed twice:
 // five contractions per pair instead of four) measured 15% slower for the
 // step (B16 H4 T2048 D256: 529 against 623 TFLOP/s).
-template <class E, int MODE, bool PAD = false, bool PUR = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified gradients: 16-bit");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     constexpr int DP = 256, NW = BwdD256Cfg::NW, BQ = 64, NST = 2, BK = BwdD256Cfg::BK;
     constexpr int KS = DP / 16, DB = DP / 32;
     constexpr int RB = DP * 2;             // bytes per tile row
     constexpr int CPR = RB / 16;           // 16-byte chunks per row
     constexpr int TB = BQ * RB;            // bytes per Q or dO tile
-    constexpr int RW = 2 * BQ * 4;         // -delta and 1/Z rows of a stage
+    constexpr int NROWS = DOC ? 3 : 2;     // -delta, 1/Z (documents: and the query ids)
+    constexpr int RW = NROWS * BQ * 4;     // those rows of a stage
     constexpr int LPW = TB / (1024 * NW);  // 1-KiB loads per wave per tile (each of Q, dO)
     constexpr bool kWin = mode_window(MODE);
     constexpr bool kCaus = mode_causal(MODE);
     static_assert(2 * TB == 0x10000 && BK * RB <= 2 * NST * TB, "stages 64 KiB apart / staging");
 
-    // Stage st: Q and dO tiles at 2 TB st; -delta and 1/Z rows at
-    // 2 NST TB + RW st.  Afterwards the output staging.
+    // Stage st: Q and dO tiles at 2 TB st; -delta, 1/Z (and the query
+    // document ids) at 2 NST TB + RW st.  Afterwards the output staging.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB + NST * RW];
+    // Documents: the kept-tile list and screening scratch.
+    constexpr int CAP = 64 * NW;  // candidate tiles screened per pass (one per thread)
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[DOC ? 2 * NW + 1 : 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -522,13 +646,18 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     const i32x4 rd = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.dout) + base, nrec);
     const i32x4 rdl = buffer_rsrc(p.ndelta + (size_t)bh * T, (uint32_t)T * 4u);
     const i32x4 rzi = buffer_rsrc(p.zinv + (size_t)bh * T, (uint32_t)T * 4u);
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
 
-    // Tile u -> stage u % NST (Q and dO tiles at 2 TB st, -delta and 1/Z
-    // rows at 2 NST TB + RW st).  Waves 0 and 1 also bring the tile's -delta
-    // and 1/Z (lanes 0-15, 16 bytes each).
+    // Tile u (documents: kept tile u of the list) -> stage u % NST (Q and dO
+    // tiles at 2 TB st, the rows at 2 NST TB + RW st).  Row r of the tile's
+    // -delta, 1/Z and (documents) query ids comes from wave r (lanes 0-15, 16
+    // bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
         uint8_t* sb = smem + (u % NST) * 2 * TB;
-        const int i0 = q_lo + u * BQ;
+        int i0 = q_lo + u * BQ;
+        if constexpr (DOC) i0 = q_lo + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne) * BQ;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
             const int slot = (wave * LPW + i) * 64 + lane;
@@ -544,6 +673,8 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                 dma_load16(rdl, la, (i0 + 4 * lane) * 4);
             else if (wave == 1)
                 dma_load16(rzi, la, (i0 + 4 * lane) * 4);
+            else if (DOC && wave == 2)
+                dma_load16(rdoc, la, (i0 + 4 * lane) * 4);
         }
     };
 
@@ -556,9 +687,14 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc_v[db] = zero16(), acc_k[db] = zero16();
 
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the lane's key document id (INT_MIN past T); per tile,
+    // whether this wave tests it per element.
+    const int kdoc = (DOC && key < T) ? docb[key] : INT_MIN;
+    bool dmw = true;
     // Per 32-query half nb of a tile (queries i0 + nb * 32 + 8 (r / 4) +
     // 4 g + r % 4 for register r; one key per lane):
     //   S   = Q K'^T                  (A = Q rows)
@@ -590,6 +726,22 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         }
         __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!PUR && decltype(m)::value == kDocm) {
+            // Masked before the lane's key (causal), past its window or in
+            // another document.
+            if (dmw) {
+                const int lim = kCaus ? qbase - key : INT_MAX / 2;
+                const int32_t* qd = reinterpret_cast<const int32_t*>(rw + 2 * BQ * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int4 d4 = *reinterpret_cast<const int4*>(qd + nb * 32 + 8 * i + 4 * g);
+                    const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                }
+            }
+        }
         if constexpr (!PUR && decltype(m)::value == kMasked) {
             // Register r (query qbase + off) is masked before the lane's key
             // (off + lim < 0) and (window) past its window (off + lim >= W).
@@ -602,9 +754,26 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         }
         uint32_t w2[8], u2[8];
         if constexpr (PUR) {
-            // Masked pairs (query before the lane's key, or past its window)
-            // weigh zero; queries past T have 1/Z = 0 from the workspace read.
+            // Masked pairs (query before the lane's key, or past its window;
+            // documents: in another document) weigh zero; queries past T
+            // have 1/Z = 0 from the workspace read.
             const int lim = qbase - key;
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int dlim = kCaus ? lim : INT_MAX / 2;
+                    const int32_t* qd = reinterpret_cast<const int32_t*>(rw + 2 * BQ * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(qd + nb * 32 + 8 * i + 4 * g);
+                        const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k + dlim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                                dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const f32x4 z4 = *reinterpret_cast<const f32x4*>(zl + nb * 32 + 8 * i + 4 * g);
@@ -621,6 +790,8 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                             const int off = 8 * (r >> 2) + (r & 3);
                             if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) uu = bb = 0.f;
                         }
+                        if constexpr (decltype(m)::value == kDocm)
+                            if ((dmask >> r) & 1u) uu = bb = 0.f;
                         const float u2_ = uu * uu;
                         const float dpz = dp[r] * z4[k + e];
                         const float a = u2_ * uu * dpz;
@@ -673,15 +844,16 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     };
 
     // Pipeline as in the dQ kernel (two stages).
-    issue(0);
+    if constexpr (!DOC) issue(0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kr[ks]), "+v"(vr[ks]));
     int u = 0;
-    auto step = [&]() __attribute__((always_inline)) {
+    auto step_n = [&](int n) __attribute__((always_inline)) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (u + 1 < ntiles) issue(u + 1);
+        if (u + 1 < n) issue(u + 1);
     };
+    auto step = [&]() __attribute__((always_inline)) { step_n(ntiles); };
     auto run = [&](int tend, auto m) __attribute__((always_inline)) {
         for (; u < tend; ++u) {
             step();
@@ -694,6 +866,61 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             ro.flip();
         }
     };
+    if constexpr (DOC) {
+        // Document range of this wave's valid keys (uniform; kone: one
+        // document) and of the whole block.
+        int klo = key < T ? kdoc : INT_MAX, khi = key < T ? kdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            klo = min(klo, __shfl_xor(klo, off));
+            khi = max(khi, __shfl_xor(khi, off));
+        }
+        klo = __builtin_amdgcn_readfirstlane(klo);
+        khi = __builtin_amdgcn_readfirstlane(khi);
+        const bool kone = klo == khi;
+        if (lane == 0) {
+            s_rng[2 * wave] = klo;
+            s_rng[2 * wave + 1] = khi;
+        }
+        __syncthreads();
+        int bk_lo = INT_MAX, bk_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bk_lo = min(bk_lo, s_rng[2 * w]);
+            bk_hi = max(bk_hi, s_rng[2 * w + 1]);
+        }
+        // The kept query tiles of each chunk of candidates through the ring.
+        // Per tile and wave: nothing to do when the tile ends before the
+        // wave's first key (or starts past its keys' windows) or is one
+        // document none of its keys belongs to; no per-element test when it
+        // starts after the wave's last key and is one document that all of
+        // them belong to.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BQ>(docb, T, q_lo, c0, min(CAP, ntiles - c0), bk_lo, bk_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            for (u = 0; u < n; ++u) {
+                step_n(n);
+                int roff = (u % NST) * RW;
+                asm volatile("" : "+s"(roff));
+                const uint8_t* rw = smem + 2 * NST * TB + roff;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                const int i0 = q_lo + (e & ~kDocOne) * BQ;
+                const bool one = (e & kDocOne) != 0;
+                const bool vis = !(kCaus && i0 + BQ - 1 < kw0) && !(kWin && i0 > kw0 + 31 + W - 1) &&
+                                 !(one && (td < klo || td > khi));
+                dmw = (kCaus && i0 < kw0 + 31) || (kWin && i0 + BQ - 1 >= kw0 + W) || !(one && kone && td == klo);
+                if (vis) {
+                    half(rw, 0, i0 + 4 * g, Docm{});
+                    half(rw, 1, i0 + 32 + 4 * g, Docm{});
+                }
+                ro.flip();
+            }
+            if (n & 1) ro.flip();  // the next chunk starts on stage 0
+            __syncthreads();       // the list and the ring are reused by the next chunk (or the output)
+        }
+    } else {
     // (ro follows the stage of tile u: flipped after every tile, idle or not.)
     for (; u < runs.ta; ++u) {
         step();
@@ -703,6 +930,7 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
+    }
 
     // Epilogue: dK = 2 s|s| / c acc, dV = (s / c)^2 acc (c = sq_pre: 1, or
     // 2|s| for fp16, where the factors are s and 1/4), packed and staged in
@@ -766,31 +994,34 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 // The purified backward at 128 < D <= 256 (bf16 or fp16): dQ (and the
 // workspace), dK/dV (and the dgamma / dtau partials); the caller reduces the
 // partials (one per dK/dV workgroup).
-template <class E, int MODE, bool PAD>
+template <class E, int MODE, bool PAD, bool DOC = false>
 hipError_t launch_purified_bwd_d256(const PurArgs& a, hipStream_t st) {
     using C = BwdD256Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + C::BM - 1) / C::BM);
     const unsigned nk = (unsigned)((a.T + C::BK - 1) / C::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d256_kernel<E, MODE, PAD, true>), dim3(nq * BH), dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d256_kernel<E, MODE, PAD, true, DOC>), dim3(nq * BH), dim3(C::NW * 64), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d256_kernel<E, MODE, PAD, true>), dim3(nk * BH), dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d256_kernel<E, MODE, PAD, true, DOC>), dim3(nk * BH), dim3(C::NW * 64), 0,
+                       st, a);
     return hipGetLastError();
 }
 
 // The 128 < D <= 256 backward: dQ (and the workspace), dK/dV, then dscale
 // from the dQ kernel's per-workgroup sums.
-template <class E, int MODE, bool PAD>
+template <class E, int MODE, bool PAD, bool DOC = false>
 hipError_t launch_bwd16_d256(const BwdArgs& a, hipStream_t st) {
     using C = BwdD256Cfg;
     const unsigned BH = (unsigned)(a.B * a.H);
     const unsigned nq = (unsigned)((a.T + C::BM - 1) / C::BM);
     const unsigned nk = (unsigned)((a.T + C::BK - 1) / C::BK);
-    hipLaunchKernelGGL((born_bwd16_dq_d256_kernel<E, MODE, PAD>), dim3(nq * BH), dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dq_d256_kernel<E, MODE, PAD, false, DOC>), dim3(nq * BH), dim3(C::NW * 64), 0, st,
+                       a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((born_bwd16_dkdv_d256_kernel<E, MODE, PAD>), dim3(nk * BH), dim3(C::NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_bwd16_dkdv_d256_kernel<E, MODE, PAD, false, DOC>), dim3(nk * BH), dim3(C::NW * 64), 0,
+                       st, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(born_bwd_dscale_groups_kernel<0>, dim3((unsigned)(a.per_head_scale ? a.H : 1)), dim3(256), 0,
                        st, a, (int)(nq * BH));

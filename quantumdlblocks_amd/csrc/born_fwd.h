@@ -730,8 +730,8 @@ hipError_t launch_fwd16(const FwdArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// 128 < D <= 256 without document ids, 16-bit inputs: the DMA-ring kernel of
-// born_fwd_d256.h (instantiated in born_fwd_d256.hip).
+// 128 < D <= 256 (documents with a causal window or none), 16-bit inputs:
+// the DMA-ring kernel of born_fwd_d256.h (instantiated in born_fwd_d256.hip).
 template <class E>
 hipError_t launch_fwd16_wide(const FwdArgs& a, hipStream_t st);
 

@@ -26,16 +26,24 @@
 // exactly into two bf16 terms: pur_pv), Z summed in fp32, O and Z stored in
 // fp32 straight from the accumulators; masks zero the weights, so without
 // causality the keys past T are masked in the last tile too.
+// DOC: document ids (with or without a causal window) as in the D == 128
+// kernel's document mode: the block's candidate key tiles screened by
+// document-id range into a list in LDS (screen_doc_tiles), each kept tile
+// loaded with its 64 key ids; per tile a wave skips the work when the tile
+// lies past its rows (or its window) or is one document none of its rows
+// belongs to, and tests it per element unless the tile is before its first
+// row and one document all of its rows belong to.
 #pragma once
 
 #include "born_bwd_d256.h"
 
 namespace qdl {
 
-template <class E, int MODE, bool PAD = false, bool PUR = false>
+template <class E, int MODE, bool PAD = false, bool PUR = false, bool DOC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
+    static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
     constexpr int DP = 256, NW = 4, BN = 64, NST = 2, BM = 32 * NW;
     constexpr int KS = DP / 16, DB = DP / 32;
@@ -51,6 +59,12 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     // Stage st: K tile at 2 TB st, V tile right after it; afterwards the
     // output staging.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * NST * TB];
+    // Documents: key document ids per stage, the kept-tile list and screening scratch.
+    constexpr int CAP = 64 * NW;  // candidate tiles screened per pass (one per thread)
+    constexpr int KDW = BN / NW;  // key ids loaded per wave per tile
+    __shared__ __attribute__((aligned(16))) int32_t kd_lds[DOC ? NST * BN : 1];
+    __shared__ int32_t t_list[DOC ? CAP : 1], t_doc[DOC ? CAP : 1], t_keep[DOC ? CAP : 1], t_tdoc[DOC ? CAP : 1];
+    __shared__ int32_t s_rng[DOC ? 2 * NW + 1 : 1];
 
     const int T = p.T;
     const int BH = p.B * p.H;
@@ -99,10 +113,17 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     const i32x4 rk = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.k) + base, nrec);
     const i32x4 rv = buffer_rsrc(reinterpret_cast<const uint16_t*>(p.v) + base, nrec);
 
-    // Tile u -> stage u % NST: wave-instruction i writes LDS slots
-    // (wave * LPW + i) * 64 + lane, slot = row * CPR + chunk'.
+    const int32_t* __restrict__ docb = nullptr;
+    if constexpr (DOC) docb = p.doc + (size_t)(bh / p.H) * T;
+    const i32x4 rdoc = buffer_rsrc(docb, DOC ? (uint32_t)T * 4u : 0u);
+
+    // Tile u (documents: kept tile u of the list) -> stage u % NST:
+    // wave-instruction i writes LDS slots (wave * LPW + i) * 64 + lane, slot =
+    // row * CPR + chunk'; documents: also this wave's KDW of the tile's key
+    // ids (lanes 0 .. KDW/4 - 1, 16 bytes each).
     auto issue = [&](int u) __attribute__((always_inline)) {
-        const int key0 = (tb + u) * BN;
+        int key0 = (tb + u) * BN;
+        if constexpr (DOC) key0 = (tb + (__builtin_amdgcn_readfirstlane(t_list[u]) & ~kDocOne)) * BN;
         uint8_t* kb = smem + (u % NST) * 2 * TB;
         uint8_t* vb = kb + TB;
 #pragma unroll
@@ -114,14 +135,15 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             dma_load16(rk, lds_addr(kb + (wave * LPW + i) * 1024), off);
             dma_load16(rv, lds_addr(vb + (wave * LPW + i) * 1024), off);
         }
+        if constexpr (DOC)
+            if (lane < KDW / 4)
+                dma_load16(rdoc, lds_addr(kd_lds + (u % NST) * BN + wave * KDW), (key0 + wave * KDW + lane * 4) * 4);
     };
 
-    // Tile 0 goes out before the Q rows are loaded, so the two overlap.
-    issue(0);
     // This lane's Q row chunks 2 ks + g (B operands of S^T), the sign of the
     // scale folded in.
     u32x4 qr[KS];
-    {
+    auto load_q = [&]() __attribute__((always_inline)) {
         const uint16_t* __restrict__ Qg = reinterpret_cast<const uint16_t*>(p.q) + base;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -131,6 +153,12 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
+    };
+    // Tile 0 goes out before the Q rows are loaded, so the two overlap
+    // (documents: after the first screening, below).
+    if constexpr (!DOC) {
+        issue(0);
+        load_q();
     }
 
     // Operand reads through the ring's lane offsets (current stage):
@@ -143,9 +171,16 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     for (int db = 0; db < DB; ++db) oacc[db] = zero16();
     float zacc[2] = {0.f, 0.f};
 
-    constexpr int kFull = 1, kMasked = 2;
+    constexpr int kFull = 1, kMasked = 2, kDocm = 3;
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
+    using Docm = std::integral_constant<int, kDocm>;
+    // Documents: the row's id (INT_MIN past T); per tile, whether this wave
+    // tests it per element (dmw), its first key and the stage's key ids.
+    int qdoc = INT_MIN;
+    bool dmw = true;
+    int dkey0 = 0;
+    const int32_t* kdp = kd_lds;
     // One 32-key half nb of a tile (lane: query c, keys kbase + 8 (r / 4) +
     // r % 4 of register r):
     //   S^T = K Q^T                 (A = K rows, B = Q^T)
@@ -180,6 +215,23 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             // before the row's window.
             const int lim = (kCaus ? qrow : T - 1) - kbase;
             const int wlo = kWin ? qrow - kbase - W + 1 : 0;
+            // Documents: bit r set for a register masked by the diagonal
+            // (causal), T, the window or another document.
+            uint32_t dmask = 0;
+            if constexpr (decltype(m)::value == kDocm) {
+                if (dmw) {
+                    const int32_t* kd = kdp + (kbase - dkey0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kd + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc)
+                                dmask |= 1u << (4 * i + k);
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 float w[2];
@@ -195,6 +247,8 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                         const int r = 2 * j + e, off = 8 * (r >> 2) + (r & 3);
                         if (off > lim || (kWin && off < wlo)) pw = 0.f;
                     }
+                    if constexpr (decltype(m)::value == kDocm)
+                        if ((dmask >> (2 * j + e)) & 1u) pw = 0.f;
                     w[e] = pw;
                 }
                 zacc[0] += w[0] + w[1];
@@ -203,6 +257,23 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                 pl[j % PW] = BF16::pack(w[0] - BF16::lo(hi), w[1] - BF16::hi(hi));
             }
         } else {
+            if constexpr (decltype(m)::value == kDocm) {
+                // Masked past the row (causal), before its window or in
+                // another document.
+                if (dmw) {
+                    const int lim = kCaus ? qrow - kbase : INT_MAX;
+                    const int wlo = kWin ? lim - W + 1 : 0;
+                    const int32_t* kd = kdp + (kbase - dkey0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int4 d4 = *reinterpret_cast<const int4*>(kd + 8 * i);
+                        const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                    }
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) pk[j] = born_weight_pair<E>(s[2 * j], s[2 * j + 1], sq_pre, zacc[j & 1]);
         }
@@ -237,11 +308,12 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     // for its own share) and the barrier has made it visible and freed tile
     // u-1's stage, tile u+1 goes out into that stage.
     int u = 0;
-    auto step = [&]() __attribute__((always_inline)) {
+    auto step_n = [&](int n) __attribute__((always_inline)) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (u + 1 < ntiles) issue(u + 1);
+        if (u + 1 < n) issue(u + 1);
     };
+    auto step = [&]() __attribute__((always_inline)) { step_n(ntiles); };
     auto run = [&](int tend, auto m) __attribute__((always_inline)) {
         for (; u < tend; ++u) {
             step();
@@ -251,6 +323,61 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             ro.flip();
         }
     };
+    if constexpr (DOC) {
+        // The rows' documents first (the screening needs them): this wave's
+        // range of ids (uniform; wone: one document) and the block's.
+        if (qrow < T) qdoc = docb[qrow];
+        int wlo = qrow < T ? qdoc : INT_MAX, whi = qrow < T ? qdoc : INT_MIN;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            wlo = min(wlo, __shfl_xor(wlo, off));
+            whi = max(whi, __shfl_xor(whi, off));
+        }
+        wlo = __builtin_amdgcn_readfirstlane(wlo);
+        whi = __builtin_amdgcn_readfirstlane(whi);
+        const bool wone = wlo == whi;
+        if (lane == 0) {
+            s_rng[2 * wave] = wlo;
+            s_rng[2 * wave + 1] = whi;
+        }
+        __syncthreads();
+        int bq_lo = INT_MAX, bq_hi = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            bq_lo = min(bq_lo, s_rng[2 * w]);
+            bq_hi = max(bq_hi, s_rng[2 * w + 1]);
+        }
+        // The kept tiles of each chunk of candidates through the ring; Q is
+        // loaded after the first chunk's first tile is issued.
+        for (int c0 = 0; c0 < ntiles; c0 += CAP) {
+            const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
+                                               t_list, t_doc, &s_rng[2 * NW]);
+            if (n > 0) issue(0);
+            if (c0 == 0) load_q();
+            for (u = 0; u < n; ++u) {
+                step_n(n);
+                kdp = kd_lds + (u % NST) * BN;
+                const int e = __builtin_amdgcn_readfirstlane(t_list[u]);
+                const int td = __builtin_amdgcn_readfirstlane(t_doc[u]);
+                dkey0 = (tb + (e & ~kDocOne)) * BN;
+                const bool one = (e & kDocOne) != 0;
+                // Window: the tile is past every row's window when it ends
+                // before the first row's, and cut by one when it starts
+                // before the last row's.
+                const bool vis = !(kCaus && dkey0 > rw + 31) && !(kWin && dkey0 + BN - 1 < rw - W + 1) &&
+                                 !(one && (td < wlo || td > whi));
+                dmw = (kCaus && dkey0 + BN - 1 > rw) || (kWin && dkey0 < rw + 32 - W) ||
+                      !(one && wone && td == wlo) || (PUR && dkey0 + BN > T);
+                if (vis) {
+                    half(0, dkey0 + 4 * g, Docm{});
+                    half(1, dkey0 + 32 + 4 * g, Docm{});
+                }
+                ro.flip();
+            }
+            if (n & 1) ro.flip();  // the next chunk starts on stage 0
+            __syncthreads();       // the list and the ring are reused by the next chunk (or the output)
+        }
+    } else {
     // (ro follows the stage of tile u: flipped after every tile, idle or not.)
     for (; u < runs.ta; ++u) {
         step();
@@ -260,6 +387,7 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     run(runs.tg, Full{});
     run(runs.tv, Masked{});
     for (; u < ntiles; ++u) step();
+    }
 
     // Epilogue: Z = s^2 z + eps and O = acc / (z + eps / s^2) (c = sq_pre
     // folded into the weights), packed and staged in this wave's own 32 rows
@@ -323,11 +451,11 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 
 // One 128-row block per workgroup, one workgroup per CU (128 KiB of LDS),
 // the longest key ranges first.
-template <class E, int MODE, bool PAD, bool PUR = false, class A>
+template <class E, int MODE, bool PAD, bool PUR = false, bool DOC = false, class A>
 hipError_t launch_fwd16_d256(const A& a, hipStream_t st) {
     const unsigned nmb = (unsigned)((a.T + 127) / 128);
-    hipLaunchKernelGGL((born_fwd16_d256_kernel<E, MODE, PAD, PUR>), dim3(nmb * (unsigned)(a.B * a.H)), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL((born_fwd16_d256_kernel<E, MODE, PAD, PUR, DOC>), dim3(nmb * (unsigned)(a.B * a.H)), dim3(256),
+                       0, st, a);
     return hipGetLastError();
 }
 

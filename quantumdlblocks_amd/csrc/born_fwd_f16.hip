@@ -37,8 +37,10 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
             return a.is_causal ? launch_fwd16_d128<F16, kWindow>(a, s) : launch_fwd16_d128<F16, kWindowNC>(a, s);
         return a.is_causal ? launch_fwd16_d128<F16, kCausal>(a, s) : launch_fwd16_d128<F16, kDense>(a, s);
     }
-    // 128 < D <= 256 without documents: the DMA-ring kernel for wide rows.
-    if (a.D > 128 && a.doc == nullptr && addr32) return launch_fwd16_wide<F16>(a, s);
+    // 128 < D <= 256 (documents with a causal window or none): the DMA-ring
+    // kernel for wide rows.
+    if (a.D > 128 && addr32 && (a.doc == nullptr || a.window == 0 || a.is_causal))
+        return launch_fwd16_wide<F16>(a, s);
     if (a.D == 64 && mode != kGeneral && addr32)
         return mode == kCausal ? launch_fwd16_fast<F16, 64, kCausal>(a, s) : launch_fwd16_fast<F16, 64, kDense>(a, s);
 #define QDL_MODE_BODY(M) return launch_fwd16<F16, DPV, M>(a, s);

@@ -11,12 +11,13 @@ namespace qdl {
 
 inline int purified_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
-// 16-bit inputs with document ids at head dims other than 64 and 128: the
-// generic 16-bit-MFMA kernels' purified mode (purified_wide.hip).
+// 16-bit inputs with document ids at head dims below 128 other than 64 (or
+// with a window without causality): the generic 16-bit-MFMA kernels'
+// purified mode (purified_wide.hip).
 hipError_t purified_wide_fwd_launch(int dtype, const PurArgs& a, hipStream_t s);
 hipError_t purified_wide_bwd_launch(int dtype, const PurArgs& a, hipStream_t s);
-// 128 < D <= 256 without document ids: the wide-row DMA-ring kernels'
-// purified mode (born_fwd_d256.hip, born_bwd_d256.hip).
+// 128 < D <= 256 (documents with a causal window or none): the wide-row
+// DMA-ring kernels' purified mode (born_fwd_d256.hip, born_bwd_d256.hip).
 hipError_t purified_fwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s);
 hipError_t purified_bwd_d256_launch(int dtype, const PurArgs& a, hipStream_t s);
 
@@ -48,7 +49,8 @@ inline bool purified_d128_doc_ok(const PurArgs& a) {
 }
 
 inline bool purified_d256_ok(const PurArgs& a) {
-    return a.D > 128 && a.D <= 256 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D > 128 && a.D <= 256 && (a.doc == nullptr || purified_window_ok(a)) &&
+           ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 inline bool purified_doc_fast_ok(const PurArgs& a) {

@@ -189,6 +189,27 @@ def test_bwd_wide_dma_kernels(cuda_device, D, dtype, case):
                std=0.5, seed=D + T + window, check_dscale=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [136, 256])
+@pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
+def test_bwd_wide_documents(cuda_device, dtype, D, is_causal, window):
+    """128 < D <= 256 with document ids (dense, causal, causal window) on the
+    wide-row kernels' document mode: the dQ kernel's key-tile and the dK/dV
+    kernel's query-tile screening, per-wave skips and per-element tests;
+    padded and unpadded head dims, per-head scales, dscale."""
+    doc = orc.geometric_doc_ids(2, 700, 90.0, seed=D + window)
+    _check_bwd(2, 2, 700, D, dtype, cuda_device, doc=doc, is_causal=is_causal, window_size=window,
+               scale=[0.3, -0.15], std=0.5, seed=D + 3, check_dscale=True)
+
+
+def test_bwd_wide_documents_many_chunks(cuda_device):
+    """D = 256, sorted documents over more candidate tiles than one screening
+    pass holds (256 key tiles for dQ, 256 query tiles for dK/dV): the ring
+    restarts on its first stage with every chunk."""
+    doc = orc.geometric_doc_ids(1, 17000, 300.0, seed=5)
+    _check_bwd(1, 1, 17000, 256, torch.bfloat16, cuda_device, doc=doc, scale=0.3, std=0.5, seed=17)
+
+
 def test_bwd_head_dim_above_256_takes_the_eager_path(cuda_device):
     """D > 256: autograd through the reference's eager formulation on the GPU
     (flash_born.py:670-690), gradients against the oracle."""

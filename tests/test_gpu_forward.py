@@ -207,6 +207,18 @@ def test_fwd_wide_dma_kernel(cuda_device, D, dtype, case):
                scale=np.array([0.3, -0.15], dtype=np.float32), std=0.5, seed=D + T + window)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [136, 256])
+@pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
+def test_fwd_wide_documents(cuda_device, dtype, D, is_causal, window):
+    """128 < D <= 256 with document ids (dense, causal, causal window) on the
+    wide-row forward's document mode; padded and unpadded head dims,
+    per-head scales; O and Z."""
+    doc = orc.geometric_doc_ids(2, 700, 90.0, seed=D + window)
+    _check_fwd(2, 2, 700, D, dtype, cuda_device, doc=doc, is_causal=is_causal, window_size=window,
+               scale=np.array([0.3, -0.15], dtype=np.float32), std=0.5, seed=D + 5)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("D", [272, 320])
 def test_fwd_head_dims_above_256_take_the_eager_path(cuda_device, D, dtype):

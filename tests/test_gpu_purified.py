@@ -197,6 +197,29 @@ def test_purified_wide_dma_kernels_long(cuda_device, dtype, D, kw):
     _check_pur((B, H, T, D, dtype, kw, scale, tau, 0.15), cuda_device)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [200, 256])
+@pytest.mark.parametrize("kw", [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=120)],
+                         ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
+def test_purified_wide_documents(cuda_device, dtype, D, kw):
+    """The wide-row kernels' purified document mode (weights masked through
+    a per-lane bit mask), T = 700 with documents of mean length 90, tau < 0
+    on one head: forward against the oracle to 1e-4, gradients, dgamma and
+    dtau."""
+    B, H, T = 1, 2, 700
+    doc = orc.geometric_doc_ids(B, T, 90.0, seed=D)
+    doc_t = torch.tensor(doc, dtype=torch.int32, device=cuda_device)
+    q, k, v = (x.to(cuda_device) for x in seeded_inputs((B, H, T, D), seed=D + 13, std=0.15, dtype=dtype))
+    scale, tau = [8.0, 5.0], [-0.05, 0.1]
+    causal, window = kw["is_causal"], kw.get("window_size", 0)
+    o32, z32 = _pur_fwd_abi(q, k, v, scale, tau, 0.05, causal, 1e-8, doc=doc_t, window=window)
+    O_ref, Z_ref = orc.purified_forward(f64(q), f64(k), f64(v), np.asarray(scale), np.asarray(tau), 0.05, causal,
+                                        1e-8, window, doc)
+    assert rel_err(f64(o32), O_ref) <= 1e-4, rel_err(f64(o32), O_ref)
+    assert np.max(np.abs(f64(z32) - Z_ref) / Z_ref) <= 1e-4
+    _check_pur((B, H, T, D, dtype, kw, scale, tau, 0.15), cuda_device, doc)
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("kw", [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=150)],
                          ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
