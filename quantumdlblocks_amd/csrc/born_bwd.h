@@ -1285,6 +1285,15 @@ hipError_t launch_bwd16(const BwdArgs& a, hipStream_t st) {
         if (a.D > 128 && addr32 && (a.doc == nullptr || a.window == 0 || a.is_causal))
             return launch_bwd16_wide<E>(a, st);
     }
+    // 64 < D < 128 with documents: the same kernels' document mode with zero
+    // columns past D.
+    if constexpr ((DP == 96 || DP == 128) && MODE == kGeneral) {
+        if (a.D > 64 && a.D < 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+            if (a.window > 0) return launch_bwd16_d128<E, kWindow, true, true>(a, st);
+            return a.is_causal ? launch_bwd16_d128<E, kCausal, true, true>(a, st)
+                               : launch_bwd16_d128<E, kDense, true, true>(a, st);
+        }
+    }
     if constexpr (DP == 96 || DP == 128) {
         if (a.D > 64 && a.D < 128 && a.doc == nullptr && addr32) {
             if (MODE == kGeneral && a.window > 0 && a.is_causal) return launch_bwd16_d128<E, kWindow, true>(a, st);

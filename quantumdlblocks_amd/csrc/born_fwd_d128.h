@@ -41,8 +41,8 @@
 // past D are not stored.  The arithmetic is that of D == 128 with zero
 // columns (which add nothing to any overlap).
 //
-// DOC: document ids (no window; flash_born.py:145-147, 175-177), one 256-row
-// block per workgroup.  The block's candidate key tiles are screened by
+// DOC: document ids (no window; flash_born.py:145-147, 175-177; also with
+// PAD), one 256-row block per workgroup.  The block's candidate key tiles are screened by
 // document-id range into a list in LDS (as the D == 64 document kernels do)
 // and only the kept tiles go through the ring, each with its 64 key ids.  Per
 // tile a wave skips the work when the tile lies past its rows or is one
@@ -80,7 +80,6 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
     static_assert(MODE == kDense || MODE == kCausal || mode_window(MODE), "mask modes");
     static_assert(MODE != kWindowNC || !DOC, "windows without causality: no documents");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
-    static_assert(!DOC || !PAD, "documents: D == 128");
     static_assert(NW == 8 || (NW == 4 && DOC), "128-row blocks: the document mode");
     using C = FwdD128Cfg;
     constexpr int DP = C::DP, BM = 32 * NW, BN = C::BN, NST = NW == 8 ? C::NST : 2;
@@ -556,7 +555,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 u32x4 x = {0u, 0u, 0u, 0u};
-                if (qrow < T) x = ldg16(Qg + (size_t)qrow * DP + (2 * ks + g) * 8);
+                if (qrow < T && (!PAD || 2 * ks + g < CG)) x = ldg16(Qg + (size_t)qrow * D + (2 * ks + g) * 8);
                 qr[ks] = x ^ flip;
             }
 #pragma unroll
@@ -747,13 +746,13 @@ inline bool d128_fwd_paired(int B, int H, int T, bool causal) {
 
 // Documents (with or without a causal window): one block per workgroup, the
 // longest key ranges first under causality.
-template <class E, int MODE>
+template <class E, int MODE, bool PAD = false>
 hipError_t launch_fwd16_d128_doc(const FwdArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     // 128-row blocks of 4 waves, two workgroups per CU.
     constexpr int NW = 4, BM = 32 * NW;
     const dim3 grid((unsigned)fast_fwd_nmb(a.T, BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, false, true, NW>), grid, dim3(NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, false, PAD, true, NW>), grid, dim3(NW * 64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -772,12 +771,12 @@ hipError_t launch_fwd16_d128(const FwdArgs& a, hipStream_t st) {
 
 // Purified-Born forward with document ids (bf16, D == 128; with or without a
 // causal window).
-template <int MODE, class E = BF16>
+template <int MODE, class E = BF16, bool PAD = false>
 hipError_t launch_purified_fwd_d128_doc(const PurArgs& a, hipStream_t st) {
     using C = FwdD128Cfg;
     constexpr int NW = 4, BM = 32 * NW;
     const dim3 grid((unsigned)fast_fwd_nmb(a.T, BM) * (unsigned)(a.B * a.H));
-    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, false, true, NW>), grid, dim3(NW * 64), 0, st, a);
+    hipLaunchKernelGGL((born_fwd16_d128_kernel<E, MODE, true, PAD, true, NW>), grid, dim3(NW * 64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -26,7 +26,13 @@ hipError_t fwd_launch_f16(const FwdArgs& a, hipStream_t s) {
         return launch_fwd16_fast<F16, 64, kWindowNC>(a, s);
     // D == 128 with document ids (and a causal window): the D == 128 kernel's
     // document mode.
-    if (a.D == 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+    // 64 < D < 128 with documents on the same kernel with zero columns past D.
+    if (a.D > 64 && a.D <= 128 && a.doc != nullptr && addr32 && (a.window == 0 || a.is_causal)) {
+        if (a.D < 128) {
+            if (a.window > 0) return launch_fwd16_d128_doc<F16, kWindow, true>(a, s);
+            return a.is_causal ? launch_fwd16_d128_doc<F16, kCausal, true>(a, s)
+                               : launch_fwd16_d128_doc<F16, kDense, true>(a, s);
+        }
         if (a.window > 0) return launch_fwd16_d128_doc<F16, kWindow>(a, s);
         return a.is_causal ? launch_fwd16_d128_doc<F16, kCausal>(a, s) : launch_fwd16_d128_doc<F16, kDense>(a, s);
     }

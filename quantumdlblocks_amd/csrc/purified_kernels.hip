@@ -43,9 +43,11 @@ inline bool purified_d128_ok(const PurArgs& a) {
     return a.D > 64 && a.D <= 128 && a.doc == nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
-// D == 128 with document ids: the D = 128 kernels' document mode.
+// 64 < D <= 128 with document ids: the D = 128 kernels' document mode (zero
+// columns past D).
 inline bool purified_d128_doc_ok(const PurArgs& a) {
-    return a.D == 128 && purified_window_ok(a) && a.doc != nullptr && ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
+    return a.D > 64 && a.D <= 128 && purified_window_ok(a) && a.doc != nullptr &&
+           ((int64_t)a.T + 256) * a.D * 2 < ((int64_t)1 << 31);
 }
 
 inline bool purified_d256_ok(const PurArgs& a) {
@@ -98,6 +100,11 @@ static hipError_t purified_fwd_dispatch(const PurArgs& a, hipStream_t s) {
     // D = 128, document ids (with or without a causal window): its document
     // mode.
     if (k16 && purified_d128_doc_ok(a)) {
+        if (a.D < 128) {
+            if (a.window > 0) return launch_purified_fwd_d128_doc<kWindow, E, true>(a, s);
+            return a.is_causal ? launch_purified_fwd_d128_doc<kCausal, E, true>(a, s)
+                               : launch_purified_fwd_d128_doc<kDense, E, true>(a, s);
+        }
         if (a.window > 0) return launch_purified_fwd_d128_doc<kWindow, E>(a, s);
         return a.is_causal ? launch_purified_fwd_d128_doc<kCausal, E>(a, s)
                            : launch_purified_fwd_d128_doc<kDense, E>(a, s);
@@ -142,9 +149,8 @@ static hipError_t purified_bwd_fast(const PurArgs& a, hipStream_t s) {
 // then the same reduction.
 template <int MODE, bool DOC = false, class E = BF16>
 static hipError_t purified_bwd_d128(const PurArgs& a, hipStream_t s) {
-    hipError_t e = DOC           ? launch_purified_bwd_d128<MODE, false, DOC, E>(a, s)
-                   : a.D == 128 ? launch_purified_bwd_d128<MODE, false, false, E>(a, s)
-                                : launch_purified_bwd_d128<MODE, true, false, E>(a, s);
+    hipError_t e = a.D == 128 ? launch_purified_bwd_d128<MODE, false, DOC, E>(a, s)
+                              : launch_purified_bwd_d128<MODE, true, DOC, E>(a, s);
     if (e != hipSuccess) return e;
     // dK/dV workgroups: 128-key blocks, 64-key blocks with documents.
     const int nwg = DOC ? ((a.T + 63) / 64) * a.B * a.H : purified_dkdv_groups(a.B, a.H, a.T, 128);

@@ -190,6 +190,18 @@ def test_bwd_wide_dma_kernels(cuda_device, D, dtype, case):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [72, 96, 120])
+@pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
+def test_bwd_padded_documents(cuda_device, dtype, D, is_causal, window):
+    """64 < D < 128 with document ids on the D = 128 kernels' document mode
+    with zero columns past D (dQ on 128-row blocks, dK/dV on 64-key blocks);
+    per-head scales, dscale."""
+    doc = orc.geometric_doc_ids(2, 700, 90.0, seed=D + window)
+    _check_bwd(2, 2, 700, D, dtype, cuda_device, doc=doc, is_causal=is_causal, window_size=window,
+               scale=[0.3, -0.15], std=0.5, seed=D + 7, check_dscale=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [136, 256])
 @pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
 def test_bwd_wide_documents(cuda_device, dtype, D, is_causal, window):

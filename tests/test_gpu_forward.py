@@ -208,6 +208,17 @@ def test_fwd_wide_dma_kernel(cuda_device, D, dtype, case):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [72, 96, 120])
+@pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
+def test_fwd_padded_documents(cuda_device, dtype, D, is_causal, window):
+    """64 < D < 128 with document ids on the D = 128 kernel's document mode
+    with zero columns past D (dense, causal, causal window); O and Z."""
+    doc = orc.geometric_doc_ids(2, 700, 90.0, seed=D + window)
+    _check_fwd(2, 2, 700, D, dtype, cuda_device, doc=doc, is_causal=is_causal, window_size=window,
+               scale=np.array([0.3, -0.15], dtype=np.float32), std=0.5, seed=D + 9)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [136, 256])
 @pytest.mark.parametrize("is_causal, window", [(True, 0), (False, 0), (True, 100)])
 def test_fwd_wide_documents(cuda_device, dtype, D, is_causal, window):

@@ -198,14 +198,15 @@ def test_purified_wide_dma_kernels_long(cuda_device, dtype, D, kw):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("D", [200, 256])
+@pytest.mark.parametrize("D", [96, 200, 256])
 @pytest.mark.parametrize("kw", [dict(is_causal=True), dict(is_causal=False), dict(is_causal=True, window_size=120)],
                          ids=lambda kw: f"causal{int(kw['is_causal'])}-W{kw.get('window_size', 0)}")
 def test_purified_wide_documents(cuda_device, dtype, D, kw):
-    """The wide-row kernels' purified document mode (weights masked through
-    a per-lane bit mask), T = 700 with documents of mean length 90, tau < 0
-    on one head: forward against the oracle to 1e-4, gradients, dgamma and
-    dtau."""
+    """Purified attention with documents off D = 64 and 128: the wide-row
+    kernels' purified document mode (200, 256) and the D = 128 kernels' with
+    zero columns (96); weights masked through a per-lane bit mask, T = 700
+    with documents of mean length 90, tau < 0 on one head: forward against
+    the oracle to 1e-4, gradients, dgamma and dtau."""
     B, H, T = 1, 2, 700
     doc = orc.geometric_doc_ids(B, T, 90.0, seed=D)
     doc_t = torch.tensor(doc, dtype=torch.int32, device=cuda_device)
