@@ -98,9 +98,10 @@ WINDOW = {"w3": 256, "w5": 512, "dw5": 512, "dwc4b": 256, "wc4b": 256, "pw5": 38
 PUR_GAMMA, PUR_TAU, PUR_EPS_BASE, PUR_EPS = 8.0, 0.0625, 0.05, 1e-8
 # Fused Q/K prologue (RoPE + L2 normalisation) on the C3 / C5 shapes.
 PROLOGUE = {"qk3": (16, 16, 1024, 64, False), "qk5": (16, 16, 2048, 64, True)}
-# The prologue folded into the attention forward (one kernel), C3 / C5 shapes,
-# Q and K read raw from the (B, T, H, D) projection layout.
-FUSED = {"qkc3": (16, 16, 1024, 64), "qkc5": (16, 16, 2048, 64)}
+# The prologue folded into the attention forward (one kernel), C3 / C5 / C4
+# shapes (C4: its documents of mean length 512), Q and K read raw from the
+# (B, T, H, D) projection layout.
+FUSED = {"qkc3": (16, 16, 1024, 64, None), "qkc5": (16, 16, 2048, 64, None), "qkc4": (4, 16, 8192, 64, 512.0)}
 
 
 def parse_args():
@@ -192,17 +193,25 @@ def make_inputs(cfg, seed, device, dtype):
         q, k = l2_normalize(q), l2_normalize(k)
     doc = None
     if doc_mean is not None:
-        rng = np.random.default_rng(seed)
-        ids = np.empty((B, T), dtype=np.int32)
-        for b in range(B):
-            t = n_doc = 0
-            while t < T:
-                n = int(rng.geometric(1.0 / doc_mean))
-                ids[b, t : t + n] = n_doc
-                t += n
-                n_doc += 1
-        doc = torch.from_numpy(ids).to(device)
+        doc = torch.from_numpy(doc_ids_np(B, T, doc_mean, seed)).to(device)
     return [x.to(device, dtype).contiguous() for x in (q, k, v, do)], doc
+
+
+def doc_ids_np(B, T, doc_mean, seed):
+    """Sorted document ids (B, T) int32: runs of geometric length with the
+    given mean, as compute_document_ids produces for packed sequences."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ids = np.empty((B, T), dtype=np.int32)
+    for b in range(B):
+        t = n_doc = 0
+        while t < T:
+            n = int(rng.geometric(1.0 / doc_mean))
+            ids[b, t : t + n] = n_doc
+            t += n
+            n_doc += 1
+    return ids
 
 
 def visible_pairs(cfg, doc, window=0):
@@ -734,10 +743,11 @@ def prologue_main(args):
 
 
 def fused_main(args):
-    """qkc3 / qkc5: qdl_flash_born_fwd_qk_prologue, RoPE + L2 normalisation of
-    Q and K folded into the Born attention forward (C3 / C5 shapes, bf16,
-    causal, scale 8; Q, K the (B, T, H, D) projection output, rotary tables of
-    the reference's UnitaryRoPE defaults).  value: the attention's
+    """qkc3 / qkc5 / qkc4: qdl_flash_born_fwd_qk_prologue, RoPE + L2
+    normalisation of Q and K folded into the Born attention forward (C3 / C5
+    / C4 shapes, C4 with its documents; bf16, causal, scale 8; Q, K the
+    (B, T, H, D) projection output, rotary tables of the reference's
+    UnitaryRoPE defaults).  value: the attention's
     algorithmic TFLOP/s of the whole fused step when no backward follows
     (1/norm and q' are not written); detail also times the fused step that
     writes them for a backward, and the same work as two launches (prologue
@@ -748,7 +758,7 @@ def fused_main(args):
 
     lib = _native.load()
     dev = torch.device("cuda:0")
-    B, H, T, D = FUSED[args.config]
+    B, H, T, D, doc_mean = FUSED[args.config]
     steps, warmup = (20, 500) if args.profile else (args.steps, args.warmup)
     code = _native.DTYPE_BF16
     cos, sin = prologue_tables(T, D // 2, dev)
@@ -756,6 +766,8 @@ def fused_main(args):
     stream = torch.cuda.current_stream(dev).cuda_stream
     st = (ctypes.c_int64 * 3)(T * H * D, D, H * D)
     scale = torch.tensor(8.0, dtype=torch.float32, device=dev)
+    doc = None if doc_mean is None else torch.from_numpy(doc_ids_np(B, T, doc_mean, args.seed)).to(dev)
+    docp = None if doc is None else doc.data_ptr()
     g = torch.Generator("cpu").manual_seed(args.seed)
     sets = []
     for _ in range(max(1, args.sets)):
@@ -772,7 +784,7 @@ def fused_main(args):
         q, k, v, out, z, qo, ko, qr, kr = sets[i % len(sets)] if rotate else sets[0]
         rc = lib.qdl_flash_born_fwd_qk_prologue(code, B, H, T, D, q.data_ptr(), st, k.data_ptr(), st, v.data_ptr(),
                                                 cos.data_ptr(), sin.data_ptr(), nf, ld, 1e-12, scale.data_ptr(), 1,
-                                                None, 1, 0, 1e-12, out.data_ptr(), z.data_ptr(), qo.data_ptr(),
+                                                docp, 1, 0, 1e-12, out.data_ptr(), z.data_ptr(), qo.data_ptr(),
                                                 ko.data_ptr(), qr.data_ptr() if bwd_outputs else None,
                                                 kr.data_ptr() if bwd_outputs else None, stream)
         _native.check(rc, "qdl_flash_born_fwd_qk_prologue")
@@ -788,7 +800,7 @@ def fused_main(args):
                                                 kr.data_ptr() if bwd_outputs else None, stream)
         _native.check(rc, "qdl_flash_born_qk_prologue_fwd")
         rc = lib.qdl_flash_born_fwd(code, B, H, T, D, qo.data_ptr(), ko.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                    z.data_ptr(), scale.data_ptr(), 1, None, 1, 0, 1e-12, stream)
+                                    z.data_ptr(), scale.data_ptr(), 1, docp, 1, 0, 1e-12, stream)
         _native.check(rc, "qdl_flash_born_fwd")
 
     for i in range(warmup):
@@ -819,7 +831,7 @@ def fused_main(args):
     for s_ in sets:
         assert torch.isfinite(s_[3].float()).all(), "non-finite output"
 
-    flops = 4.0 * D * (T * (T + 1) // 2) * B * H
+    flops = 4.0 * D * visible_pairs((B, H, T), doc) * H
     rows = B * H * T
     # Algorithmic bytes of the step without a backward: read Q, K, V and the
     # tables, write O and Z.
@@ -841,11 +853,13 @@ def fused_main(args):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.015625) Q, K, V; %d rotated input sets)" % len(sets),
         "config": {"workload": args.config, "batch": B, "heads": H, "seq_len": T, "head_dim": D, "causal": True,
+                   "doc_mask": doc_mean is not None, "doc_mean_len": doc_mean,
                    "rope_pairs": nf, "qk_layout": "(B, T, H, D) viewed as (B, H, T, D)", "scale": 8.0},
         "pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "roofline": roof,
         "cpu_baseline": None,
         "detail": {
+            "flops_counted_on": "visible (causal, same-document) pairs",
             "fused_kernel_us_per_step_events": round(ev_step * 1e6, 3),
             "separate_two_launches_us_per_step_events": round(sep_ev * 1e6, 3),
             "separate_two_launches_us_per_step_wall": round(sep_wall * 1e6, 3),

@@ -250,11 +250,11 @@ int qdl_flash_born_qk_prologue_bwd(int dtype, int64_t B, int64_t H, int64_t T,
  * prologue; scale, doc_ids, is_causal, window_size, eps as for the forward.
  * Also writes q_out, k_out (contiguous (B, H, T, D), the normalised rows) and
  * q_rinv, k_rinv (1/norm per row), which the backward needs.  For bf16 with
- * D == 64, no documents and no window, the keys are normalised by the
- * prologue kernel (keys only) and the attention kernel normalises each query
- * block in registers as it loads it, so the normalised queries are never read
- * back from memory; other cases run the prologue kernel on both and then the
- * attention kernels.  The results are those of the two separate calls, bit
+ * D == 64 and no window (with document ids: no window or a causal one), the
+ * keys are normalised by the prologue kernel (keys only) and the attention
+ * kernel normalises each query block in registers as it loads it, so the
+ * normalised queries are never read back from memory; other cases run the
+ * prologue kernel on both and then the attention kernels.  The results are those of the two separate calls, bit
  * for bit.  q_rinv and k_rinv may be NULL when no backward follows: then
  * neither 1/norm is written, and q_out is scratch (the one-kernel path does
  * not write it).

@@ -170,7 +170,8 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
         return QDL_BORN_E_NULL;
     if (!aligned16(v) || !aligned16(out) || !aligned16(q_out) || !aligned16(k_out)) return QDL_BORN_E_ALIGN;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // bf16, D = 64, dense or causal: K is normalised by the prologue kernel
+    // bf16, D = 64, dense or causal, with or without document ids (with
+    // documents also a causal window): K is normalised by the prologue kernel
     // (K alone), then one attention kernel normalises each query block as it
     // loads it (raw rows 16-byte aligned, (T + 256) rows of their time stride
     // within 32-bit offsets) and, when q_rinv is given (a backward follows),
@@ -178,7 +179,8 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
     const bool q_rows_ok = aligned16(q) && q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 &&
                            q_strides[2] % 8 == 0 && q_strides[2] >= D &&
                            (T + 256) * q_strides[2] * 2 < ((int64_t)1 << 31);
-    if (dtype == QDL_BORN_DTYPE_BF16 && D == 64 && !doc_ids && window_size == 0 && q_rows_ok &&
+    const bool masks_ok = doc_ids ? (window_size == 0 || is_causal) : window_size == 0;
+    if (dtype == QDL_BORN_DTYPE_BF16 && D == 64 && masks_ok && q_rows_ok &&
         (!cos_table || n_freq >= 1) && (T + 256) * D * 2 < ((int64_t)1 << 31)) {
         rc = qdl_flash_born_qk_prologue_fwd(dtype, B, H, T, D, nullptr, nullptr, k, k_strides, cos_table, sin_table,
                                             n_freq, table_ld, norm_eps, nullptr, k_out, nullptr, k_rinv, stream);
@@ -190,14 +192,14 @@ int qdl_flash_born_fwd_qk_prologue(int dtype, int64_t B, int64_t H, int64_t T, i
         a.o = out;
         a.z = z;
         a.scale = scale;
-        a.doc = nullptr;
+        a.doc = doc_ids;
         a.per_head_scale = n_scale > 1 ? 1 : 0;
         a.B = (int)B;
         a.H = (int)H;
         a.T = (int)T;
         a.D = (int)D;
         a.is_causal = is_causal ? 1 : 0;
-        a.window = 0;
+        a.window = (int)window_size;
         a.eps = (float)eps;
         a.q_sb = q_strides[0];
         a.q_sh = q_strides[1];

@@ -58,7 +58,13 @@ hipError_t fwd_launch_bf16(const FwdArgs& a, hipStream_t s) {
 }
 
 hipError_t fwd_prologue_launch_bf16(const FwdProArgs& a, hipStream_t s) {
-    if (a.D != 64 || a.doc != nullptr || a.window != 0) return hipErrorInvalidValue;
+    if (a.D != 64) return hipErrorInvalidValue;
+    // Documents (with or without a causal window): the document kernel.
+    if (a.doc != nullptr) {
+        if (a.window == 0) return launch_fwd16_doc_prologue<false>(a, s);
+        return a.is_causal ? launch_fwd16_doc_prologue<true>(a, s) : hipErrorInvalidValue;
+    }
+    if (a.window != 0) return hipErrorInvalidValue;
     return a.is_causal ? launch_fwd16_fast_prologue<kCausal>(a, s) : launch_fwd16_fast_prologue<kDense>(a, s);
 }
 

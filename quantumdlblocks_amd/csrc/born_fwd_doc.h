@@ -51,11 +51,19 @@ namespace qdl {
 // either way; 128-row blocks straddle fewer document edges and cut the
 // causal diagonal finer (C4's documents: 1.28x the visible pairs executed
 // against 1.53x for 256-row blocks).
-template <class E, int DP, bool PUR = false, bool WIN = false, int NW = 4>
+//
+// PRO: the Q prologue folded into the Q load (bf16 Born): q holds the raw
+// query rows (element strides q_sb, q_sh, q_st), each lane rotates and
+// normalises its rows' operands in registers as the standalone prologue
+// kernel would (born_qk_fold.h), and, when a backward follows (q_rinv set),
+// writes the normalised rows and their 1/norm.
+template <class E, int DP, bool PUR = false, bool WIN = false, int NW = 4, bool PRO = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::type p) {
+void born_fwd16_doc_kernel(
+    typename std::conditional<PUR, PurArgs, typename std::conditional<PRO, FwdProArgs, FwdArgs>::type>::type p) {
     static_assert(DP == 64, "tuned for D = 64");
     static_assert(!PUR || std::is_same<E, BF16>::value || std::is_same<E, F16>::value, "purified: 16-bit inputs");
+    static_assert(!PRO || (std::is_same<E, BF16>::value && !PUR), "the fused prologue is bf16 Born only");
     static_assert(NW == 4 || NW == 2, "256- or 128-row blocks");
     constexpr int NQB = 2, BN = 64, NST = NW == 4 ? 3 : 2, BM = 64 * NW;
     constexpr int KS = DP / 16;
@@ -124,17 +132,58 @@ void born_fwd16_doc_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::typ
     const int lrow = (BM / 4) * (c >> 4) + 16 * wave + (c & 15);
     int qrow[NQB], qdoc[NQB];
     u32x4 qr[NQB][KS];
+    if constexpr (PRO) {
+        // Raw rows, the table entries of every row of the lane first (one
+        // memory round trip), then q' in registers.
+        const uint16_t* Qraw = reinterpret_cast<const uint16_t*>(p.q) + (size_t)b * p.q_sb + (size_t)h * p.q_sh;
+        const bool rot = p.cos != nullptr;
+        const bool vec = rot && ((reinterpret_cast<uintptr_t>(p.cos) | reinterpret_cast<uintptr_t>(p.sin)) & 15) == 0 &&
+                         (p.ld & 3) == 0 && p.nfreq >= DP / 2;
+        RotRow rt[NQB][2];
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        qrow[qb] = R + (BM / 2) * qb + lrow;
-        const bool ok = qrow[qb] < T;
+        for (int qb = 0; qb < NQB; ++qb) {
+            qrow[qb] = R + (BM / 2) * qb + lrow;
+            const bool ok = qrow[qb] < T;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            u32x4 x = {0u, 0u, 0u, 0u};
-            if (ok) x = ldg16(Qg + (size_t)qrow[qb] * DP + (2 * ks + g) * 8);
-            qr[qb][ks] = x ^ flip;
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 x = {0u, 0u, 0u, 0u};
+                if (ok) x = ldg16(Qraw + (size_t)qrow[qb] * p.q_st + (2 * ks + g) * 8);
+                qr[qb][ks] = x;
+            }
+            if (rot) {
+                rot_load(p.cos, p.sin, p.ld, p.nfreq, T, qrow[qb], 8 * g, vec, rt[qb][0]);
+                rot_load(p.cos, p.sin, p.ld, p.nfreq, T, qrow[qb], 8 * (2 + g), vec, rt[qb][1]);
+            }
+            qdoc[qb] = ok ? docb[qrow[qb]] : INT_MIN;
         }
-        qdoc[qb] = ok ? docb[qrow[qb]] : INT_MIN;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            const float rinv = rot_normalise_row(qr[qb], rt[qb][0], rt[qb][1], rot, p.norm_eps);
+            // The normalised rows and their 1/norm, for the backward (not
+            // written when no backward follows: q_rinv null).
+            if (qrow[qb] < T && p.q_rinv != nullptr) {
+                uint16_t* qo = reinterpret_cast<uint16_t*>(p.q_out) + base + (size_t)qrow[qb] * DP;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    __builtin_nontemporal_store(qr[qb][ks], reinterpret_cast<u32x4*>(qo + 8 * (2 * ks + g)));
+                if (g == 0) __builtin_nontemporal_store(rinv, p.q_rinv + (size_t)bh * T + qrow[qb]);
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qr[qb][ks] ^= flip;
+        }
+    } else {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+            qrow[qb] = R + (BM / 2) * qb + lrow;
+            const bool ok = qrow[qb] < T;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 x = {0u, 0u, 0u, 0u};
+                if (ok) x = ldg16(Qg + (size_t)qrow[qb] * DP + (2 * ks + g) * 8);
+                qr[qb][ks] = x ^ flip;
+            }
+            qdoc[qb] = ok ? docb[qrow[qb]] : INT_MIN;
+        }
     }
 
     const int kv_hi = causal ? min(T, R + BM) : T;
@@ -619,6 +668,17 @@ hipError_t launch_fwd16_doc(const FwdArgs& a, hipStream_t st) {
     constexpr int NW = 2, BM = 64 * NW;
     const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
     hipLaunchKernelGGL((born_fwd16_doc_kernel<E, DP, false, WIN, NW>), grid, dim3(64 * NW), 0, st, a);
+    return hipGetLastError();
+}
+
+// Born forward with document ids and the Q prologue folded into the Q load
+// (bf16, D = 64; WIN: with a causal sliding window); the keys arrive
+// normalised.  Same grid as launch_fwd16_doc.
+template <bool WIN = false>
+hipError_t launch_fwd16_doc_prologue(const FwdProArgs& a, hipStream_t st) {
+    constexpr int NW = 2, BM = 64 * NW;
+    const dim3 grid((unsigned)((a.T + BM - 1) / BM) * (unsigned)(a.B * a.H));
+    hipLaunchKernelGGL((born_fwd16_doc_kernel<BF16, 64, false, WIN, NW, true>), grid, dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 

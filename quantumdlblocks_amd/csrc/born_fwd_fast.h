@@ -49,6 +49,7 @@
 #include <type_traits>
 
 #include "born_common.h"
+#include "born_qk_fold.h"
 #include "purified_args.h"
 
 namespace qdl {
@@ -469,15 +470,9 @@ void born_fwd16_fast_kernel(
 
     // Q prologue folded into the query-block load (PRO): the raw query rows
     // come in through the Q block's LDS staging as usual, and each lane turns
-    // its rows' operands into q' = l2_normalize(rope(q)) in registers, with
-    // the rounding of the standalone prologue kernel (qk_prologue.hip), so the
-    // rows are bit-identical to its output: each table entry, product, sum and
-    // difference rounded to bf16, the fp32 sum of squares accumulated pair by
-    // pair and then across the row's four 8-pair chunks as ((c0 + c1) +
-    // (c2 + c3)), 1/norm = 1/sqrt(sum + eps) correctly rounded from double.
-    // Chunk c of a row (columns 8c .. 8c+7) rotates against chunk c + 4; a
-    // lane's operands hold chunks g, 2 + g and their partners.  The keys
-    // arrive normalised (the prologue kernel runs on K alone first):
+    // its rows' operands into q' = l2_normalize(rope(q)) in registers
+    // (born_qk_fold.h: bit-identical to the standalone prologue kernel).  The
+    // keys arrive normalised (the prologue kernel runs on K alone first):
     // normalising each K tile in LDS here measured slower than the two
     // separate launches (every key tile is staged by ~2.5 workgroups, and the
     // tile loop is bound by instruction issue).
@@ -489,100 +484,6 @@ void born_fwd16_fast_kernel(
         KargPtr ka = (KargPtr)(__builtin_amdgcn_kernarg_segment_ptr());
         asm volatile("" : "+s"(ka));
         return ka;
-    };
-    // Table entries of row t (clamped to T - 1; rows past T hold zeros, so
-    // any table row gives zeros) for pairs i0 .. i0+7, rounded to bf16 as
-    // the prologue kernel rounds them; pairs past nfreq rotate by angle 0.
-    // Loaded for all of a lane's rows before any is used, so one memory
-    // round trip covers the whole Q block.
-    struct RotRow {
-        float c[8], s[8];
-    };
-    // vec: 16-byte loads (tables aligned, ld a multiple of 4, and all 32
-    // pairs of the head dim inside the table), the same for every lane.
-    auto load_rot = [&](int t, int i0, bool vec, RotRow& r) __attribute__((always_inline)) {
-        if constexpr (PRO) {
-            KargPtr ka = pro_args();
-            const int nf = ka->nfreq, ld = ka->ld;
-            const int tt = min(t, T - 1);
-            const float* cr = ka->cos + (size_t)tt * ld;
-            const float* sr = ka->sin + (size_t)tt * ld;
-            if (vec) {
-#pragma unroll
-                for (int v = 0; v < 8; v += 4) {
-                    const f32x4 x = *reinterpret_cast<const f32x4*>(cr + i0 + v);
-                    const f32x4 y = *reinterpret_cast<const f32x4*>(sr + i0 + v);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        r.c[v + e] = x[e];
-                        r.s[v + e] = y[e];
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const int idx = min(i0 + v, nf - 1);
-                    const float x = cr[idx], y = sr[idx];
-                    r.c[v] = (i0 + v < nf) ? x : 1.f;
-                    r.s[v] = (i0 + v < nf) ? y : 0.f;
-                }
-            }
-        }
-    };
-    // Rotate the 8 pairs (a[v], b[v]) of columns i0 .. i0+7 of a row by the
-    // table entries r (rot: a table was given); returns the pairs' sum of
-    // squares.  ya, yb: the rotated (bf16-exact) values.
-    auto rope8 = [&](const u32x4& a, const u32x4& b, RotRow& r, bool rot, u32x4& ya, u32x4& yb)
-        __attribute__((always_inline)) -> float {
-#pragma clang fp contract(off)
-        float ss = 0.f;
-        if constexpr (PRO) {
-            if (rot) {
-#pragma unroll
-                for (int v = 0; v < 8; v += 2) {
-                    const uint32_t uc = BF16::pack(r.c[v], r.c[v + 1]), us = BF16::pack(r.s[v], r.s[v + 1]);
-                    r.c[v] = BF16::lo(uc);
-                    r.c[v + 1] = BF16::hi(uc);
-                    r.s[v] = BF16::lo(us);
-                    r.s[v + 1] = BF16::hi(us);
-                }
-            }
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                float y1[2], y2[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const float x1 = e ? BF16::hi(a[w]) : BF16::lo(a[w]);
-                    const float x2 = e ? BF16::hi(b[w]) : BF16::lo(b[w]);
-                    if (rot) {
-                        const int v = 2 * w + e;
-                        const float r0 = BF16::lo(BF16::pack(x1 * r.c[v], 0.f));
-                        const float r1 = BF16::lo(BF16::pack(x2 * r.s[v], 0.f));
-                        const float r2 = BF16::lo(BF16::pack(x1 * r.s[v], 0.f));
-                        const float r3 = BF16::lo(BF16::pack(x2 * r.c[v], 0.f));
-                        y1[e] = BF16::lo(BF16::pack(r0 - r1, 0.f));
-                        y2[e] = BF16::lo(BF16::pack(r2 + r3, 0.f));
-                    } else {
-                        y1[e] = x1;
-                        y2[e] = x2;
-                    }
-                    ss = fmaf(y1[e], y1[e], fmaf(y2[e], y2[e], ss));
-                }
-                ya[w] = BF16::pack(y1[0], y1[1]);
-                yb[w] = BF16::pack(y2[0], y2[1]);
-            }
-        }
-        return ss;
-    };
-    auto rinv_of = [&](float ss) __attribute__((always_inline)) -> float {
-        float ne = 0.f;
-        if constexpr (PRO) ne = pro_args()->norm_eps;
-        const float se = ss + ne;
-        return (float)(1.0 / sqrt((double)se));
-    };
-    auto scale_row = [&](u32x4& y, float rinv) __attribute__((always_inline)) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) y[w] = BF16::pack(BF16::lo(y[w]) * rinv, BF16::hi(y[w]) * rinv);
     };
     // This wave's rows of the Q block in LDS -> B operands of S^T.  The sign
     // of the scale is folded into Q; the asm pins the result in registers so
@@ -603,8 +504,9 @@ void born_fwd16_fast_kernel(
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
                     const int t = mb * BM + 128 * qb + lr;
-                    load_rot(t, 8 * (ln >> 5), vec, rtab[qb][0]);
-                    load_rot(t, 8 * (2 + (ln >> 5)), vec, rtab[qb][1]);
+                    KargPtr kt = pro_args();
+                    rot_load(kt->cos, kt->sin, kt->ld, kt->nfreq, T, t, 8 * (ln >> 5), vec, rtab[qb][0]);
+                    rot_load(kt->cos, kt->sin, kt->ld, kt->nfreq, T, t, 8 * (2 + (ln >> 5)), vec, rtab[qb][1]);
                 }
             };
             if (rot) {
@@ -629,20 +531,7 @@ void born_fwd16_fast_kernel(
                 // 4 + g, 6 + g (ks 2, 3); the other half-wave the rest of the row.
                 const int gg = ln >> 5;
                 const int t = mb * BM + 128 * qb + lr;
-                u32x4 y0, y1, y2, y3;
-                const float pa = rope8(qr[qb][0], qr[qb][2], rtab[qb][0], rot, y0, y2);
-                const float pb = rope8(qr[qb][1], qr[qb][3], rtab[qb][1], rot, y1, y3);
-                const float s01 = pa + __shfl_xor(pa, 32);
-                const float s23 = pb + __shfl_xor(pb, 32);
-                const float rinv = rinv_of(s01 + s23);
-                scale_row(y0, rinv);
-                scale_row(y1, rinv);
-                scale_row(y2, rinv);
-                scale_row(y3, rinv);
-                qr[qb][0] = y0;
-                qr[qb][1] = y1;
-                qr[qb][2] = y2;
-                qr[qb][3] = y3;
+                const float rinv = rot_normalise_row(qr[qb], rtab[qb][0], rtab[qb][1], rot, pro_args()->norm_eps);
                 // The normalised rows and their 1/norm, for the backward
                 // (not written when no backward follows: q_rinv null).
                 if (t < T && pro_args()->q_rinv != nullptr) {

@@ -4,11 +4,13 @@ K through the prologue kernel, Q normalised by the attention kernel as it
 loads each query block).
 
 Bars:
-  * bit for bit: the fused path (bf16, D = 64, dense or causal) gives the
+  * bit for bit: the fused path (bf16, D = 64, dense or causal; with
+    document ids also a causal window, on the document kernel) gives the
     same O, Z, normalised Q and K and 1/norm as the standalone prologue kernel
     on Q and K followed by the attention kernel, on
     contiguous and projection-layout inputs, full, partial and no rotary
-    tables, both scale signs, per-head scales, ragged T and the C3 shape;
+    tables, both scale signs, per-head scales, ragged T, sorted and unsorted
+    document ids and the C3 shape;
   * against the oracles: the normalised rows equal the prologue oracle's
     rounding model given the kernel's 1/norm, 1/norm within 4 ulps, and O
     within 2e-2 (normwise) of ``born_oracle.forward`` applied to the
@@ -16,8 +18,9 @@ Bars:
   * gradients: the autograd entry gives bit-identical gradients to the
     composition ``flash_born_attention(fused_qk_rope_l2_normalize(...))``
     (the backward is the attention backward then the prologue backward);
-  * other shapes (fp16, D = 32, documents, window) take the two-launch path
-    through the same entry and equal the composition.
+  * other shapes (fp16, D = 32, windows without documents, documents with a
+    window but no causality) take the two-launch path through the same entry
+    and equal the composition.
 """
 
 from __future__ import annotations
@@ -128,6 +131,78 @@ def test_fused_equals_prologue_then_attention_bitwise(cuda_device, case):
         assert _same(x, y), name
 
 
+DOC_CASES = [
+    # (B, H, T, nfreq or None, strided, causal, window, mean document length or "unsorted", scale)
+    (2, 3, 700, 32, True, True, 0, 90.0, 8.0),
+    (1, 2, 1500, 20, True, False, 0, 200.0, -3.0),
+    (2, 2, 513, 32, False, True, 100, 60.0, np.array([1.5, 9.0])),
+    (1, 4, 777, None, True, True, 0, 50.0, 8.0),
+    (1, 1, 1, 32, False, True, 0, 4.0, 8.0),
+    (1, 2, 2500, 7, True, True, 256, 300.0, 8.0),
+    (2, 2, 640, 32, True, True, 0, "unsorted", 8.0),
+    (1, 2, 900, 32, True, True, 64, "unsorted", 2.0),
+]
+
+
+def _doc_ids(B, T, how, seed):
+    if how == "unsorted":  # ids repeat in no order: documents are sets of positions
+        return np.random.default_rng(seed).integers(0, 5, size=(B, T)).astype(np.int32)
+    return orc.geometric_doc_ids(B, T, how, seed=seed)
+
+
+@pytest.mark.parametrize("case", DOC_CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}-n{c[3]}-{'strided' if c[4] else 'dense'}-{'causal' if c[5] else 'full'}-W{c[6]}-{c[7]}")
+def test_fused_documents_equal_prologue_then_attention_bitwise(cuda_device, case):
+    """Document ids (and with them a causal window) on the document kernel
+    with the Q prologue in its Q load: bit for bit against the two launches."""
+    B, H, T, nf, strided, causal, window, how, scale = case
+    q, k, v, _ = _inputs(B, H, T, 64, torch.bfloat16, strided, seed=T + 5, dev=cuda_device, std=0.7)
+    cos = sin = None
+    if nf is not None:
+        cos, sin = (x.to(cuda_device) for x in _tables(T, nf))
+    doc = _doc_ids(B, T, how, seed=T)
+    print(f"fused documents B{B} H{H} T{T} n={nf} strided={strided} causal={causal} W={window} docs={how}",
+          flush=True)
+    a = _abi(True, q, k, v, scale, cos, sin, causal, doc=doc, window=window)
+    b = _abi(False, q, k, v, scale, cos, sin, causal, doc=doc, window=window)
+    for name, x, y in zip(("out", "z", "q'", "k'", "q_rinv", "k_rinv"), a, b):
+        assert _same(x, y), name
+    for fused in (True, False):  # no backward follows: O, Z and k' as with the 1/norm outputs
+        part = _abi(fused, q, k, v, scale, cos, sin, causal, doc=doc, window=window, rinv=False)
+        for name, i in (("out", 0), ("z", 1), ("k'", 3)):
+            assert _same(part[i], a[i]), (fused, name)
+        assert torch.isnan(part[4]).all() and torch.isnan(part[5]).all(), fused
+
+
+def test_fused_documents_c4_shape_against_oracles(cuda_device):
+    """C4's shape (B4 H16 T8192, documents of mean 512) in the projection
+    layout: bit for bit against the two launches; sampled heads against the
+    composition of the prologue and attention oracles."""
+    B, H, T, D = 4, 16, 8192, 64
+    q, k, v, _ = _inputs(B, H, T, D, torch.bfloat16, True, seed=13, dev=cuda_device)
+    cos, sin = _tables(T, D // 2, base=10000.0)
+    cos_np, sin_np = cos[0, 0].numpy(), sin[0, 0].numpy()
+    cos, sin = cos.to(cuda_device), sin.to(cuda_device)
+    doc = orc.geometric_doc_ids(B, T, 512.0, seed=3)
+    a = _abi(True, q, k, v, 8.0, cos, sin, doc=doc)
+    b = _abi(False, q, k, v, 8.0, cos, sin, doc=doc)
+    for name, x, y in zip(("out", "z", "q'", "k'", "q_rinv", "k_rinv"), a, b):
+        assert _same(x, y), name
+    out, z, qo, ko, qr, kr = a
+    for bb, hh in ((0, 0), (3, 15)):
+        rows = slice(0, 1536)  # causal: the first 1536 rows see keys among themselves only
+        qn = po.prologue_forward(q[bb, hh, rows].float().cpu().numpy(), cos_np[rows], sin_np[rows], 1e-12, "bf16")[0]
+        kn = po.prologue_forward(k[bb, hh, rows].float().cpu().numpy(), cos_np[rows], sin_np[rows], 1e-12, "bf16")[0]
+        vn = v[bb, hh, rows].float().cpu().numpy()
+        d = doc[bb:bb + 1, rows]
+        ref, zref = orc.forward(qn[None, None], kn[None, None], vn[None, None], 8.0, doc_ids=d)
+        err = rel_err(f64(out[bb, hh, rows]), ref[0, 0])
+        print(f"C4 fused head ({bb},{hh}): O rel {err:.3e}", flush=True)
+        assert err <= 2e-2
+        bound = z_row_bound(qn[None, None], kn[None, None], 8.0, zref, 1e-12, torch.bfloat16,
+                            orc.visible_mask(1536, True, 0, d))
+        assert np.all(np.abs(f64(z[bb, hh, rows]) - zref[0, 0]) <= bound[0, 0])
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_fused_without_backward_outputs(cuda_device, causal):
     """1/norm pointers NULL (no backward follows): O and Z bit for bit as
@@ -183,23 +258,26 @@ def test_fused_c3_shape_bitwise_and_oracle(cuda_device):
         assert np.all(np.abs(f64(z[bb, hh]) - zref[0, 0]) <= bound[0, 0])
 
 
-@pytest.mark.parametrize("strided", [True, False])
-def test_fused_autograd_equals_composition(cuda_device, strided):
+@pytest.mark.parametrize("strided, docs, window", [(True, False, 0), (False, False, 0), (True, True, 0),
+                                                   (True, True, 80)])
+def test_fused_autograd_equals_composition(cuda_device, strided, docs, window):
     from quantumdlblocks_amd import flash_born_attention, flash_born_attention_qk_prologue, fused_qk_rope_l2_normalize
 
     B, H, T, D = 2, 4, 333, 64
     q, k, v, do = _inputs(B, H, T, D, torch.bfloat16, strided, seed=5, dev=cuda_device)
     cos, sin = (x.to(cuda_device) for x in _tables(T, 32))
     sc = torch.tensor([2.0, -3.0, 8.0, 0.5], device=cuda_device)
+    doc_t = torch.as_tensor(orc.geometric_doc_ids(B, T, 60.0, seed=2), device=cuda_device) if docs else None
+    kw = dict(window_size=window, doc_ids=doc_t)
 
     def run(fused):
         qa, ka, va = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
         s = sc.detach().clone().requires_grad_(True)
         if fused:
-            out = flash_born_attention_qk_prologue(qa, ka, va, s, cos, sin)
+            out = flash_born_attention_qk_prologue(qa, ka, va, s, cos, sin, **kw)
         else:
             qn, kn = fused_qk_rope_l2_normalize(qa, ka, cos, sin)
-            out = flash_born_attention(qn, kn, va, s)
+            out = flash_born_attention(qn, kn, va, s, **kw)
         out.backward(do)
         torch.cuda.synchronize()
         return out, qa.grad, ka.grad, va.grad, s.grad
@@ -211,18 +289,21 @@ def test_fused_autograd_equals_composition(cuda_device, strided):
     assert a[1].stride() == q.stride()
 
 
-@pytest.mark.parametrize("dtype, D, doc, window", [
-    (torch.float16, 64, False, 0), (torch.bfloat16, 32, False, 0), (torch.bfloat16, 64, True, 0),
-    (torch.bfloat16, 64, False, 50), (torch.float32, 128, False, 0)])
-def test_other_shapes_take_the_two_launch_path(cuda_device, dtype, D, doc, window):
+@pytest.mark.parametrize("dtype, D, doc, window, causal", [
+    (torch.float16, 64, False, 0, True), (torch.bfloat16, 32, False, 0, True), (torch.bfloat16, 64, True, 0, True),
+    (torch.bfloat16, 64, False, 50, True), (torch.bfloat16, 64, True, 50, False), (torch.float32, 128, False, 0, True)])
+def test_other_shapes_take_the_two_launch_path(cuda_device, dtype, D, doc, window, causal):
+    """The entry against the composition through the public functions (the
+    bf16 D = 64 document case is the fused one)."""
     from quantumdlblocks_amd import flash_born_attention, flash_born_attention_qk_prologue, fused_qk_rope_l2_normalize
 
     B, H, T = 2, 2, 200
     q, k, v, do = _inputs(B, H, T, D, dtype, True, seed=D, dev=cuda_device)
     cos, sin = (x.to(cuda_device) for x in _tables(T, D // 2))
     doc_t = torch.as_tensor(orc.geometric_doc_ids(B, T, 40.0, seed=1), device=cuda_device) if doc else None
-    a = flash_born_attention_qk_prologue(q, k, v, 4.0, cos, sin, window_size=window, doc_ids=doc_t)
+    kw = dict(window_size=window, doc_ids=doc_t, is_causal=causal)
+    a = flash_born_attention_qk_prologue(q, k, v, 4.0, cos, sin, **kw)
     qn, kn = fused_qk_rope_l2_normalize(q, k, cos, sin)
-    b = flash_born_attention(qn, kn, v, 4.0, window_size=window, doc_ids=doc_t)
+    b = flash_born_attention(qn, kn, v, 4.0, **kw)
     torch.cuda.synchronize()
     assert _same(a, b)
