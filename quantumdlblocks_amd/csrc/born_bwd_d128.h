@@ -470,9 +470,14 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         }
     };
     for (; u < runs.ta; ++u) step();
-    run(runs.tf, Masked{});
-    run(runs.tg, Full{});
-    run(runs.tv, Masked{});
+    if constexpr (MODE == kDense) {
+        // Nothing to mask (keys past T have zero K rows): one loop.
+        run(ntiles, Full{});
+    } else {
+        run(runs.tf, Masked{});
+        run(runs.tg, Full{});
+        run(runs.tv, Masked{});
+    }
     for (; u < ntiles; ++u) step();
     }
 

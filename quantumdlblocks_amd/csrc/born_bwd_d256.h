@@ -505,9 +505,14 @@ void born_bwd16_dq_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
         step();
         ro.flip();
     }
-    run(runs.tf, Masked{});
-    run(runs.tg, Full{});
-    run(runs.tv, Masked{});
+    if constexpr (MODE == kDense) {
+        // Nothing to mask (the rows past T contribute zero): one loop.
+        run(ntiles, Full{});
+    } else {
+        run(runs.tf, Masked{});
+        run(runs.tg, Full{});
+        run(runs.tv, Masked{});
+    }
     for (; u < ntiles; ++u) step();
     }
 
@@ -691,6 +696,12 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     using Full = std::integral_constant<int, kFull>;
     using Masked = std::integral_constant<int, kMasked>;
     using Docm = std::integral_constant<int, kDocm>;
+    // Query at offset d = query - key masked by causality (d < 0) or the
+    // window (d >= W): with both, one unsigned compare.
+    auto cut = [&](int d) __attribute__((always_inline)) -> bool {
+        if constexpr (kCaus && kWin) return (uint32_t)d >= (uint32_t)W;
+        return (kCaus && d < 0) || (kWin && d >= W);
+    };
     // Documents: the lane's key document id (INT_MIN past T); per tile,
     // whether this wave tests it per element.
     const int kdoc = (DOC && key < T) ? docb[key] : INT_MIN;
@@ -738,7 +749,7 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc) s[4 * i + k] = 0.f;
+                        if (cut(8 * i + k + lim) || dq[k] != kdoc) s[4 * i + k] = 0.f;
                 }
             }
         }
@@ -749,7 +760,7 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) s[r] = 0.f;
+                if (cut(off + lim)) s[r] = 0.f;
             }
         }
         uint32_t w2[8], u2[8];
@@ -761,7 +772,6 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             uint32_t dmask = 0;
             if constexpr (decltype(m)::value == kDocm) {
                 if (dmw) {
-                    const int dlim = kCaus ? lim : INT_MAX / 2;
                     const int32_t* qd = reinterpret_cast<const int32_t*>(rw + 2 * BQ * 4);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -769,7 +779,7 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k + dlim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                            if (cut(8 * i + k + lim) || dq[k] != kdoc)
                                 dmask |= 1u << (4 * i + k);
                     }
                 }
@@ -788,7 +798,7 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         float bb = __int_as_float(max(__float_as_int(x), 0));
                         if constexpr (decltype(m)::value == kMasked) {
                             const int off = 8 * (r >> 2) + (r & 3);
-                            if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) uu = bb = 0.f;
+                            if (cut(off + lim)) uu = bb = 0.f;
                         }
                         if constexpr (decltype(m)::value == kDocm)
                             if ((dmask >> r) & 1u) uu = bb = 0.f;
@@ -926,9 +936,14 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
         step();
         ro.flip();
     }
-    run(runs.tf, Masked{});
-    run(runs.tg, Full{});
-    run(runs.tv, Masked{});
+    if constexpr (MODE == kDense) {
+        // Nothing to mask (the rows past T contribute zero): one loop.
+        run(ntiles, Full{});
+    } else {
+        run(runs.tf, Masked{});
+        run(runs.tg, Full{});
+        run(runs.tv, Masked{});
+    }
     for (; u < ntiles; ++u) step();
     }
 
