@@ -697,9 +697,12 @@ void born_bwd16_dkdv_d256_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
     using Masked = std::integral_constant<int, kMasked>;
     using Docm = std::integral_constant<int, kDocm>;
     // Query at offset d = query - key masked by causality (d < 0) or the
-    // window (d >= W): with both, one unsigned compare.
+    // window (d >= W): with both, one unsigned compare; documents under
+    // causality take the unsigned form too (|d| < T), which measured fewer
+    // spilled registers with padded head dims.
     auto cut = [&](int d) __attribute__((always_inline)) -> bool {
         if constexpr (kCaus && kWin) return (uint32_t)d >= (uint32_t)W;
+        if constexpr (kCaus && DOC) return (uint32_t)d >= 0x7fffffffu;
         return (kCaus && d < 0) || (kWin && d >= W);
     };
     // Documents: the lane's key document id (INT_MIN past T); per tile,
