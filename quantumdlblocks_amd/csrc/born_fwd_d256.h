@@ -155,7 +155,7 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qr[ks]));
     };
     // Tile 0 goes out before the Q rows are loaded, so the two overlap
-    // (documents: after the first screening, below).
+    // (documents: Q first, during the screening, below).
     if constexpr (!DOC) {
         issue(0);
         load_q();
@@ -324,9 +324,11 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
         }
     };
     if constexpr (DOC) {
-        // The rows' documents first (the screening needs them): this wave's
-        // range of ids (uniform; wone: one document) and the block's.
+        // The rows' documents (the screening needs them), then the Q rows,
+        // whose transfer overlaps the screening: this wave's range of ids
+        // (uniform; wone: one document) and the block's.
         if (qrow < T) qdoc = docb[qrow];
+        load_q();
         int wlo = qrow < T ? qdoc : INT_MAX, whi = qrow < T ? qdoc : INT_MIN;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -347,13 +349,11 @@ void born_fwd16_d256_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
             bq_lo = min(bq_lo, s_rng[2 * w]);
             bq_hi = max(bq_hi, s_rng[2 * w + 1]);
         }
-        // The kept tiles of each chunk of candidates through the ring; Q is
-        // loaded after the first chunk's first tile is issued.
+        // The kept tiles of each chunk of candidates through the ring.
         for (int c0 = 0; c0 < ntiles; c0 += CAP) {
             const int n = screen_doc_tiles<BN>(docb, T, tb * BN, c0, min(CAP, ntiles - c0), bq_lo, bq_hi, t_keep, t_tdoc,
                                                t_list, t_doc, &s_rng[2 * NW]);
             if (n > 0) issue(0);
-            if (c0 == 0) load_q();
             for (u = 0; u < n; ++u) {
                 step_n(n);
                 kdp = kd_lds + (u % NST) * BN;
