@@ -286,7 +286,7 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
             // A masked pair weighs zero even where its overlap is zero (u =
             // relu(-gamma tau) > 0 for tau < 0).  Keys past T need no mask
             // here: their K rows (zero) multiply U.
-            const int lim = qrow - kbase;
+            const int lim = qrow - kbase;  // query - key of register 0
             const int wlo = kWin ? lim - W + 1 : 0;  // window: first visible key
             // Documents: bit r set for a register masked by the diagonal
             // (causal), the window or another document.
@@ -318,7 +318,10 @@ void born_bwd16_dq_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                     float d = f * fmaf(t[r], zinv, nd);
                     if constexpr (decltype(m)::value == kMasked) {
                         const int off = 8 * (r >> 2) + (r & 3);
-                        if ((kCaus && off > lim) || (kWin && off < wlo)) d = 0.f;
+                        // Causal with a window: one unsigned compare.
+                        const bool cut = (kCaus && kWin) ? pair_cut<kCaus, kWin>(lim - off, W)
+                                                         : ((kCaus && off > lim) || (kWin && off < wlo));
+                        if (cut) d = 0.f;
                     }
                     if constexpr (decltype(m)::value == kDocm)
                         if ((dmask >> r) & 1u) d = 0.f;
@@ -754,7 +757,6 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             uint32_t dmask = 0;
             if constexpr (decltype(m)::value == kDocm) {
                 if (dmw) {
-                    const int dlim = kCaus ? lim : INT_MAX / 2;
                     const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -762,7 +764,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k + dlim < 0 || (kWin && 8 * i + k + lim >= W) || dq[k] != kdoc)
+                            if (pair_cut<kCaus, kWin>(8 * i + k + lim, W) || dq[k] != kdoc)
                                 dmask |= 1u << (4 * i + k);
                     }
                 }
@@ -781,7 +783,7 @@ void born_bwd16_dkdv_d128_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         float bb = __int_as_float(max(__float_as_int(x), 0));
                         if constexpr (decltype(m)::value == kMasked) {
                             const int off = 8 * (r >> 2) + (r & 3);
-                            if ((kCaus && off + lim < 0) || (kWin && off + lim >= W)) u = bb = 0.f;
+                            if (pair_cut<kCaus, kWin>(off + lim, W)) u = bb = 0.f;
                         }
                         if constexpr (decltype(m)::value == kDocm)
                             if ((dmask >> r) & 1u) u = bb = 0.f;

@@ -440,11 +440,13 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                         // A masked pair weighs zero even where its overlap is
                         // zero (u = relu(-gamma tau) > 0 for tau < 0).
                         if constexpr (DOC) {
-                            if (dm[qb] && ((kCaus && off > lim) || (kWin && off < lim - W + 1) ||
-                                           kdp[nb * 32 + 4 * g + off] != rd))
-                                dr_ = 0.f;
+                            const bool cut = kWin ? pair_cut<kCaus, kWin>(lim - off, W) : (kCaus && off > lim);
+                            if (dm[qb] && (cut || kdp[nb * 32 + 4 * g + off] != rd)) dr_ = 0.f;
                         } else {
-                            if (mk[qb] && ((kCaus && off > lim) || (kWin && off < lim - W + 1))) dr_ = 0.f;
+                            // Causal with a window: one unsigned compare.
+                            const bool cut = (kCaus && kWin) ? pair_cut<kCaus, kWin>(lim - off, W)
+                                                             : ((kCaus && off > lim) || (kWin && off < lim - W + 1));
+                            if (mk[qb] && cut) dr_ = 0.f;
                         }
                         w[e] = dr_;
                     }
@@ -458,16 +460,21 @@ void born_bwd16_dq_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs>:
                 // Key kbase + 8 (r / 4) + r % 4 of register r is masked past
                 // the lane's row (causal) or in another document.
                 if (dm[qb]) {
+                    // Last visible key offset (causal); with a window the
+                    // two bounds as one unsigned compare (causal alone keeps
+                    // the plain test, which compiles shorter here).
                     const int lim = kCaus ? qrow[qb] - kbase : INT_MAX;
-                    const int wlo = kWin ? qrow[qb] - kbase - W + 1 : 0;  // window: first visible key
                     const int rd = r_doc[(BM / 2) * qb + (BM / 4) * (c >> 4) + 16 * wave + (c & 15)];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int4 d4 = *reinterpret_cast<const int4*>(kdp + nb * 32 + 4 * g + 8 * i);
                         const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != rd) s[qb][4 * i + k] = 0.f;
+                        for (int k = 0; k < 4; ++k) {
+                            const int off = 8 * i + k;
+                            const bool cut = kWin ? pair_cut<kCaus, kWin>(lim - off, W) : off > lim;
+                            if (cut || dk[k] != rd) s[qb][4 * i + k] = 0.f;
+                        }
                     }
                 }
             } else if (mk[qb]) {
@@ -962,11 +969,10 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                         const int off = 8 * (r >> 2) + (r & 3);
                         if constexpr (DOC) {
                             const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
-                            if (xm && ((kCaus && off + lim < 0) || (kWin && off + lim >= W) ||
-                                       qd[nb * 32 + 4 * g + off] != kdoc))
+                            if (xm && (pair_cut<kCaus, kWin>(off + lim, W) || qd[nb * 32 + 4 * g + off] != kdoc))
                                 u = bb = 0.f;
                         } else {
-                            if (mk && ((kCaus && off + lim < 0) || (kWin && off + lim >= W))) u = bb = 0.f;
+                            if (mk && pair_cut<kCaus, kWin>(off + lim, W)) u = bb = 0.f;
                         }
                         const float u2_ = u * u;
                         const float dpz = dp[r] * z4[k + e];
@@ -985,8 +991,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
             // Query qbase + 8 (r / 4) + r % 4 of register r is masked before
             // the lane's key (causal) or in another document.
             if (xm) {
-                const int lim = kCaus ? qbase - key : INT_MAX / 2;
-                const int wl = qbase - key;  // window: query - key >= W is masked
+                const int lim = qbase - key;  // query - key of register 0
                 const int32_t* qd = reinterpret_cast<const int32_t*>(sb + 2 * TB + 2 * BQ * 4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -994,8 +999,7 @@ void born_bwd16_dkdv_fast_kernel(typename std::conditional<PUR, PurArgs, BwdArgs
                     const int dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k + lim < 0 || (kWin && 8 * i + k + wl >= W) || dq[k] != kdoc)
-                            s[4 * i + k] = 0.f;
+                        if (pair_cut<kCaus, kWin>(8 * i + k + lim, W) || dq[k] != kdoc) s[4 * i + k] = 0.f;
                 }
             }
         } else if (mk) {

@@ -107,6 +107,18 @@ struct F16 {
 
 __device__ __forceinline__ float relu_f32(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 
+// Whether a (query, key) pair at offset d = query - key is masked by
+// causality (d < 0) and/or a sliding window (d >= W); causal with a window
+// as one unsigned compare, (unsigned)d >= W, which keeps fewer condition
+// registers live than the two signed tests.
+template <bool CAUS, bool WIN>
+__device__ __forceinline__ bool pair_cut(int d, int W) {
+    if constexpr (CAUS && WIN) return (uint32_t)d >= (uint32_t)W;
+    else if constexpr (CAUS) return d < 0;
+    else if constexpr (WIN) return d >= W;
+    else return false;
+}
+
 // One pair of Born weights of a tile, packed for the P.V product, added to
 // the row's running sum z.  x0, x1: the overlaps r' (fp32; the sign of the
 // scale folded into Q, masked elements already zero); c: the fp16 scale |s|.
