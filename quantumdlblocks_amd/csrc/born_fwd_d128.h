@@ -257,7 +257,8 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                         const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k)
-                            if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc)
+                            if (((kCaus && kWin) ? pair_cut<true, true>(lim - (8 * i + k), W) : (8 * i + k > lim || (kWin && 8 * i + k < wlo))) ||
+                                dk[k] != qdoc)
                                 dmask |= 1u << (4 * i + k);
                     }
                 }
@@ -275,7 +276,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                     float pw = fmaf(u2, u2, bq * bq);
                     if constexpr (decltype(m)::value == kMasked) {
                         const int r = 2 * j + e, off = 8 * (r >> 2) + (r & 3);
-                        if (off > lim || (kWin && off < wlo)) pw = 0.f;
+                        if ((kCaus && kWin) ? pair_cut<true, true>(lim - off, W) : (off > lim || (kWin && off < wlo))) pw = 0.f;
                     }
                     if constexpr (decltype(m)::value == kDocm)
                         if ((dmask >> (2 * j + e)) & 1u) pw = 0.f;
@@ -294,7 +295,7 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if ((kCaus && off > lim) || (kWin && off < wlo)) s[r] = 0.f;
+                if ((kCaus && kWin) ? pair_cut<true, true>(lim - off, W) : ((kCaus && off > lim) || (kWin && off < wlo))) s[r] = 0.f;
             }
         }
         if constexpr (decltype(m)::value == kDocm) {
@@ -309,7 +310,9 @@ void born_fwd16_d128_kernel(typename std::conditional<PUR, PurArgs, FwdArgs>::ty
                     const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (8 * i + k > lim || (kWin && 8 * i + k < wlo) || dk[k] != qdoc) s[4 * i + k] = 0.f;
+                        if (((kCaus && kWin) ? pair_cut<true, true>(lim - (8 * i + k), W) : (8 * i + k > lim || (kWin && 8 * i + k < wlo))) ||
+                            dk[k] != qdoc)
+                            s[4 * i + k] = 0.f;
                 }
             }
         }

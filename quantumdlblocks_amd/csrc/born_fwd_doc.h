@@ -349,14 +349,15 @@ void born_fwd16_doc_kernel(
     // the causal limit.
     auto apply_mask = [&](f32x16& s, int qb, int key0h, const int32_t* kd, bool single, bool vis)
         __attribute__((always_inline)) {
+        // Last visible key offset (causal; WIN: the window's first is W - 1
+        // before it, both tested as one unsigned compare).
         int lim = causal ? qrow[qb] - (key0h + 4 * g) : INT_MAX;
-        const int wlo = WIN ? lim - W + 1 : 0;  // window: first visible key
         if (single) {
             if (!vis) lim = -1;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 8 * (r >> 2) + (r & 3);
-                if (off > lim || (WIN && off < wlo)) s[r] = 0.f;
+                if (WIN ? pair_cut<true, true>(lim - off, W) : off > lim) s[r] = 0.f;
             }
         } else {
 #pragma unroll
@@ -365,7 +366,7 @@ void born_fwd16_doc_kernel(
                 const int dk[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    if (8 * i + k > lim || (WIN && 8 * i + k < wlo) || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
+                    if ((WIN ? pair_cut<true, true>(lim - (8 * i + k), W) : 8 * i + k > lim) || dk[k] != qdoc[qb]) s[4 * i + k] = 0.f;
             }
         }
     };
@@ -428,7 +429,6 @@ void born_fwd16_doc_kernel(
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
             int lim = (causal ? qrow[qb] : T - 1) - (key0h + 4 * g);
-            const int wlo = WIN ? lim - W + 1 : 0;  // window: first visible key
             if (single && !vv[qb]) lim = -1;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -445,7 +445,7 @@ void born_fwd16_doc_kernel(
                     float pw = fmaf(u2, u2, bq * bq);
                     bool masked = false;
                     if (mm[qb]) {
-                        masked = off > lim || (WIN && off < wlo);
+                        masked = WIN ? pair_cut<true, true>(lim - off, W) : off > lim;
                         if (!single) masked = masked || kd[4 * g + off] != qdoc[qb];
                     } else if (ll[qb]) {
                         masked = !vv[qb];
