@@ -331,7 +331,7 @@ def test_bwd_document_mask(cuda_device, dtype, is_causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 96, 128, 200, 256])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_bwd_unsorted_document_ids(cuda_device, dtype, D, is_causal):
     """Arbitrary (unsorted, repeating) document ids: the span of tiles a

@@ -353,11 +353,12 @@ def test_fwd_document_mask(cuda_device, dtype, is_causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 96, 128, 200, 256])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_fwd_unsorted_document_ids(cuda_device, dtype, D, is_causal):
     """Arbitrary (unsorted, repeating) document ids: the kernels' tile
-    screening by document-id range must stay conservative."""
+    screening by document-id range must stay conservative (D = 96 and 200:
+    the document modes with zero columns past D)."""
     rng = np.random.default_rng(D)
     doc = rng.integers(0, 4, size=(2, 700)).astype(np.int32)
     doc[1, 350:] = rng.integers(10, 12, size=350)

@@ -232,7 +232,7 @@ def test_purified_f16_documents_backward_fast(cuda_device, D, kw):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 96, 128, 200, 256])
 @pytest.mark.parametrize("is_causal", [True, False])
 def test_purified_unsorted_document_ids(cuda_device, dtype, D, is_causal):
     """Arbitrary (unsorted, repeating) document ids, tau < 0 (masked pairs
