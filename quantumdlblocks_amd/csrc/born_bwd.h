@@ -904,13 +904,16 @@ void born_bwd_dq32_kernel(BwdArgs p) {
 // B operands, in registers (KV_LDS = false) or, for wide heads, read from a
 // per-workgroup LDS copy (KV_LDS = true, one wave per workgroup).  Same
 // arithmetic as the 16-bit kernel; fp32 operands need no transposed copies.
+// CS column splits as in the 16-bit kernel: with CS == 2 two workgroups share
+// a key block, each accumulating dK, dV for half of the head dim's columns.
 // ---------------------------------------------------------------------------
-template <int DP, int NW, int BQ, int MODE, int WPE, bool KV_LDS>
+template <int DP, int NW, int BQ, int MODE, int WPE, bool KV_LDS, int CS = 1>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void born_bwd_dkdv32_kernel(BwdArgs p) {
     constexpr int BK = NW * 32;
     constexpr int KQ = DP / 8;
-    constexpr int DB = DP / 32;
+    constexpr int DBF = DP / 32;             // column blocks of the head dim
+    constexpr int DB = (DBF + CS - 1) / CS;  // column blocks accumulated here (at most)
     constexpr int NQ = BQ / 32;
     constexpr int NT = NW * 64;
     constexpr int RS = DP + 4;
@@ -933,7 +936,9 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
     const int window = (MODE == kGeneral) ? p.window : 0;
     const bool has_doc = kDoc && p.doc != nullptr;
 
-    const int bid = blockIdx.x;
+    const int cs = (CS > 1) ? (int)(blockIdx.x % CS) : 0;
+    const int bid = blockIdx.x / CS;
+    const int db0 = cs * DB;  // first column block accumulated here
     const int bh = bid % BH;
     const int kb = bid / BH;
     const int b = bh / p.H, h = bh % p.H;
@@ -1115,8 +1120,9 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
                     const int qrow = qs * 32 + acc_row(r, g);
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
-                        dv[db] = mfma_f32(d_lds[buf][qrow * RS + db * 32 + c], w[r], dv[db]);
-                        dk[db] = mfma_f32(q_lds[buf][qrow * RS + db * 32 + c], uu[r], dk[db]);
+                        if (DBF % CS != 0 && db0 + db >= DBF) break;  // the last split's short share
+                        dv[db] = mfma_f32(d_lds[buf][qrow * RS + (db0 + db) * 32 + c], w[r], dv[db]);
+                        dk[db] = mfma_f32(q_lds[buf][qrow * RS + (db0 + db) * 32 + c], uu[r], dk[db]);
                     }
                 }
             }
@@ -1143,7 +1149,7 @@ void born_bwd_dkdv32_kernel(BwdArgs p) {
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int d = db * 32 + 8 * j + 4 * g;
+                const int d = (db0 + db) * 32 + 8 * j + 4 * g;
                 if (d < D) {
                     f32x4 wk = {dk[db][4 * j] * fk, dk[db][4 * j + 1] * fk, dk[db][4 * j + 2] * fk,
                                 dk[db][4 * j + 3] * fk};
@@ -1180,6 +1186,12 @@ struct Bwd32Cfg {
     static constexpr bool KV_LDS = DP > 128;
     static constexpr int KV_NW = KV_LDS ? 1 : 4;
     static constexpr int KV_WPE = DP <= 64 ? 2 : 1;
+    // dK/dV column splits: dense launches at D = 192 and 256 (each split
+    // forms S and dP again, which outweighs the spills it removes elsewhere:
+    // B4 H2 T2048 backward D = 256 dense 6917 -> 5034 us, D = 192 dense
+    // 3901 -> 3695, but causal D = 256 3146 -> 3227 and D = 160 1489 -> 1913).
+    template <int MODE>
+    static constexpr int kv_cs() { return (MODE == kDense && (DP == 192 || DP == 256)) ? 2 : 1; }
     static constexpr int BQ = 32;
     static constexpr int NW = 4;
     static constexpr int BN = 32;
@@ -1346,8 +1358,9 @@ hipError_t launch_bwd32(const BwdArgs& a, hipStream_t st) {
     const unsigned BH = (unsigned)(a.B * a.H);
     {
         constexpr int BK = C::KV_NW * 32;
-        const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH);
-        hipLaunchKernelGGL((born_bwd_dkdv32_kernel<DP, C::KV_NW, C::BQ, MODE, C::KV_WPE, C::KV_LDS>), grid,
+        constexpr int CS = C::template kv_cs<MODE>();
+        const dim3 grid((unsigned)((a.T + BK - 1) / BK) * BH * CS);
+        hipLaunchKernelGGL((born_bwd_dkdv32_kernel<DP, C::KV_NW, C::BQ, MODE, C::KV_WPE, C::KV_LDS, CS>), grid,
                            dim3(C::KV_NW * 64), 0, st, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }

@@ -171,6 +171,19 @@ def test_bwd_wide_head_dims_column_split(cuda_device, D, dtype, mode):
     _check_bwd(2, 2, 300, D, dtype, cuda_device, scale=[0.2, -0.1], std=0.5, seed=D + 1, check_dscale=True, **kw)
 
 
+@pytest.mark.parametrize("D", [136, 192, 224, 256])
+@pytest.mark.parametrize("mode", ["causal", "dense", "window", "documents"])
+def test_bwd_wide_head_dims_fp32_column_split(cuda_device, D, mode):
+    """fp32 above D = 128 on the fp32-MFMA kernels, every mask mode (dense
+    launches at D = 256 run the dK/dV kernel in two workgroups per key block,
+    each accumulating half of the column blocks); several key blocks and
+    query tiles, per-head scales.  (dscale, from the fp32 row sums of D
+    products, is held to the fp32 bar at smaller head dims.)"""
+    kw = dict(is_causal=mode != "dense", window_size=90 if mode == "window" else 0,
+              doc=orc.geometric_doc_ids(2, 300, 60.0, seed=D) if mode == "documents" else None)
+    _check_bwd(2, 2, 300, D, torch.float32, cuda_device, scale=[0.2, -0.1], std=0.5, seed=D + 2, **kw)
+
+
 @pytest.mark.parametrize("D", [136, 200, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", [(True, 0, 1), (True, 0, 64), (True, 0, 129), (True, 0, 700), (False, 0, 300),
